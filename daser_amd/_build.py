@@ -1,0 +1,59 @@
+"""Builds libdaser_kv.so (gfx950) in-tree with hipcc.
+
+Run as ``python -m daser_amd._build`` or through ``__graft_entry__.build()``.
+The library is written next to this file so that it travels with the source
+tree; ``daser_amd._lib`` loads it from there.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+SRC = os.path.join(HERE, "csrc", "kv_move.hip")
+INCLUDE = os.path.join(ROOT, "include")
+OUT = os.path.join(HERE, "libdaser_kv.so")
+
+ARCH = "gfx950"
+
+# -packed-fp32-ops keeps v_pk_{add,mul,fma}_f32 out of the generated code.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-shared",
+    "-fPIC",
+    "-Wall",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found; the HIP library cannot be built")
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles the kernels and C ABI into ``daser_amd/libdaser_kv.so``."""
+    tmp = OUT + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", SRC, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

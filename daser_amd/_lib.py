@@ -1,0 +1,90 @@
+"""ctypes binding of libdaser_kv.so (declarations in include/daser_kv.h).
+
+torch is imported first on purpose: torch ships its own libamdhip64.so.7 and
+the dynamic loader then resolves the library's HIP dependency to that same
+runtime, so streams and device pointers handed over from torch are valid in
+the library.
+
+There is no fallback: if the library has not been built, ``lib()`` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede loading the HIP library)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so")
+
+DSR_ABI_VERSION = 1
+DSR_OK = 0
+DSR_ERR_ARG = -1
+DSR_ERR_ALIGN = -2
+DSR_ERR_SHAPE = -3
+
+DSR_DTYPE_BF16 = 0
+DSR_DTYPE_FP16 = 1
+DSR_DTYPE_FP8_E4M3 = 2
+
+DSR_ROPE_NEOX = 0
+DSR_ROPE_GPTJ = 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+
+# Argument lists, one per exported entry point, in header order.
+_COPY_ARGS = [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _P, _I64, _I64, _I, _P]
+SIGNATURES = {
+    "dsr_abi_version": ([], _I),
+    "dsr_error_string": ([_I], ctypes.c_char_p),
+    "dsr_gather": (_COPY_ARGS, _I),
+    "dsr_scatter": (_COPY_ARGS, _I),
+    "dsr_scatter_rerotate": (
+        _COPY_ARGS[:-1] + [_P, _P, _I, _I, _I, _I, _I, _P, _P],
+        _I,
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class DaserKVError(RuntimeError):
+    """A non-zero return code from libdaser_kv."""
+
+    def __init__(self, fn: str, code: int, text: str) -> None:
+        super().__init__(f"{fn} failed with code {code}: {text}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """Loads (once) and returns the HIP library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build it with "
+                    "`python -m daser_amd._build` (there is no CPU fallback)"
+                )
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, (args, res) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.argtypes = args
+                fn.restype = res
+            ver = handle.dsr_abi_version()
+            if ver != DSR_ABI_VERSION:
+                raise RuntimeError(f"libdaser_kv ABI {ver} != expected {DSR_ABI_VERSION}")
+            _lib = handle
+    return _lib
+
+
+def check(fn: str, code: int) -> None:
+    if code != DSR_OK:
+        text = lib().dsr_error_string(code).decode()
+        raise DaserKVError(fn, code, text)

@@ -1,0 +1,294 @@
+"""Host-side wrappers of the HIP gather / scatter / re-rotate kernels.
+
+The functions take torch tensors (device memory and streams only) and call
+the C ABI of libdaser_kv.so on torch's current stream. Index tables given as
+host data (lists, numpy arrays, CPU tensors) are validated on the host and
+uploaded; tables given as device tensors are used as they are (the kernels
+then skip out-of-range entries instead of faulting).
+
+Reference semantics restated here:
+  * LAYER_SIZE = kv.nbytes // kv.shape[1], SLOT_SIZE = LAYER_SIZE * L
+    (daser/connector/daser_connector.py:404-408);
+  * record of (slot i, layer l) at i * SLOT_SIZE + l * LAYER_SIZE, holding
+    bytes(kv_l[:, block_id]) = K page then V page (:625-632, :536-551).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from daser_amd import _lib
+
+_DTYPE_CODES = {
+    torch.bfloat16: _lib.DSR_DTYPE_BF16,
+    torch.float16: _lib.DSR_DTYPE_FP16,
+    torch.float8_e4m3fn: _lib.DSR_DTYPE_FP8_E4M3,
+}
+
+ROPE_STYLES = {"neox": _lib.DSR_ROPE_NEOX, "gptj": _lib.DSR_ROPE_GPTJ}
+
+
+@dataclass(frozen=True)
+class PagedKVLayout:
+    """Geometry of vLLM's per-layer paged caches ``kv_l[2, NB, bs, H, D]``.
+
+    Built from the registered caches (reference ``register_kv_caches``,
+    daser/connector/daser_connector.py:383-413): layer order is the dict's
+    insertion order, every layer must share shape, dtype and strides, and a
+    page (``kv_l[0, b]``) must be contiguous.
+    """
+
+    num_layers: int
+    num_blocks: int
+    block_size: int
+    num_heads: int
+    head_dim: int
+    dtype: torch.dtype
+    elem_bytes: int
+    page_bytes: int  # one K (or V) page
+    kv_stride: int  # bytes K page -> V page
+    page_stride: int  # bytes block b -> b + 1
+    layer_bytes: int  # LAYER_SIZE of the slot record
+    device: torch.device
+
+    @property
+    def slot_bytes(self) -> int:
+        """SLOT_SIZE: one block's record over all layers."""
+        return self.layer_bytes * self.num_layers
+
+    @staticmethod
+    def from_caches(kv_caches: Sequence[torch.Tensor]) -> "PagedKVLayout":
+        if not kv_caches:
+            raise ValueError("no KV caches registered")
+        t0 = kv_caches[0]
+        if t0.dim() != 5 or t0.shape[0] != 2:
+            raise ValueError(
+                f"expected per-layer KV cache of shape (2, num_blocks, block_size, "
+                f"num_heads, head_dim), got {tuple(t0.shape)}"
+            )
+        for t in kv_caches:
+            if t.shape != t0.shape or t.dtype != t0.dtype or t.stride() != t0.stride():
+                raise ValueError("all layer caches must share shape, dtype and strides")
+            if t.device != t0.device:
+                raise ValueError("all layer caches must live on one device")
+        _, nb, bs, h, d = t0.shape
+        s = t0.stride()
+        if s[4] != 1 or s[3] != d or s[2] != h * d:
+            raise ValueError("a KV page (block_size, num_heads, head_dim) must be contiguous")
+        e = t0.element_size()
+        page_bytes = bs * h * d * e
+        # LAYER_SIZE as the reference derives it (kv.nbytes // num_blocks).
+        layer_bytes = t0.numel() * e // nb if nb else 2 * page_bytes
+        return PagedKVLayout(
+            num_layers=len(kv_caches),
+            num_blocks=nb,
+            block_size=bs,
+            num_heads=h,
+            head_dim=d,
+            dtype=t0.dtype,
+            elem_bytes=e,
+            page_bytes=page_bytes,
+            kv_stride=s[0] * e,
+            page_stride=s[1] * e,
+            layer_bytes=layer_bytes,
+            device=t0.device,
+        )
+
+
+class LayerTable:
+    """Device array of per-layer cache base addresses (uint64)."""
+
+    def __init__(self, kv_caches: Sequence[torch.Tensor]) -> None:
+        self.layout = PagedKVLayout.from_caches(kv_caches)
+        self._caches = list(kv_caches)  # keep the borrowed tensors alive
+        ptrs = np.array([t.data_ptr() for t in kv_caches], dtype=np.uint64)
+        self.table = torch.from_numpy(ptrs.view(np.int64)).to(self.layout.device)
+
+    def ptr(self, first: int = 0) -> int:
+        return self.table.data_ptr() + 8 * first
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _as_device_table(
+    x, dtype: torch.dtype, device: torch.device, name: str
+) -> torch.Tensor:
+    if isinstance(x, torch.Tensor) and x.device.type != "cpu":
+        if x.dtype != dtype or not x.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {dtype} tensor")
+        return x
+    arr = torch.as_tensor(np.asarray(x), dtype=dtype)
+    return arr.to(device, non_blocking=False)
+
+
+def _host_array(x, np_dtype) -> Optional[np.ndarray]:
+    if isinstance(x, torch.Tensor):
+        if x.device.type != "cpu":
+            return None
+        return x.numpy().astype(np_dtype, copy=False)
+    return np.asarray(x, dtype=np_dtype)
+
+
+def _validate(layout: PagedKVLayout, page_ids, slot_offsets, staging, layer0, n_layers):
+    ids = _host_array(page_ids, np.int64)
+    offs = _host_array(slot_offsets, np.int64)
+    if ids is not None and offs is not None and ids.shape != offs.shape:
+        raise ValueError("page_ids and slot_offsets differ in length")
+    if ids is not None and ids.size and (ids.min() < 0 or ids.max() >= layout.num_blocks):
+        raise IndexError(f"block id out of range [0, {layout.num_blocks})")
+    if offs is not None and offs.size:
+        end = offs.max() + (layer0 + n_layers - 1) * layout.layer_bytes + 2 * layout.page_bytes
+        if offs.min() < 0 or end > staging.numel() * staging.element_size():
+            raise IndexError("slot record outside the staging buffer")
+        if np.any(offs % 16):
+            raise ValueError("slot offsets must be multiples of 16 bytes")
+
+
+def _copy_args(table: LayerTable, page_ids, slot_offsets, staging, layer0, layers):
+    lay = table.layout
+    first, count = (0, lay.num_layers) if layers is None else layers
+    if first < 0 or count < 0 or first + count > lay.num_layers:
+        raise IndexError("layer range outside the registered caches")
+    if staging.device != lay.device:
+        raise ValueError("staging must live on the KV caches' device")
+    if not staging.is_contiguous():
+        raise ValueError("staging must be contiguous")
+    _validate(lay, page_ids, slot_offsets, staging, layer0 + first, count)
+    ids = _as_device_table(page_ids, torch.int32, lay.device, "page_ids")
+    offs = _as_device_table(slot_offsets, torch.int64, lay.device, "slot_offsets")
+    if ids.numel() != offs.numel():
+        raise ValueError("page_ids and slot_offsets differ in length")
+    args = (
+        table.ptr(first),
+        count,
+        lay.kv_stride,
+        lay.page_stride,
+        lay.page_bytes,
+        lay.num_blocks,
+        ids.data_ptr(),
+        offs.data_ptr(),
+        ids.numel(),
+        staging.data_ptr(),
+        staging.numel() * staging.element_size(),
+        lay.layer_bytes,
+        layer0 + first,
+    )
+    return args, (ids, offs)
+
+
+def gather(
+    table: LayerTable,
+    page_ids,
+    slot_offsets,
+    staging: torch.Tensor,
+    *,
+    layer0: int = 0,
+    layers: Optional[tuple[int, int]] = None,
+) -> None:
+    """Packs pages into slot records (reference save loop, :610-632).
+
+    ``layers=(first, count)`` restricts the launch to a layer range; the
+    record index of table layer ``first + i`` is ``layer0 + first + i``.
+    """
+    args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
+    rc = _lib.lib().dsr_gather(*args, _stream_handle(table.layout.device))
+    _lib.check("dsr_gather", rc)
+
+
+def scatter(
+    table: LayerTable,
+    page_ids,
+    slot_offsets,
+    staging: torch.Tensor,
+    *,
+    layer0: int = 0,
+    layers: Optional[tuple[int, int]] = None,
+) -> None:
+    """Unpacks slot records into pages (reference load loop, :536-551)."""
+    args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
+    rc = _lib.lib().dsr_scatter(*args, _stream_handle(table.layout.device))
+    _lib.check("dsr_scatter", rc)
+
+
+def scatter_rerotate(
+    table: LayerTable,
+    page_ids,
+    slot_offsets,
+    staging: torch.Tensor,
+    cos_sin: torch.Tensor,
+    rope_idx,
+    *,
+    rot_dim: Optional[int] = None,
+    style: str = "neox",
+    k_scale: Optional[torch.Tensor] = None,
+    layer0: int = 0,
+    layers: Optional[tuple[int, int]] = None,
+) -> None:
+    """Scatter with K re-rotated by ``cos_sin[rope_idx[p]]`` (-1 = copy).
+
+    ``cos_sin`` is a float32 tensor ``[n_tables, rot_dim/2, 2]`` from
+    :func:`daser_amd.position.delta_tables`; ``k_scale`` holds per-layer
+    fp32 scales (fp8 caches only).
+    """
+    lay = table.layout
+    if lay.dtype not in _DTYPE_CODES:
+        raise TypeError(f"re-rotation does not support KV dtype {lay.dtype}")
+    rot_dim = lay.head_dim if rot_dim is None else rot_dim
+    if cos_sin.dtype != torch.float32 or cos_sin.dim() != 3 or cos_sin.shape[1:] != (
+        rot_dim // 2,
+        2,
+    ):
+        raise ValueError(f"cos_sin must be float32 [n, {rot_dim // 2}, 2]")
+    if cos_sin.device != lay.device or not cos_sin.is_contiguous():
+        raise ValueError("cos_sin must be a contiguous device tensor")
+    ridx = _host_array(rope_idx, np.int64)
+    if ridx is not None and ridx.size and (ridx.max() >= cos_sin.shape[0] or ridx.min() < -1):
+        raise IndexError("rope_idx outside [-1, n_tables)")
+    args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
+    ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")
+    if ridx_d.numel() != keep[0].numel():
+        raise ValueError("rope_idx and page_ids differ in length")
+    ks_ptr = None
+    if lay.dtype == torch.float8_e4m3fn:
+        if k_scale is None:
+            raise ValueError("fp8 re-rotation needs per-layer k_scale")
+        if (
+            k_scale.dtype != torch.float32
+            or k_scale.device != lay.device
+            or k_scale.numel() < layer0 + lay.num_layers
+        ):
+            raise ValueError("k_scale must be a float32 device tensor with one scale per layer")
+        ks_ptr = k_scale.data_ptr()
+    rc = _lib.lib().dsr_scatter_rerotate(
+        *args,
+        cos_sin.data_ptr(),
+        ridx_d.data_ptr(),
+        cos_sin.shape[0],
+        lay.head_dim,
+        rot_dim,
+        ROPE_STYLES[style],
+        _DTYPE_CODES[lay.dtype],
+        ks_ptr,
+        _stream_handle(lay.device),
+    )
+    _lib.check("dsr_scatter_rerotate", rc)
+
+
+def slot_offsets_for(num_pages: Sequence[int], slot_bytes: int, base: int = 0) -> np.ndarray:
+    """Record offsets for requests packed back to back in one staging buffer:
+    request r's slot i lives at ``base + (pages before r + i) * slot_bytes``."""
+    total = int(sum(num_pages))
+    return base + np.arange(total, dtype=np.int64) * slot_bytes
+
+
+def pages_for_tokens(token_count: int, block_size: int) -> int:
+    """ceil(tokens / block_size): pages holding token_count tokens
+    (daser/connector/daser_connector.py:280, :292)."""
+    return math.ceil(token_count / block_size)

@@ -1,0 +1,120 @@
+"""Position encoders and RoPE delta tables for reused-chunk re-rotation.
+
+``PositionEncoder`` / ``FixedOffsetEncoder`` keep the reference interface
+(daser/position/base.py:10-48, daser/position/fixed_offset.py:11-50): an
+integer offset is assigned when a chunk is allocated and returned when it is
+loaded. The reference stops there; this module adds what the load path needs
+to make a chunk stored at position ``stored`` valid at position ``new``: the
+per-chunk angle table of ``R(new) . R(stored)^-1 = R(new - stored)``.
+
+The tables are computed on the host in float64 (angles reach
+``32768 * 1 rad`` for theta = 5e5 at head_dim 128, where float32 argument
+reduction would lose ~1e-3 rad) and rounded once to float32 for the kernel.
+"""
+
+from __future__ import annotations
+
+from abc import ABC, abstractmethod
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+
+class PositionEncoder(ABC):
+    """Pluggable position strategy (reference daser/position/base.py:10-48)."""
+
+    @abstractmethod
+    def assign_offset(self, chunk_key: str, token_count: int) -> int:
+        """Position of the chunk's first token when it is stored."""
+
+    @abstractmethod
+    def get_offset(self, meta) -> int:
+        """Stored position to undo when the chunk is loaded (``meta.pos_offset``)."""
+
+
+class FixedOffsetEncoder(PositionEncoder):
+    """Every chunk is stored at one fixed position (default 0).
+
+    Reference daser/position/fixed_offset.py:11-50; its docstring names the
+    case this build implements: RoPE re-applied at load time.
+    """
+
+    def __init__(self, fixed_offset: int = 0) -> None:
+        self._offset = int(fixed_offset)
+
+    def assign_offset(self, chunk_key: str, token_count: int) -> int:
+        return self._offset
+
+    def get_offset(self, meta) -> int:
+        return int(meta.pos_offset)
+
+
+def rope_inv_freq(rot_dim: int, theta: float) -> np.ndarray:
+    """inv_freq_j = theta^(-2j/rot_dim), j < rot_dim/2, in float64
+    (RoFormer, Su et al. 2021; the Llama / GPT-NeoX convention)."""
+    if rot_dim <= 0 or rot_dim % 2:
+        raise ValueError("rot_dim must be a positive even number")
+    j = np.arange(rot_dim // 2, dtype=np.float64)
+    return np.power(float(theta), -2.0 * j / rot_dim)
+
+
+def llama3_inv_freq(
+    rot_dim: int,
+    theta: float,
+    factor: float,
+    low_freq_factor: float,
+    high_freq_factor: float,
+    original_max_position: int,
+) -> np.ndarray:
+    """Frequency-dependent scaling of Llama 3.1 ("rope_type": "llama3")."""
+    inv = rope_inv_freq(rot_dim, theta)
+    low_wl = original_max_position / low_freq_factor
+    high_wl = original_max_position / high_freq_factor
+    wl = 2.0 * np.pi / inv
+    smooth = (original_max_position / wl - low_freq_factor) / (high_freq_factor - low_freq_factor)
+    scaled = np.where(wl > low_wl, inv / factor, inv)
+    mid = (wl <= low_wl) & (wl >= high_wl)
+    return np.where(mid, (1 - smooth) * inv / factor + smooth * inv, scaled)
+
+
+def delta_tables(
+    deltas: Sequence[int],
+    rot_dim: int,
+    theta: float = 10000.0,
+    inv_freq: Optional[np.ndarray] = None,
+    device: Optional[torch.device] = None,
+) -> torch.Tensor:
+    """float32 ``[len(deltas), rot_dim/2, 2]`` of (cos, sin)(delta * inv_freq).
+
+    Row r rotates a chunk whose tokens move by ``deltas[r]`` positions.
+    """
+    inv = rope_inv_freq(rot_dim, theta) if inv_freq is None else np.asarray(inv_freq, np.float64)
+    if inv.shape != (rot_dim // 2,):
+        raise ValueError("inv_freq must have rot_dim/2 entries")
+    d = np.asarray(deltas, dtype=np.float64).reshape(-1, 1)
+    ang = d * inv.reshape(1, -1)
+    tab = np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+    t = torch.from_numpy(np.ascontiguousarray(tab))
+    return t.to(device) if device is not None else t
+
+
+def page_rope_index(
+    num_pages_per_chunk: Sequence[int], deltas: Sequence[int]
+) -> tuple[np.ndarray, list[int]]:
+    """Per-page table index for chunks laid out back to back.
+
+    Chunks with delta 0 map to -1 (bit-exact copy, no table). Returns the
+    int32 per-page index and the list of distinct non-zero deltas, whose
+    order is the table order.
+    """
+    uniq: dict[int, int] = {}
+    out = []
+    for n, dl in zip(num_pages_per_chunk, deltas):
+        dl = int(dl)
+        if dl == 0:
+            idx = -1
+        else:
+            idx = uniq.setdefault(dl, len(uniq))
+        out.extend([idx] * int(n))
+    return np.asarray(out, dtype=np.int32), list(uniq.keys())

@@ -1,0 +1,155 @@
+/*
+ * daser_kv.h -- C ABI of the MI355X (gfx950) KV data-movement library
+ * (libdaser_kv.so).
+ *
+ * The library moves vLLM paged-KV pages between the per-layer block cache and
+ * contiguous DaseR slot records, and optionally re-rotates the K half of
+ * reused chunks to a new RoPE position while scattering them back.
+ *
+ * Byte layouts (all offsets in bytes):
+ *   per-layer block cache  kv_l[2][num_blocks][block_size][H][D]  (index 0 = K)
+ *       K page of block b  = layer_base[l] + b * page_stride
+ *       V page of block b  = layer_base[l] + b * page_stride + kv_stride
+ *       page_bytes         = block_size * H * D * elem_bytes (contiguous)
+ *   slot record            = [layer 0: K page | V page][layer 1: ...]...
+ *       record of (page p, layer l) starts at
+ *           staging + slot_offsets[p] + l * layer_bytes
+ *       K page first, V page at + page_bytes; layer_bytes >= 2 * page_bytes.
+ *   This is the on-disk `daser.store` slot format of the reference
+ *   (daser/connector/daser_connector.py:531-535, :625-632; SLOT = LAYER * L,
+ *   LAYER = kv.nbytes // num_blocks, :404-408).
+ *
+ * Conventions for every entry point:
+ *   - pointer arguments marked [device] are device addresses; the tables they
+ *     point to must be resident before the stream reaches the launch;
+ *   - every base pointer, stride, page_bytes, layer_bytes and slot offset
+ *     must be a multiple of 16 bytes (one 16-byte lane vector); violations
+ *     return DSR_ERR_ALIGN without launching;
+ *   - launches are stream-ordered on `stream` (0 = the null stream), never
+ *     synchronise, never allocate, and are reentrant across streams;
+ *   - pages whose block id lies outside [0, num_blocks), or whose record
+ *     would end beyond staging_bytes, are skipped by the kernel (the host
+ *     wrappers reject them before launching);
+ *   - return value: 0 on success, a DSR_ERR_* code (< 0) for argument errors,
+ *     or a positive hipError_t from the launch.
+ */
+#ifndef DASER_KV_H
+#define DASER_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
+
+#define DSR_ABI_VERSION 1
+
+#define DSR_OK 0
+#define DSR_ERR_ARG (-1)   /* null pointer, negative count, bad enum     */
+#define DSR_ERR_ALIGN (-2) /* a pointer/stride/size is not 16-byte aligned */
+#define DSR_ERR_SHAPE (-3) /* rot_dim/head_dim/page geometry inconsistent */
+
+/* Element types understood by the re-rotation kernel. Plain gather/scatter
+ * is dtype-agnostic (raw bytes, bit-exact for every dtype incl. fp8). */
+#define DSR_DTYPE_BF16 0
+#define DSR_DTYPE_FP16 1
+#define DSR_DTYPE_FP8_E4M3 2 /* OCP e4m3fn: bias 7, max 448, NaN 0x7F/0xFF */
+
+/* RoPE pairings. */
+#define DSR_ROPE_NEOX 0 /* rotate-half: pairs (j, j + rot_dim/2)  (Llama) */
+#define DSR_ROPE_GPTJ 1 /* interleaved: pairs (2j, 2j + 1)                */
+
+/* Returns DSR_ABI_VERSION. */
+int dsr_abi_version(void);
+
+/* Human-readable text for a return code of this library. */
+const char* dsr_error_string(int code);
+
+/*
+ * Offload gather: for every page p in [0, n_pages) and layer l in
+ * [0, n_layers), copy the K and V pages of block page_ids[p] of layer l into
+ * the slot record at staging + slot_offsets[p] + (layer0 + l) * layer_bytes.
+ *
+ * Replaces the per-(request, block) loop of DaserConnector.save_kv_layer,
+ * reference daser/connector/daser_connector.py:610-632 (one launch covers
+ * every store request of a step, and with n_layers > 1 every layer).
+ *
+ *   layer_base    [device] n_layers byte addresses of the per-layer caches
+ *   kv_stride     bytes from a block's K page to its V page (kv.stride(0))
+ *   page_stride   bytes between consecutive blocks (kv.stride(1))
+ *   page_bytes    bytes of one K (or V) page
+ *   num_blocks    blocks per layer cache (kv.shape[1])
+ *   page_ids      [device] n_pages int32 block ids
+ *   slot_offsets  [device] n_pages int64 offsets of each page's slot record
+ *   staging       [device] destination records, staging_bytes long
+ *   layer_bytes   record stride between layers (LAYER_SIZE)
+ *   layer0        layer index of layer_base[0] inside the record
+ */
+int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+               int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+               const int32_t* page_ids, const int64_t* slot_offsets,
+               int n_pages, void* staging, int64_t staging_bytes,
+               int64_t layer_bytes, int layer0, dsr_stream_t stream);
+
+/*
+ * Load scatter: the inverse of dsr_gather. Copies each slot record back into
+ * the K and V pages of block page_ids[p] of every layer.
+ *
+ * Replaces the per-(request, slot, layer) copy loop of
+ * DaserConnector.start_load_kv, reference
+ * daser/connector/daser_connector.py:536-551.
+ */
+int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                const int32_t* page_ids, const int64_t* slot_offsets,
+                int n_pages, const void* staging, int64_t staging_bytes,
+                int64_t layer_bytes, int layer0, dsr_stream_t stream);
+
+/*
+ * Load scatter with fused RoPE position-delta re-rotation of K.
+ *
+ * Same copy as dsr_scatter. In addition, for a page p with
+ * rope_idx[p] >= 0, every K row (one token of one head, head_dim elements)
+ * is rotated by the angle table cos_sin[rope_idx[p]][0 .. rot_dim/2):
+ *   neox: (x_j, x_{j+R/2}) -> (x_j c_j - x_{j+R/2} s_j, x_{j+R/2} c_j + x_j s_j)
+ *   gptj: (x_{2j}, x_{2j+1}) rotated the same way with (c_j, s_j)
+ * with (c_j, s_j) = (cos, sin)(delta * inv_freq_j) and delta = new position
+ * - stored position of the page's chunk, i.e. R(new) . R(stored)^-1 applied
+ * in one step, fp32 arithmetic, one round to the storage type.
+ * Elements j >= rot_dim and all V bytes are copied unchanged; pages with
+ * rope_idx[p] < 0 are copied bit-exactly.
+ *
+ * fp8 (DSR_DTYPE_FP8_E4M3): x = e4m3(q) * k_scale[layer0 + l], rotate,
+ * q' = e4m3_rne(clamp(y / k_scale, -448, 448)); NaN stays NaN (0x7F).
+ * bf16/fp16: round-to-nearest-even from fp32; NaN -> canonical quiet NaN.
+ *
+ * The reference has no re-rotation (daser/position/fixed_offset.py:11-50
+ * only carries an integer offset, which this path consumes); the copy it
+ * fuses into replaces daser/connector/daser_connector.py:536-551.
+ *
+ *   cos_sin   [device] n_tables * (rot_dim/2) float pairs (cos, sin)
+ *   rope_idx  [device] n_pages int32 table index per page, -1 = no rotation
+ *   n_tables  number of tables (bounds rope_idx)
+ *   head_dim, rot_dim   rot_dim even, <= head_dim, page_bytes a multiple of
+ *                       one row; see DSR_ERR_SHAPE for vector constraints
+ *   k_scale   [device] per-layer fp32 scales, indexed layer0 + l; required
+ *             for fp8, ignored otherwise (may be null)
+ */
+int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
+                         int64_t kv_stride, int64_t page_stride,
+                         int64_t page_bytes, int64_t num_blocks,
+                         const int32_t* page_ids, const int64_t* slot_offsets,
+                         int n_pages, const void* staging,
+                         int64_t staging_bytes, int64_t layer_bytes,
+                         int layer0, const float* cos_sin,
+                         const int32_t* rope_idx, int n_tables, int head_dim,
+                         int rot_dim, int rope_style, int dtype,
+                         const float* k_scale, dsr_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DASER_KV_H */

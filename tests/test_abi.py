@@ -1,0 +1,89 @@
+"""The C-ABI library loads, exports every symbol include/daser_kv.h
+declares, and rejects bad arguments before touching the device."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+from daser_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "daser_kv.h")
+
+
+def declared_symbols() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsr_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert {"dsr_gather", "dsr_scatter", "dsr_scatter_rerotate",
+            "dsr_abi_version", "dsr_error_string"} <= set(syms)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for s in declared_symbols():
+        assert hasattr(lib, s), s
+    assert set(_lib.SIGNATURES) == set(declared_symbols())
+
+
+def test_abi_version_and_error_strings():
+    lib = _lib.lib()
+    assert lib.dsr_abi_version() == _lib.DSR_ABI_VERSION
+    for code in (_lib.DSR_ERR_ARG, _lib.DSR_ERR_ALIGN, _lib.DSR_ERR_SHAPE):
+        assert len(lib.dsr_error_string(code)) > 10
+    assert lib.dsr_error_string(0) == b"success"
+
+
+def _gather(**kw):
+    args = dict(layer_base=16, n_layers=2, kv_stride=4096, page_stride=4096,
+                page_bytes=4096, num_blocks=8, page_ids=32, slot_offsets=48,
+                n_pages=1, staging=64, staging_bytes=1 << 20, layer_bytes=8192,
+                layer0=0, stream=None)
+    args.update(kw)
+    return _lib.lib().dsr_gather(*args.values())
+
+
+def test_argument_errors_return_before_launch():
+    # These never reach the device: validation fails first.
+    assert _gather(kv_stride=4100) == _lib.DSR_ERR_ALIGN
+    assert _gather(staging=72) == _lib.DSR_ERR_ALIGN
+    assert _gather(n_pages=-1) == _lib.DSR_ERR_ARG
+    assert _gather(page_ids=None) == _lib.DSR_ERR_ARG
+    assert _gather(layer_bytes=4096) == _lib.DSR_ERR_SHAPE
+    # empty work is a successful no-op with no launch
+    assert _gather(n_pages=0) == _lib.DSR_OK
+    assert _gather(n_layers=0) == _lib.DSR_OK
+
+
+def test_rerotate_argument_errors():
+    lib = _lib.lib()
+    base = [16, 1, 4096, 4096, 4096, 8, 32, 48, 1, 64, 1 << 20, 8192, 0]
+
+    def call(head_dim=128, rot_dim=128, style=0, dtype=0, k_scale=80, n_tables=1):
+        return lib.dsr_scatter_rerotate(*base, 96, 112, n_tables, head_dim, rot_dim,
+                                        style, dtype, k_scale, None)
+
+    assert call(style=7) == _lib.DSR_ERR_ARG
+    assert call(dtype=9) == _lib.DSR_ERR_ARG
+    assert call(rot_dim=130) == _lib.DSR_ERR_SHAPE
+    assert call(rot_dim=127) == _lib.DSR_ERR_SHAPE
+    assert call(head_dim=100, rot_dim=100) == _lib.DSR_ERR_SHAPE  # page not whole rows
+    assert call(dtype=2, rot_dim=48, head_dim=64) == _lib.DSR_ERR_SHAPE
+    assert call(dtype=2, k_scale=None) == _lib.DSR_ERR_ARG
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
+    try:
+        _lib.lib()
+    except RuntimeError as e:
+        assert "no CPU fallback" in str(e)
+    else:
+        raise AssertionError("expected a RuntimeError")

@@ -1,0 +1,262 @@
+"""Parity of the HIP kernels against the C oracle (bit-exact copies, <= 1 ulp
+re-rotation), called through the C ABI via daser_amd.ops."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from daser_amd import ops, position, workloads
+from daser_amd._lib import DaserKVError
+from daser_amd.workloads import KVShape
+from oracle import oracle
+from tests.helpers import ORC_DT, rand_caches, rotation_within_tolerance, to_bits_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _np_layers(caches, dt):
+    return [to_bits_np(c, dt) for c in caches]
+
+
+def _gather_both(wl, caches, dt, gpu):
+    table = ops.LayerTable(caches)
+    staging = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(table, wl.page_ids, wl.slot_offsets, staging)
+    ref = np.zeros(wl.staging_bytes, dtype=np.uint8)
+    oracle.gather(_np_layers(caches, dt), wl.page_ids, wl.slot_offsets, ref,
+                  wl.shape.layer_bytes)
+    return staging, ref
+
+
+def test_gather_cfg1_bit_exact(gpu):
+    print("case: gather cfg1", flush=True)
+    wl = workloads.config(1)
+    caches = rand_caches(wl.shape, wl.num_blocks, "bf16", gpu, seed=1)
+    staging, ref = _gather_both(wl, caches, "bf16", gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(staging.cpu().numpy(), ref)
+
+
+def test_scatter_cfg1_bit_exact_and_round_trip(gpu):
+    print("case: scatter cfg1", flush=True)
+    wl = workloads.config(1)
+    caches = rand_caches(wl.shape, wl.num_blocks, "bf16", gpu, seed=2)
+    staging, ref = _gather_both(wl, caches, "bf16", gpu)
+    dst = [torch.zeros_like(c) for c in caches]
+    ops.scatter(ops.LayerTable(dst), wl.page_ids, wl.slot_offsets, staging)
+    dst_ref = [np.zeros_like(a) for a in _np_layers(caches, "bf16")]
+    oracle.scatter(dst_ref, wl.page_ids, wl.slot_offsets, ref, wl.shape.layer_bytes)
+    torch.cuda.synchronize()
+    touched = torch.zeros(wl.num_blocks, dtype=torch.bool)
+    touched[torch.from_numpy(wl.page_ids.astype(np.int64))] = True
+    for l in range(wl.shape.num_layers):
+        got = to_bits_np(dst[l], "bf16")
+        assert np.array_equal(got, dst_ref[l])
+        # scatter . gather = identity on touched pages, untouched stay zero
+        assert torch.equal(dst[l][:, touched.to(gpu)], caches[l][:, touched.to(gpu)])
+        assert not dst[l][:, (~touched).to(gpu)].view(torch.int16).any()
+
+
+@pytest.mark.parametrize("dt", ["e4m3", "fp16"])
+def test_gather_scatter_other_dtypes_bit_exact(gpu, dt):
+    print(f"case: gather/scatter {dt}", flush=True)
+    shape = KVShape(4, 8, 128, 16, 1 if dt == "e4m3" else 2)
+    wl = workloads.ragged(shape, 5, 1, 300, seed=3, pool_slack=1.5)
+    caches = rand_caches(shape, wl.num_blocks, dt, gpu, seed=4, scale=3.0)
+    staging, ref = _gather_both(wl, caches, dt, gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(staging.cpu().numpy(), ref)
+    dst = [torch.zeros_like(c) for c in caches]
+    ops.scatter(ops.LayerTable(dst), wl.page_ids, wl.slot_offsets, staging)
+    torch.cuda.synchronize()
+    ids = torch.from_numpy(wl.page_ids.astype(np.int64)).to(gpu)
+    for l in range(shape.num_layers):
+        assert torch.equal(dst[l].view(torch.uint8)[:, ids], caches[l].view(torch.uint8)[:, ids])
+
+
+def test_per_layer_launches_match_all_layer_launch(gpu):
+    """save_kv_layer issues one launch per layer (layer0 = layer index)."""
+    print("case: per-layer gather", flush=True)
+    wl = workloads.config(1)
+    caches = rand_caches(wl.shape, wl.num_blocks, "bf16", gpu, seed=5)
+    table = ops.LayerTable(caches)
+    full = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(table, wl.page_ids, wl.slot_offsets, full)
+    per = torch.zeros_like(full)
+    for l in range(wl.shape.num_layers):
+        ops.gather(table, wl.page_ids, wl.slot_offsets, per, layers=(l, 1))
+    torch.cuda.synchronize()
+    assert torch.equal(full, per)
+
+
+def test_strided_layout_block_major(gpu):
+    """A cache allocated block-major (NB, 2, bs, H, D) and viewed as
+    (2, NB, ...) has kv_stride = page, page_stride = 2 pages."""
+    print("case: block-major layout", flush=True)
+    shape = KVShape(3, 2, 64, 16, 2)
+    nb = 40
+    g = torch.Generator().manual_seed(6)
+    caches = [torch.randn((nb, 2, 16, 2, 64), generator=g).to(torch.bfloat16).to(gpu)
+              .permute(1, 0, 2, 3, 4) for _ in range(3)]
+    wl = workloads.ragged(shape, 3, 1, 100, seed=7, num_blocks=nb)
+    staging, ref = _gather_both(wl, [c.contiguous() for c in caches], "bf16", gpu)
+    table = ops.LayerTable(caches)
+    assert table.layout.kv_stride == table.layout.page_bytes
+    st2 = torch.zeros_like(staging)
+    ops.gather(table, wl.page_ids, wl.slot_offsets, st2)
+    torch.cuda.synchronize()
+    assert np.array_equal(st2.cpu().numpy(), ref)
+
+
+def test_empty_and_single_page(gpu):
+    print("case: empty/single", flush=True)
+    shape = KVShape(2, 1, 64, 16, 2)
+    caches = rand_caches(shape, 8, "bf16", gpu, seed=8)
+    table = ops.LayerTable(caches)
+    staging = torch.zeros(shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(table, np.zeros(0, np.int32), np.zeros(0, np.int64), staging)
+    assert not staging.any()
+    ops.gather(table, [7], [0], staging)  # last block of the pool
+    torch.cuda.synchronize()
+    exp = torch.cat([c[:, 7].reshape(-1).view(torch.uint8) for c in caches])
+    assert torch.equal(staging, exp)
+
+
+def test_out_of_range_rejected(gpu):
+    shape = KVShape(2, 1, 64, 16, 2)
+    caches = rand_caches(shape, 8, "bf16", gpu, seed=9)
+    table = ops.LayerTable(caches)
+    staging = torch.zeros(shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    with pytest.raises(IndexError):
+        ops.gather(table, [8], [0], staging)
+    with pytest.raises(IndexError):
+        ops.gather(table, [0], [16], staging)
+    with pytest.raises(ValueError):
+        ops.gather(table, [0], [8], torch.zeros(2 * shape.slot_bytes, dtype=torch.uint8, device=gpu))
+
+
+def test_device_tables_out_of_range_skipped(gpu):
+    """Device-side tables are not validated on the host; the kernel skips
+    entries outside the pool or the staging buffer instead of faulting."""
+    print("case: device tables skip", flush=True)
+    shape = KVShape(2, 1, 64, 16, 2)
+    caches = rand_caches(shape, 8, "bf16", gpu, seed=10)
+    table = ops.LayerTable(caches)
+    staging = torch.zeros(2 * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ids = torch.tensor([3, 1000, -1, 2], dtype=torch.int32, device=gpu)
+    offs = torch.tensor([0, 0, 0, 1 << 40], dtype=torch.int64, device=gpu)
+    ops.gather(table, ids, offs, staging)
+    torch.cuda.synchronize()
+    exp = torch.cat([c[:, 3].reshape(-1).view(torch.uint8) for c in caches])
+    assert torch.equal(staging[: shape.slot_bytes], exp)
+    assert not staging[shape.slot_bytes:].any()
+
+
+# ---------------------------------------------------------------------------
+# fused re-rotation
+
+
+def _rerotate_case(gpu, dt, style, head_dim, rot_dim, heads=4, layers=3, seed=0,
+                   deltas=(0, 1, 517, 32767, 123), theta=500000.0, scale=1.0):
+    shape = KVShape(layers, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    rng = np.random.default_rng(seed)
+    chunk_pages = [int(x) for x in rng.integers(1, 4, size=len(deltas))]
+    n = sum(chunk_pages)
+    nb = n + 5
+    src_caches = rand_caches(shape, nb, dt, gpu, seed=seed + 1, scale=scale)
+    # records: gather every block of a source pool into staging
+    staging = torch.zeros(n * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    offs = np.arange(n, dtype=np.int64) * shape.slot_bytes
+    ops.gather(ops.LayerTable(src_caches), rng.permutation(nb)[:n].astype(np.int32), offs, staging)
+    dst = rand_caches(shape, nb, dt, gpu, seed=seed + 2)
+    dst_ref = [to_bits_np(c, dt) for c in dst]
+    page_ids = rng.permutation(nb)[:n].astype(np.int32)
+    ridx, uniq = position.page_rope_index(chunk_pages, deltas)
+    tabs = position.delta_tables(uniq or [0], rot_dim, theta, device=gpu)
+    k_scale = None
+    ks_np = None
+    if dt == "e4m3":
+        ks_np = (rng.random(layers).astype(np.float32) * 0.5 + 0.01)
+        k_scale = torch.from_numpy(ks_np).to(gpu)
+    ops.scatter_rerotate(ops.LayerTable(dst), page_ids, offs, staging, tabs, ridx,
+                         rot_dim=rot_dim, style=style, k_scale=k_scale)
+    page_delta = np.repeat(np.asarray(deltas, np.int64), chunk_pages)
+    oracle.scatter_rerotate(
+        dst_ref, page_ids, offs, staging.cpu().numpy(), shape.layer_bytes,
+        dtype=ORC_DT[dt], rot_dim=rot_dim, style=0 if style == "neox" else 1,
+        stored_pos=np.zeros(n, np.int64), new_pos=page_delta, rotate=page_delta != 0,
+        theta=theta, k_scale=ks_np)
+    torch.cuda.synchronize()
+    return shape, dst, dst_ref, page_ids, page_delta
+
+
+@pytest.mark.parametrize(
+    "dt,style,head_dim,rot_dim",
+    [
+        ("bf16", "neox", 128, 128),
+        ("bf16", "gptj", 128, 128),
+        ("bf16", "neox", 128, 64),
+        ("bf16", "neox", 64, 64),
+        ("fp16", "neox", 128, 128),
+        ("fp16", "gptj", 256, 128),
+        ("e4m3", "neox", 128, 128),
+        ("e4m3", "gptj", 128, 96),
+    ],
+)
+def test_rerotate_matches_oracle(gpu, dt, style, head_dim, rot_dim):
+    print(f"case: rerotate {dt} {style} D{head_dim} R{rot_dim}", flush=True)
+    shape, dst, dst_ref, page_ids, page_delta = _rerotate_case(
+        gpu, dt, style, head_dim, rot_dim, scale=40.0 if dt == "e4m3" else 1.0)
+    for l in range(shape.num_layers):
+        got = to_bits_np(dst[l], dt)
+        ref = dst_ref[l]
+        # V (index 1) and untouched blocks: bit-exact
+        assert np.array_equal(got[1], ref[1])
+        ok, msg = rotation_within_tolerance(got[0], ref[0], dt)
+        assert ok, f"layer {l}: {msg}"
+        # un-rotated pages (delta 0) are bit-exact copies
+        zero_pages = page_ids[page_delta == 0]
+        assert np.array_equal(got[0][zero_pages], ref[0][zero_pages])
+        if dt == "bf16":
+            # atol 1e-2 against the float64 result
+            a = torch.from_numpy(got[0].view(np.int16)).view(torch.bfloat16).float()
+            b = torch.from_numpy(ref[0].view(np.int16)).view(torch.bfloat16).float()
+            assert (a - b).abs().max().item() <= 1e-2 * max(1.0, b.abs().max().item())
+
+
+def test_rerotate_inverse_is_identity(gpu):
+    """Rotating by +d then -d returns the input within 2 bf16 ulps."""
+    print("case: rerotate inverse", flush=True)
+    shape = KVShape(2, 8, 128, 16, 2)
+    nb = 12
+    caches = rand_caches(shape, nb, "bf16", gpu, seed=21)
+    ids = np.arange(nb, dtype=np.int32)
+    offs = np.arange(nb, dtype=np.int64) * shape.slot_bytes
+    st = torch.zeros(nb * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(caches), ids, offs, st)
+    tabs = position.delta_tables([12345, -12345], 128, 500000.0, device=gpu)
+    mid = [torch.zeros_like(c) for c in caches]
+    ops.scatter_rerotate(ops.LayerTable(mid), ids, offs, st, tabs, np.zeros(nb, np.int32))
+    st2 = torch.zeros_like(st)
+    ops.gather(ops.LayerTable(mid), ids, offs, st2)
+    back = [torch.zeros_like(c) for c in caches]
+    ops.scatter_rerotate(ops.LayerTable(back), ids, offs, st2, tabs, np.ones(nb, np.int32))
+    torch.cuda.synchronize()
+    for c, b in zip(caches, back):
+        ok, msg = rotation_within_tolerance(to_bits_np(b, "bf16"), to_bits_np(c, "bf16"),
+                                            "bf16", rel_row=2.0 ** -7)
+        assert ok, msg
+        assert torch.equal(b[1], c[1])
+
+
+def test_rerotate_bad_geometry_rejected(gpu):
+    shape = KVShape(1, 1, 64, 16, 1)
+    caches = rand_caches(shape, 2, "e4m3", gpu, seed=22)
+    st = torch.zeros(shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    tabs = position.delta_tables([5], 48, device=gpu)
+    with pytest.raises(DaserKVError):
+        # neox fp8 needs rot_dim/2 to be a multiple of 16 elements
+        ops.scatter_rerotate(ops.LayerTable(caches), [0], [0], st, tabs, [0], rot_dim=48,
+                             k_scale=torch.ones(1, device=gpu))
