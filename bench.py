@@ -1,0 +1,314 @@
+"""Benchmark of the MI355X KV data-movement path.
+
+A step is one offload gather plus one load scatter over the Llama-3-8B
+workload (config 2: 32 layers, 8 KV heads, head_dim 128, block_size 16,
+bf16, 64 requests with U[512, 8192] tokens on a randomly permuted block
+pool, records packed into 256-token chunk buffers). Each pass is one kernel
+launch covering every page of every request over all 32 layers.
+
+value = algorithmic bytes of the step (gather reads P, writes P; scatter the
+same: 4P) / step time, inputs resident in HBM. The fused re-rotate+scatter of
+config 3 (RAG reuse) is reported beside it in tokens/s.
+
+Per-kernel durations come from HIP events recorded on the launch stream
+around every timed launch. cpu_baseline times the C oracle (one thread) on a
+bounded sample of the same shape on the host.
+
+Usage: python bench.py [--steps K] [--warmup W] [--configs 2,3,4,5] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "KV gather/scatter GB/s + % HBM peak; fused re-rotate+load tokens/s"
+HBM_PEAK_GBS = 8000.0
+THETA = 500000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def fill_caches(torch, shape, num_blocks, dtype, dev, seed):
+    """One (L, 2, NB, bs, H, D) allocation, viewed per layer, ~N(0,1).
+
+    dtype "bf16", or "fp8": e4m3fn codes of N(0,1) values quantised with a
+    per-layer scale amax / 448 (returned as the third element)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    dims = (shape.num_layers, 2, num_blocks, shape.block_size, shape.num_heads,
+            shape.head_dim)
+    if dtype == "bf16":
+        full = torch.empty(dims, dtype=torch.bfloat16, device=dev)
+        flat = full.view(-1)
+        for i in range(0, flat.numel(), 1 << 30):
+            flat[i:i + (1 << 30)].normal_(generator=g)
+        return full, [full[l] for l in range(shape.num_layers)], None
+    full = torch.empty(dims, dtype=torch.float8_e4m3fn, device=dev)
+    scales = torch.empty(shape.num_layers, dtype=torch.float32, device=dev)
+    for l in range(shape.num_layers):
+        tmp = torch.empty(dims[1:], dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        s = tmp.abs().amax().float() / 448.0
+        full[l].copy_((tmp.float() / s).to(torch.float8_e4m3fn))
+        scales[l] = s
+        del tmp
+    return full, [full[l] for l in range(shape.num_layers)], scales
+
+
+class Timer:
+    """HIP events around each launch on the current (launch) stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def __enter__(self):
+        s = self.torch.cuda.Event(enable_timing=True)
+        s.record()
+        self.pairs.append([s, None])
+        return self
+
+    def __exit__(self, *exc):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs[-1][1] = e
+
+    def mean_ms(self):
+        ts = [s.elapsed_time(e) for s, e in self.pairs]
+        return float(np.mean(ts)) if ts else float("nan")
+
+    def reset(self):
+        self.pairs = []
+
+
+def bench_copy(torch, ops, wl, dtype, dev, steps, warmup):
+    """Config 2/4: gather then scatter per step. Returns the result dict."""
+    shape = wl.shape
+    log(f"[bench] allocating caches {wl.num_blocks} blocks x {shape.num_layers} layers "
+        f"({wl.num_blocks * shape.slot_bytes / 1e9:.1f} GB) + staging "
+        f"{wl.staging_bytes / 1e9:.1f} GB")
+    full, caches, _ = fill_caches(torch, shape, wl.num_blocks, dtype, dev, seed=1)
+    table = ops.LayerTable(caches)
+    staging = torch.empty(wl.staging_bytes, dtype=torch.uint8, device=dev)
+    ids = torch.from_numpy(wl.page_ids).to(dev)
+    offs = torch.from_numpy(wl.slot_offsets).to(dev)
+    # the scatter's page list in destination-block order (as ops.scatter
+    # orders host tables)
+    s_ids_np, s_offs_np, _ = ops.dest_order(wl.page_ids, wl.slot_offsets)
+    s_ids = torch.from_numpy(s_ids_np.astype(np.int32)).to(dev)
+    s_offs = torch.from_numpy(s_offs_np).to(dev)
+    tg, ts = Timer(torch), Timer(torch)
+    for i in range(warmup):
+        ops.gather(table, ids, offs, staging)
+        ops.scatter(table, s_ids, s_offs, staging)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        with tg:
+            ops.gather(table, ids, offs, staging)
+        with ts:
+            ops.scatter(table, s_ids, s_offs, staging)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # a cheap end-to-end check: the scatter wrote back what the gather read
+    probe = int(wl.page_ids[len(wl.page_ids) // 2])
+    p_idx = len(wl.page_ids) // 2
+    rec = staging[int(wl.slot_offsets[p_idx]):int(wl.slot_offsets[p_idx]) + shape.layer_bytes]
+    ok = torch.equal(rec, caches[0][:, probe].reshape(-1).view(torch.uint8))
+    P = wl.payload_bytes
+    g_ms, s_ms = tg.mean_ms(), ts.mean_ms()
+    del full, caches, table, staging
+    torch.cuda.empty_cache()
+    return {
+        "payload_bytes": P,
+        "pages": wl.n_pages,
+        "tokens": wl.tokens,
+        "step_ms": wall * 1e3 / steps,
+        "gather_ms": g_ms,
+        "scatter_ms": s_ms,
+        "gather_GBps": 2 * P / (g_ms * 1e-3) / 1e9,
+        "scatter_GBps": 2 * P / (s_ms * 1e-3) / 1e9,
+        "step_GBps": 4 * P / wall * steps / 1e9,
+        "probe_ok": bool(ok),
+    }
+
+
+def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
+    """Config 3/5: fused re-rotate+scatter of reused chunks."""
+    shape = wl.shape
+    src_bytes = wl.meta["src_staging_bytes"]
+    log(f"[bench] rerotate: source records {src_bytes / 1e9:.1f} GB, destination "
+        f"{wl.num_blocks * shape.slot_bytes / 1e9:.1f} GB")
+    full, caches, k_scale = fill_caches(torch, shape, wl.num_blocks, dtype, dev, seed=2)
+    table = ops.LayerTable(caches)
+    src = torch.empty(src_bytes, dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev).manual_seed(3)
+    for i in range(0, src_bytes, 1 << 30):
+        n = min(1 << 30, src_bytes - i)
+        if dtype == "fp8":
+            src[i:i + n].random_(0, 256, generator=g)
+            src[i:i + n][src[i:i + n] == 0x7F] = 0  # no NaN codes in the synthetic data
+        else:
+            src[i:i + n].view(torch.bfloat16).normal_(generator=g)
+    ridx, uniq = position.page_rope_index(wl.chunk_pages, wl.chunk_delta)
+    tabs = position.delta_tables(uniq, shape.head_dim, THETA, device=dev)
+    s_ids, s_offs, s_ridx = ops.dest_order(wl.page_ids, wl.src_offsets, ridx)
+    ids = torch.from_numpy(s_ids.astype(np.int32)).to(dev)
+    offs = torch.from_numpy(s_offs).to(dev)
+    ridx_d = torch.from_numpy(s_ridx.astype(np.int32)).to(dev)
+    t = Timer(torch)
+    for _ in range(warmup):
+        ops.scatter_rerotate(table, ids, offs, src, tabs, ridx_d, k_scale=k_scale)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        with t:
+            ops.scatter_rerotate(table, ids, offs, src, tabs, ridx_d, k_scale=k_scale)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = t.mean_ms()
+    P = wl.n_pages * shape.slot_bytes
+    del full, caches, table, src
+    torch.cuda.empty_cache()
+    return {
+        "payload_bytes": P,
+        "pages": wl.n_pages,
+        "tokens": wl.tokens,
+        "kernel_ms": ms,
+        "wall_ms_per_launch": wall * 1e3 / steps,
+        "tokens_per_s": wl.tokens / (ms * 1e-3),
+        "GBps": 2 * P / (ms * 1e-3) / 1e9,
+        "frac_hbm_peak": 2 * P / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    }
+
+
+def cpu_baseline(budget_s: float = 12.0) -> dict:
+    """C oracle (single thread) gather+scatter on a sample of config 2's
+    shape: 256 pages of a 1024-block host pool, repeated to ~budget_s."""
+    from daser_amd import workloads
+    from oracle import oracle
+
+    shape = workloads.LLAMA3_8B
+    wl = workloads.ragged(shape, 4, 1024, 1024, seed=0, num_blocks=1024)
+    layers = [np.full((2, 1024, 16, 8, 128), 0x3F80 + l, dtype=np.uint16)
+              for l in range(shape.num_layers)]
+    staging = np.zeros(wl.staging_bytes, dtype=np.uint8)
+    P = wl.payload_bytes
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.gather(layers, wl.page_ids, wl.slot_offsets, staging, shape.layer_bytes)
+        oracle.scatter(layers, wl.page_ids, wl.slot_offsets, staging, shape.layer_bytes)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {
+        "value": 4 * P * n / el / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"C oracle gather+scatter, {wl.n_pages} pages (256 x 2 MiB records, "
+                  f"Llama-3-8B shape) x {n} repetitions in {el:.1f} s, one thread",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--configs", default="2,3")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the KV path shards per rank with no "
+              "exchange, so --gpus must be 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from daser_amd import ops, position, workloads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    configs = [int(c) for c in args.configs.split(",") if c]
+    res = {}
+    for c in configs:
+        log(f"[bench] config {c}: {workloads.CONFIG_NAMES[c]}")
+        wl = workloads.config(c)
+        if c in (2, 4):
+            res[c] = bench_copy(torch, ops, wl, "bf16" if c == 2 else "fp8", dev,
+                                args.steps, args.warmup)
+        else:
+            res[c] = bench_rerotate(torch, ops, position, wl, "bf16", dev,
+                                    args.steps, args.warmup)
+        log(f"[bench] config {c}: {json.dumps(res[c])}")
+
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "data": "synthetic (seeded N(0,1) bf16 KV, seeded random block permutation)"}
+    if 2 in res:
+        r = res[2]
+        out.update({
+            "value": round(r["step_GBps"], 1),
+            "unit": "GB/s",
+            "ms_per_step": round(r["step_ms"], 3),
+            "dtype": "u8",
+            "config": {"workload": workloads.CONFIG_NAMES[2], "kv_dtype": "bf16",
+                       "pages": r["pages"], "tokens": r["tokens"],
+                       "payload_bytes_per_pass": r["payload_bytes"]},
+        })
+        dom = "gather" if r["gather_ms"] >= r["scatter_ms"] else "scatter"
+        achieved = r[f"{dom}_GBps"]
+        out["roofline"] = {
+            "kernel": f"kv_page_copy_kernel<{'true' if dom == 'gather' else 'false'}> ({dom})",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        }
+        out["kernels"] = {
+            "gather": {"ms": round(r["gather_ms"], 4), "GBps": round(r["gather_GBps"], 1),
+                       "frac": round(r["gather_GBps"] / HBM_PEAK_GBS, 4)},
+            "scatter": {"ms": round(r["scatter_ms"], 4), "GBps": round(r["scatter_GBps"], 1),
+                        "frac": round(r["scatter_GBps"] / HBM_PEAK_GBS, 4)},
+        }
+        out["check"] = {"round_trip_probe": r["probe_ok"]}
+    for c in (3, 5):
+        if c in res:
+            r = res[c]
+            out[f"rerotate_cfg{c}"] = {
+                "workload": workloads.CONFIG_NAMES[c],
+                "tokens_per_s": round(r["tokens_per_s"]),
+                "GBps": round(r["GBps"], 1), "frac": round(r["frac_hbm_peak"], 4),
+                "kernel_ms": round(r["kernel_ms"], 4), "tokens": r["tokens"]}
+    if 4 in res:
+        r = res[4]
+        out["fp8_cfg4"] = {"gather_GBps": round(r["gather_GBps"], 1),
+                           "scatter_GBps": round(r["scatter_GBps"], 1),
+                           "gather_ms": round(r["gather_ms"], 4),
+                           "scatter_ms": round(r["scatter_ms"], 4)}
+    if "value" not in out:
+        r = res[configs[0]]
+        out.update({"value": round(r.get("tokens_per_s", 0.0)), "unit": "tokens/s",
+                    "ms_per_step": round(r.get("kernel_ms", 0.0), 3), "dtype": "bf16",
+                    "config": {"workload": workloads.CONFIG_NAMES[configs[0]]}})
+    if not args.no_cpu:
+        log("[bench] cpu baseline (C oracle, one thread)")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

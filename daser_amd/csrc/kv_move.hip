@@ -11,11 +11,12 @@
 // contiguous inside each per-layer cache; only the block index is permuted.
 // The unit of work is therefore one (page, layer): two contiguous runs of
 // page_bytes (K and V) on each side. One 256-lane workgroup owns one unit and
-// moves it with 16-byte lane vectors (global_load_dwordx4 /
-// global_store_dwordx4), issuing every load of a round before any store so
-// each lane keeps up to 2*kUnroll 16-byte requests in flight. No LDS is
-// needed for the copy: both sides are contiguous within a unit. The
-// re-rotation kernel keeps the unit's (cos, sin) table in LDS.
+// moves it with 16-byte lane vectors (buffer_load_dwordx4 /
+// buffer_store_dwordx4 through a descriptor bounded to the run), issuing
+// every load of a round before any store so each lane keeps up to 2*U
+// 16-byte requests in flight. No LDS is needed for the copy: both sides are
+// contiguous within a unit. The re-rotation kernel keeps the unit's
+// (cos, sin) table in LDS.
 //
 // Reference being replaced: the Python per-(request, block, layer) torch
 // copy_ loops of daser/connector/daser_connector.py:536-551 (load) and
@@ -30,10 +31,21 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;   // 4 wave64 per workgroup
-constexpr int kCopyUnroll = 8;  // 16-byte vectors per lane per half per round
-constexpr int kRotUnroll = 4;   // rotation tasks per lane per round
-constexpr int kMaxRotHalf = 512;  // LDS table capacity: rot_dim <= 1024
+constexpr int kThreads = 256;     // 4 wave64 per workgroup
+constexpr int kGatherUnroll = 16;  // 16-byte vectors per lane per half per round
+constexpr int kScatterUnroll = 8;
+constexpr int kRotUnroll = 4;      // rotation tasks per lane per round
+constexpr int kMaxRotHalf = 512;   // LDS table capacity: rot_dim <= 1024
+constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
+
+// Cache-policy bits of gfx950 buffer instructions (CPol: sc0 = 1, nt = 2,
+// sc1 = 16). Loads stream through (nt); stores are written with sc0 sc1,
+// which measured fastest for these write-once streams (6.0 vs 5.2 TB/s for
+// default-policy stores at the Llama-3-8B shape).
+constexpr int kLoadPolicy = 2;
+constexpr int kStorePolicy = 17;
+// Buffer descriptor word 3 for raw (untyped) dword access on CDNA3/4.
+constexpr int kRsrcWord3 = 0x00020000;
 
 struct UnitArgs {
   const uint64_t* layer_base;
@@ -46,13 +58,25 @@ struct UnitArgs {
   uint8_t* staging;
   int64_t staging_bytes;
   int64_t layer_bytes;
+  int64_t n_units;
   int32_t n_layers;
   int32_t layer0;
 };
 
-// Resolves the cache-side and record-side addresses of the workgroup's unit.
-// Returns false when the unit's block id or record range is out of bounds
-// (the unit is then skipped, never touched).
+// Workgroup -> unit. Hardware deals consecutive workgroup ids round-robin
+// over the 8 XCDs; remapping so that each XCD walks one contiguous eighth of
+// the unit list keeps each XCD's stream of records contiguous (measured
+// +2% over the identity mapping for the gather). Returns -1 past the end.
+__device__ __forceinline__ int64_t xcd_unit(int64_t n_units) {
+  const int64_t per = (n_units + kXcds - 1) / kXcds;
+  const int64_t b = blockIdx.x;
+  const int64_t u = (b % kXcds) * per + b / kXcds;
+  return u < n_units ? u : -1;
+}
+
+// Resolves the cache-side and record-side addresses of unit (page, layer),
+// page-major. Returns false when the unit's block id or record range is out
+// of bounds (the unit is then skipped, never touched).
 __device__ __forceinline__ bool unit_addresses(const UnitArgs& a, int64_t unit,
                                                uint8_t** cache, uint8_t** rec,
                                                int* layer) {
@@ -68,73 +92,69 @@ __device__ __forceinline__ bool unit_addresses(const UnitArgs& a, int64_t unit,
   return true;
 }
 
-__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// A buffer descriptor over [p, p + bytes): out-of-range accesses through it
+// read 0 / are dropped by the hardware.
+__device__ __forceinline__ rsrc_t make_rsrc(const uint8_t* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p), 0, (int)bytes,
+                                           kRsrcWord3);
 }
-__device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+__device__ __forceinline__ u32x4 bload(rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kLoadPolicy);
 }
-__device__ __forceinline__ void st16(uint8_t* p, u32x4 v) {
-  *reinterpret_cast<u32x4*>(p) = v;
-}
-__device__ __forceinline__ void st16_stream(uint8_t* p, u32x4 v) {
-  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+__device__ __forceinline__ void bstore(rsrc_t r, int off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kStorePolicy);
 }
 
-// Copies the two page_bytes runs (K at +0, V at +kv_src_off / +kv_dst_off).
-// Record-side accesses are streamed (non-temporal): records are produced once
-// and consumed by a DMA or consumed once by the load.
-template <bool kToRecord>
-__device__ __forceinline__ void copy_halves(const uint8_t* src_k,
-                                            const uint8_t* src_v,
+// Copies the two page_bytes runs src_k -> dst_k and src_v -> dst_v, issuing
+// all 2*U loads of a round before its stores.
+template <int U>
+__device__ __forceinline__ void copy_halves(const uint8_t* src_k, const uint8_t* src_v,
                                             uint8_t* dst_k, uint8_t* dst_v,
                                             int64_t page_bytes) {
-  const int64_t nvec = page_bytes >> 4;
-  for (int64_t base = threadIdx.x; base < nvec;
-       base += (int64_t)kThreads * kCopyUnroll) {
-    u32x4 rk[kCopyUnroll], rv[kCopyUnroll];
+  const rsrc_t sk = make_rsrc(src_k, page_bytes), sv = make_rsrc(src_v, page_bytes);
+  const rsrc_t dk = make_rsrc(dst_k, page_bytes), dv = make_rsrc(dst_v, page_bytes);
+  const int nvec = (int)(page_bytes >> 4);
+  for (int base = threadIdx.x; base < nvec; base += kThreads * U) {
+    u32x4 rk[U], rv[U];
 #pragma unroll
-    for (int k = 0; k < kCopyUnroll; ++k) {
-      const int64_t i = base + (int64_t)k * kThreads;
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * kThreads;
       if (i < nvec) {
-        if (kToRecord) {
-          rk[k] = ld16(src_k + (i << 4));
-          rv[k] = ld16(src_v + (i << 4));
-        } else {
-          rk[k] = ld16_stream(src_k + (i << 4));
-          rv[k] = ld16_stream(src_v + (i << 4));
-        }
+        rk[k] = bload(sk, i << 4);
+        rv[k] = bload(sv, i << 4);
       }
     }
 #pragma unroll
-    for (int k = 0; k < kCopyUnroll; ++k) {
-      const int64_t i = base + (int64_t)k * kThreads;
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * kThreads;
       if (i < nvec) {
-        if (kToRecord) {
-          st16_stream(dst_k + (i << 4), rk[k]);
-          st16_stream(dst_v + (i << 4), rv[k]);
-        } else {
-          st16(dst_k + (i << 4), rk[k]);
-          st16(dst_v + (i << 4), rv[k]);
-        }
+        bstore(dk, i << 4, rk[k]);
+        bstore(dv, i << 4, rv[k]);
       }
     }
   }
 }
 
-// One workgroup per (page, layer) unit; grid.x = n_pages * n_layers.
-template <bool kGather>
-__global__ __launch_bounds__(kThreads) void kv_page_copy_kernel(UnitArgs a) {
+// Gather: one workgroup per (page, layer) unit, XCD-contiguous order.
+__global__ __launch_bounds__(kThreads) void kv_gather_kernel(UnitArgs a) {
+  const int64_t u = xcd_unit(a.n_units);
+  uint8_t *cache, *rec;
+  int l;
+  if (u < 0 || !unit_addresses(a, u, &cache, &rec, &l)) return;
+  copy_halves<kGatherUnroll>(cache, cache + a.kv_stride, rec, rec + a.page_bytes,
+                             a.page_bytes);
+}
+
+// Scatter: one workgroup per unit in page-list order (the host orders the
+// list by destination block, which keeps the page writes near-sequential).
+__global__ __launch_bounds__(kThreads) void kv_scatter_kernel(UnitArgs a) {
   uint8_t *cache, *rec;
   int l;
   if (!unit_addresses(a, blockIdx.x, &cache, &rec, &l)) return;
-  if (kGather) {
-    copy_halves<true>(cache, cache + a.kv_stride, rec, rec + a.page_bytes,
-                      a.page_bytes);
-  } else {
-    copy_halves<false>(rec, rec + a.page_bytes, cache, cache + a.kv_stride,
-                       a.page_bytes);
-  }
+  copy_halves<kScatterUnroll>(rec, rec + a.page_bytes, cache, cache + a.kv_stride,
+                              a.page_bytes);
 }
 
 // ---------------------------------------------------------------------------
@@ -272,40 +292,41 @@ __device__ __forceinline__ void rotate_k_page(const RotArgs& ra,
                                               float inv_scale) {
   using C = Codec<DT>;
   constexpr int VE = C::VE;
-  const int64_t row_bytes = (int64_t)ra.row_vecs << 4;
-  const int64_t rows = ra.u.page_bytes / row_bytes;
-  const int64_t ntask = rows * ra.tasks_per_row;
-  const int64_t half_off = (int64_t)ra.rot_half * 16 / VE;  // bytes to partner
-  for (int64_t base = threadIdx.x; base < ntask;
-       base += (int64_t)kThreads * kRotUnroll) {
+  const rsrc_t rs = make_rsrc(src, ra.u.page_bytes);
+  const rsrc_t rd = make_rsrc(dst, ra.u.page_bytes);
+  const int row_bytes = ra.row_vecs << 4;
+  const int rows = (int)(ra.u.page_bytes / row_bytes);
+  const int ntask = rows * ra.tasks_per_row;
+  const int half_off = ra.rot_half * 16 / VE;  // bytes to the neox partner
+  for (int base = threadIdx.x; base < ntask; base += kThreads * kRotUnroll) {
     u32x4 a[kRotUnroll], b[kRotUnroll];
-    int64_t off[kRotUnroll];
+    int off[kRotUnroll];
     int kind[kRotUnroll];  // 0 = rotate, 1 = copy, -1 = none
     int c_of[kRotUnroll];
 #pragma unroll
     for (int k = 0; k < kRotUnroll; ++k) {
-      const int64_t t = base + (int64_t)k * kThreads;
+      const int t = base + k * kThreads;
       kind[k] = -1;
       if (t < ntask) {
-        const int64_t row = t / ra.tasks_per_row;
-        const int c = (int)(t - row * ra.tasks_per_row);
+        const int row = t / ra.tasks_per_row;
+        const int c = t - row * ra.tasks_per_row;
         c_of[k] = c;
         if (c < ra.task_vecs) {
           kind[k] = 0;
-          off[k] = row * row_bytes + ((int64_t)c << 4);
-          a[k] = ld16_stream(src + off[k]);
-          if (STYLE == DSR_ROPE_NEOX) b[k] = ld16_stream(src + off[k] + half_off);
+          off[k] = row * row_bytes + (c << 4);
+          a[k] = bload(rs, off[k]);
+          if (STYLE == DSR_ROPE_NEOX) b[k] = bload(rs, off[k] + half_off);
         } else {
           kind[k] = 1;
-          off[k] = row * row_bytes + ((int64_t)(ra.tail_vec0 + c - ra.task_vecs) << 4);
-          a[k] = ld16_stream(src + off[k]);
+          off[k] = row * row_bytes + ((ra.tail_vec0 + c - ra.task_vecs) << 4);
+          a[k] = bload(rs, off[k]);
         }
       }
     }
 #pragma unroll
     for (int k = 0; k < kRotUnroll; ++k) {
       if (kind[k] == 1) {
-        st16(dst + off[k], a[k]);
+        bstore(rd, off[k], a[k]);
       } else if (kind[k] == 0) {
         float x[VE];
         C::decode(a[k], x);
@@ -320,8 +341,8 @@ __device__ __forceinline__ void rotate_k_page(const RotArgs& ra,
             x[e] = (x1 * cs.x - x2 * cs.y) * inv_scale;
             z[e] = (x2 * cs.x + x1 * cs.y) * inv_scale;
           }
-          st16(dst + off[k], C::encode(x));
-          st16(dst + off[k] + half_off, C::encode(z));
+          bstore(rd, off[k], C::encode(x));
+          bstore(rd, off[k] + half_off, C::encode(z));
         } else {
           const int j0 = c_of[k] * (VE / 2);
 #pragma unroll
@@ -331,13 +352,37 @@ __device__ __forceinline__ void rotate_k_page(const RotArgs& ra,
             x[2 * e] = (x1 * cs.x - x2 * cs.y) * inv_scale;
             x[2 * e + 1] = (x2 * cs.x + x1 * cs.y) * inv_scale;
           }
-          st16(dst + off[k], C::encode(x));
+          bstore(rd, off[k], C::encode(x));
         }
       }
     }
   }
 }
 
+// Copies one page_bytes run, all U loads of a round before its stores.
+template <int U>
+__device__ __forceinline__ void copy_run(const uint8_t* src, uint8_t* dst,
+                                         int64_t page_bytes) {
+  const rsrc_t rs = make_rsrc(src, page_bytes), rd = make_rsrc(dst, page_bytes);
+  const int nvec = (int)(page_bytes >> 4);
+  for (int base = threadIdx.x; base < nvec; base += kThreads * U) {
+    u32x4 r[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * kThreads;
+      if (i < nvec) r[k] = bload(rs, i << 4);
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * kThreads;
+      if (i < nvec) bstore(rd, i << 4, r[k]);
+    }
+  }
+}
+
+// One workgroup per (page, layer) unit in page-list order. V, and K of pages
+// without a table (rope_idx < 0), are copied bit-exactly; K of the others is
+// re-rotated row by row with the page's (cos, sin) table staged in LDS.
 template <int DT, int STYLE>
 __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs ra) {
   __shared__ float2 tab[kMaxRotHalf];
@@ -347,9 +392,8 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
   const int64_t p = (int64_t)blockIdx.x / ra.u.n_layers;
   const int ti = ra.rope_idx[p];
   const int64_t pb = ra.u.page_bytes;
-  // V half (and K when not rotated) is a plain copy.
   if (ti < 0 || ti >= ra.n_tables) {
-    copy_halves<false>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    copy_halves<kScatterUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
     return;
   }
   const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
@@ -360,26 +404,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
     inv_scale = 1.0f / scale;
   }
   __syncthreads();
-  // V: copy with the full unroll (no rotation).
-  {
-    const uint8_t* sv = rec + pb;
-    uint8_t* dv = cache + ra.u.kv_stride;
-    const int64_t nvec = pb >> 4;
-    for (int64_t base = threadIdx.x; base < nvec;
-         base += (int64_t)kThreads * kCopyUnroll) {
-      u32x4 r[kCopyUnroll];
-#pragma unroll
-      for (int k = 0; k < kCopyUnroll; ++k) {
-        const int64_t i = base + (int64_t)k * kThreads;
-        if (i < nvec) r[k] = ld16_stream(sv + (i << 4));
-      }
-#pragma unroll
-      for (int k = 0; k < kCopyUnroll; ++k) {
-        const int64_t i = base + (int64_t)k * kThreads;
-        if (i < nvec) st16(dv + (i << 4), r[k]);
-      }
-    }
-  }
+  copy_run<kScatterUnroll>(rec + pb, cache + ra.u.kv_stride, pb);
   rotate_k_page<DT, STYLE>(ra, rec, cache, tab, scale, inv_scale);
 }
 
@@ -397,6 +422,7 @@ int check_common(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   if (n_pages == 0 || n_layers == 0) return DSR_OK;
   if (!layer_base || !page_ids || !slot_offsets || !staging) return DSR_ERR_ARG;
   if (layer_bytes < 2 * page_bytes) return DSR_ERR_SHAPE;
+  if (page_bytes > 0x7fffffffLL) return DSR_ERR_SHAPE;  // one buffer descriptor per run
   if ((int64_t)n_pages * n_layers > 0x7fffffffLL) return DSR_ERR_ARG;
   if (!aligned16(kv_stride) || !aligned16(page_stride) || !aligned16(page_bytes) ||
       !aligned16(layer_bytes) || !aligned16p(staging))
@@ -407,7 +433,7 @@ int check_common(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
 UnitArgs make_unit(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
                    int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
                    const int32_t* page_ids, const int64_t* slot_offsets,
-                   const void* staging, int64_t staging_bytes,
+                   int n_pages, const void* staging, int64_t staging_bytes,
                    int64_t layer_bytes, int layer0) {
   UnitArgs a;
   a.layer_base = layer_base;
@@ -422,6 +448,7 @@ UnitArgs make_unit(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   a.layer_bytes = layer_bytes;
   a.n_layers = n_layers;
   a.layer0 = layer0;
+  a.n_units = (int64_t)n_pages * n_layers;
   return a;
 }
 
@@ -465,10 +492,11 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
                         staging_bytes, layer_bytes, layer0);
   if (rc != DSR_OK || n_pages == 0 || n_layers == 0) return rc;
   UnitArgs a = make_unit(layer_base, n_layers, kv_stride, page_stride, page_bytes,
-                         num_blocks, page_ids, slot_offsets, staging,
+                         num_blocks, page_ids, slot_offsets, n_pages, staging,
                          staging_bytes, layer_bytes, layer0);
-  const unsigned grid = (unsigned)((int64_t)n_pages * n_layers);
-  kv_page_copy_kernel<true><<<grid, kThreads, 0, (hipStream_t)stream>>>(a);
+  // whole multiple of the XCD count so that the remap covers every unit
+  const unsigned grid = (unsigned)((a.n_units + kXcds - 1) / kXcds * kXcds);
+  kv_gather_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(a);
   return (int)hipGetLastError();
 }
 
@@ -482,10 +510,9 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
                         staging_bytes, layer_bytes, layer0);
   if (rc != DSR_OK || n_pages == 0 || n_layers == 0) return rc;
   UnitArgs a = make_unit(layer_base, n_layers, kv_stride, page_stride, page_bytes,
-                         num_blocks, page_ids, slot_offsets, staging,
+                         num_blocks, page_ids, slot_offsets, n_pages, staging,
                          staging_bytes, layer_bytes, layer0);
-  const unsigned grid = (unsigned)((int64_t)n_pages * n_layers);
-  kv_page_copy_kernel<false><<<grid, kThreads, 0, (hipStream_t)stream>>>(a);
+  kv_scatter_kernel<<<(unsigned)a.n_units, kThreads, 0, (hipStream_t)stream>>>(a);
   return (int)hipGetLastError();
 }
 
@@ -539,8 +566,8 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
 
   RotArgs ra;
   ra.u = make_unit(layer_base, n_layers, kv_stride, page_stride, page_bytes,
-                   num_blocks, page_ids, slot_offsets, staging, staging_bytes,
-                   layer_bytes, layer0);
+                   num_blocks, page_ids, slot_offsets, n_pages, staging,
+                   staging_bytes, layer_bytes, layer0);
   ra.cos_sin = reinterpret_cast<const float2*>(cos_sin);
   ra.rope_idx = rope_idx;
   ra.n_tables = n_tables;
@@ -550,7 +577,7 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
   ra.tail_vec0 = rot_dim * esize / 16;
   ra.tasks_per_row = task_vecs + (head_dim - rot_dim) * esize / 16;
   ra.k_scale = k_scale;
-  const unsigned grid = (unsigned)((int64_t)n_pages * n_layers);
+  const unsigned grid = (unsigned)ra.u.n_units;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case DSR_DTYPE_BF16:

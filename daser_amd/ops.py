@@ -136,7 +136,8 @@ def _host_array(x, np_dtype) -> Optional[np.ndarray]:
     return np.asarray(x, dtype=np_dtype)
 
 
-def _validate(layout: PagedKVLayout, page_ids, slot_offsets, staging, layer0, n_layers):
+def _validate(layout: PagedKVLayout, page_ids, slot_offsets, staging, layer0, n_layers,
+              records_written: bool):
     ids = _host_array(page_ids, np.int64)
     offs = _host_array(slot_offsets, np.int64)
     if ids is not None and offs is not None and ids.shape != offs.shape:
@@ -149,9 +150,38 @@ def _validate(layout: PagedKVLayout, page_ids, slot_offsets, staging, layer0, n_
             raise IndexError("slot record outside the staging buffer")
         if np.any(offs % 16):
             raise ValueError("slot offsets must be multiples of 16 bytes")
+        span = (n_layers - 1) * layout.layer_bytes + 2 * layout.page_bytes
+        so = np.sort(offs)
+        # a gather writes the records: two pages' records must not overlap
+        # (a scatter may read one cached record into several pages)
+        if records_written and so.size > 1 and np.any(np.diff(so) < span):
+            raise ValueError("slot records of two pages overlap")
 
 
-def _copy_args(table: LayerTable, page_ids, slot_offsets, staging, layer0, layers):
+def dest_order(page_ids, slot_offsets, extra=None):
+    """Host tables of a scatter, reordered by destination block (stable).
+
+    Processing order does not change the result (each destination block is
+    written once) but near-sequential page writes run faster. Duplicate
+    destination blocks would race inside one launch and are rejected.
+    Device tables are returned unchanged."""
+    ids = _host_array(page_ids, np.int64)
+    offs = _host_array(slot_offsets, np.int64)
+    if ids is None or offs is None or ids.size == 0:
+        return page_ids, slot_offsets, extra
+    order = np.argsort(ids, kind="stable")
+    sids = ids[order]
+    if sids.size > 1 and np.any(sids[1:] == sids[:-1]):
+        raise ValueError("a destination block appears twice in one scatter")
+    ex = None
+    if extra is not None:
+        e = _host_array(extra, np.int64)
+        ex = extra if e is None else e[order]
+    return sids, offs[order], ex
+
+
+def _copy_args(table: LayerTable, page_ids, slot_offsets, staging, layer0, layers,
+               records_written: bool = False):
     lay = table.layout
     first, count = (0, lay.num_layers) if layers is None else layers
     if first < 0 or count < 0 or first + count > lay.num_layers:
@@ -160,7 +190,7 @@ def _copy_args(table: LayerTable, page_ids, slot_offsets, staging, layer0, layer
         raise ValueError("staging must live on the KV caches' device")
     if not staging.is_contiguous():
         raise ValueError("staging must be contiguous")
-    _validate(lay, page_ids, slot_offsets, staging, layer0 + first, count)
+    _validate(lay, page_ids, slot_offsets, staging, layer0 + first, count, records_written)
     ids = _as_device_table(page_ids, torch.int32, lay.device, "page_ids")
     offs = _as_device_table(slot_offsets, torch.int64, lay.device, "slot_offsets")
     if ids.numel() != offs.numel():
@@ -197,7 +227,8 @@ def gather(
     ``layers=(first, count)`` restricts the launch to a layer range; the
     record index of table layer ``first + i`` is ``layer0 + first + i``.
     """
-    args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
+    args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers,
+                            records_written=True)
     rc = _lib.lib().dsr_gather(*args, _stream_handle(table.layout.device))
     _lib.check("dsr_gather", rc)
 
@@ -212,6 +243,7 @@ def scatter(
     layers: Optional[tuple[int, int]] = None,
 ) -> None:
     """Unpacks slot records into pages (reference load loop, :536-551)."""
+    page_ids, slot_offsets, _ = dest_order(page_ids, slot_offsets)
     args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
     rc = _lib.lib().dsr_scatter(*args, _stream_handle(table.layout.device))
     _lib.check("dsr_scatter", rc)
@@ -251,6 +283,7 @@ def scatter_rerotate(
     ridx = _host_array(rope_idx, np.int64)
     if ridx is not None and ridx.size and (ridx.max() >= cos_sin.shape[0] or ridx.min() < -1):
         raise IndexError("rope_idx outside [-1, n_tables)")
+    page_ids, slot_offsets, rope_idx = dest_order(page_ids, slot_offsets, rope_idx)
     args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
     ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")
     if ridx_d.numel() != keep[0].numel():
