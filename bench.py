@@ -177,6 +177,13 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = t.mean_ms()
+    # the same page list as a plain scatter: the copy ceiling of this layout
+    tc = Timer(torch)
+    for _ in range(steps):
+        with tc:
+            ops.scatter(table, ids, offs, src)
+    torch.cuda.synchronize()
+    copy_ms = tc.mean_ms()
     P = wl.n_pages * shape.slot_bytes
     del full, caches, table, src
     torch.cuda.empty_cache()
@@ -189,6 +196,8 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
         "tokens_per_s": wl.tokens / (ms * 1e-3),
         "GBps": 2 * P / (ms * 1e-3) / 1e9,
         "frac_hbm_peak": 2 * P / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "plain_scatter_ms": copy_ms,
+        "plain_scatter_GBps": 2 * P / (copy_ms * 1e-3) / 1e9,
     }
 
 
@@ -291,7 +300,8 @@ def main() -> int:
                 "workload": workloads.CONFIG_NAMES[c],
                 "tokens_per_s": round(r["tokens_per_s"]),
                 "GBps": round(r["GBps"], 1), "frac": round(r["frac_hbm_peak"], 4),
-                "kernel_ms": round(r["kernel_ms"], 4), "tokens": r["tokens"]}
+                "kernel_ms": round(r["kernel_ms"], 4), "tokens": r["tokens"],
+                "same_pages_plain_scatter_GBps": round(r["plain_scatter_GBps"], 1)}
     if 4 in res:
         r = res[4]
         out["fp8_cfg4"] = {"gather_GBps": round(r["gather_GBps"], 1),

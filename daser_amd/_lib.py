@@ -16,7 +16,9 @@ import threading
 
 import torch  # noqa: F401  (must precede loading the HIP library)
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so")
+LIB_PATH = os.environ.get("DASER_KV_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so"
+)
 
 DSR_ABI_VERSION = 1
 DSR_OK = 0

@@ -34,7 +34,13 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;     // 4 wave64 per workgroup
 constexpr int kGatherUnroll = 16;  // 16-byte vectors per lane per half per round
 constexpr int kScatterUnroll = 8;
-constexpr int kRotUnroll = 4;      // rotation tasks per lane per round
+constexpr int kRotUnroll = 4;      // rotation tasks per lane per round (pair-task kernel)
+// Re-rotation runs fastest with two workgroups per CU (measured 5.54 TB/s
+// vs 5.31 TB/s at the register-limited 4 per CU, Llama-3-8B shape): the
+// rotation leaves each workgroup without loads in flight between its read
+// and write phases, and fewer, fuller workgroups per CU keep HBM busier.
+// The cap is applied with dynamic LDS sized from the CU's LDS capacity.
+constexpr int kRotWgPerCu = 2;
 constexpr int kMaxRotHalf = 512;   // LDS table capacity: rot_dim <= 1024
 constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
 
@@ -278,6 +284,8 @@ struct RotArgs {
   int32_t task_vecs;   // rotation tasks per row
   int32_t tail_vec0;   // first un-rotated vector of a row
   int32_t tasks_per_row;
+  int32_t rot_vecs;   // 16-byte vectors of a row inside the rotated region
+  int32_t half_vecs;  // neox: vectors from a first-half vector to its partner
   const float* k_scale;
 };
 
@@ -285,28 +293,30 @@ struct RotArgs {
 // neox task c: vector c of the first half and its partner at +rot_half;
 // gptj task c: vector c, whose VE/2 adjacent pairs rotate in place;
 // tail task: one un-rotated 16-byte vector, copied.
+// K-page rotation in rounds of kRotUnroll tasks per lane. Task t covers row
+// t / tasks_per_row, column c = t % tasks_per_row:
+//   neox, c < task_vecs: vector c of the rotated first half and its partner
+//                        at +rot_half elements;
+//   gptj, c < task_vecs: vector c, whose VE/2 adjacent pairs rotate in place;
+//   c >= task_vecs:      one un-rotated 16-byte tail vector, copied.
 template <int DT, int STYLE>
-__device__ __forceinline__ void rotate_k_page(const RotArgs& ra,
-                                              const uint8_t* src, uint8_t* dst,
-                                              const float2* tab, float scale,
-                                              float inv_scale) {
-  using C = Codec<DT>;
-  constexpr int VE = C::VE;
-  const rsrc_t rs = make_rsrc(src, ra.u.page_bytes);
-  const rsrc_t rd = make_rsrc(dst, ra.u.page_bytes);
-  const int row_bytes = ra.row_vecs << 4;
-  const int rows = (int)(ra.u.page_bytes / row_bytes);
-  const int ntask = rows * ra.tasks_per_row;
-  const int half_off = ra.rot_half * 16 / VE;  // bytes to the neox partner
-  for (int base = threadIdx.x; base < ntask; base += kThreads * kRotUnroll) {
-    u32x4 a[kRotUnroll], b[kRotUnroll];
-    int off[kRotUnroll];
-    int kind[kRotUnroll];  // 0 = rotate, 1 = copy, -1 = none
-    int c_of[kRotUnroll];
+struct KRound {
+  static constexpr int VE = Codec<DT>::VE;
+  u32x4 a[kRotUnroll], b[kRotUnroll];
+  int off[kRotUnroll];
+  int kind[kRotUnroll];  // 0 = rotate, 1 = copy, -1 = none
+  int c_of[kRotUnroll];
+
+  __device__ __forceinline__ void load(const RotArgs& ra, rsrc_t rs, int base, int ntask,
+                                       int row_bytes, int half_off) {
 #pragma unroll
     for (int k = 0; k < kRotUnroll; ++k) {
       const int t = base + k * kThreads;
       kind[k] = -1;
+      off[k] = 0;
+      c_of[k] = 0;
+      a[k] = u32x4{0u, 0u, 0u, 0u};
+      b[k] = a[k];
       if (t < ntask) {
         const int row = t / ra.tasks_per_row;
         const int c = t - row * ra.tasks_per_row;
@@ -323,6 +333,12 @@ __device__ __forceinline__ void rotate_k_page(const RotArgs& ra,
         }
       }
     }
+  }
+
+  __device__ __forceinline__ void store(rsrc_t rd, const float2* tab, int half_off,
+                                        float scale, float inv_scale) {
+    using C = Codec<DT>;
+    constexpr bool kScaled = DT == DSR_DTYPE_FP8_E4M3;
 #pragma unroll
     for (int k = 0; k < kRotUnroll; ++k) {
       if (kind[k] == 1) {
@@ -337,9 +353,12 @@ __device__ __forceinline__ void rotate_k_page(const RotArgs& ra,
 #pragma unroll
           for (int e = 0; e < VE; ++e) {
             const float2 cs = tab[j0 + e];
-            const float x1 = x[e] * scale, x2 = z[e] * scale;
-            x[e] = (x1 * cs.x - x2 * cs.y) * inv_scale;
-            z[e] = (x2 * cs.x + x1 * cs.y) * inv_scale;
+            const float x1 = kScaled ? x[e] * scale : x[e];
+            const float x2 = kScaled ? z[e] * scale : z[e];
+            const float y1 = x1 * cs.x - x2 * cs.y;
+            const float y2 = x2 * cs.x + x1 * cs.y;
+            x[e] = kScaled ? y1 * inv_scale : y1;
+            z[e] = kScaled ? y2 * inv_scale : y2;
           }
           bstore(rd, off[k], C::encode(x));
           bstore(rd, off[k] + half_off, C::encode(z));
@@ -348,41 +367,45 @@ __device__ __forceinline__ void rotate_k_page(const RotArgs& ra,
 #pragma unroll
           for (int e = 0; e < VE / 2; ++e) {
             const float2 cs = tab[j0 + e];
-            const float x1 = x[2 * e] * scale, x2 = x[2 * e + 1] * scale;
-            x[2 * e] = (x1 * cs.x - x2 * cs.y) * inv_scale;
-            x[2 * e + 1] = (x2 * cs.x + x1 * cs.y) * inv_scale;
+            const float x1 = kScaled ? x[2 * e] * scale : x[2 * e];
+            const float x2 = kScaled ? x[2 * e + 1] * scale : x[2 * e + 1];
+            const float y1 = x1 * cs.x - x2 * cs.y;
+            const float y2 = x2 * cs.x + x1 * cs.y;
+            x[2 * e] = kScaled ? y1 * inv_scale : y1;
+            x[2 * e + 1] = kScaled ? y2 * inv_scale : y2;
           }
           bstore(rd, off[k], C::encode(x));
         }
       }
     }
   }
-}
+};
 
-// Copies one page_bytes run, all U loads of a round before its stores.
+// One page_bytes run copied in rounds of U vectors per lane.
 template <int U>
-__device__ __forceinline__ void copy_run(const uint8_t* src, uint8_t* dst,
-                                         int64_t page_bytes) {
-  const rsrc_t rs = make_rsrc(src, page_bytes), rd = make_rsrc(dst, page_bytes);
-  const int nvec = (int)(page_bytes >> 4);
-  for (int base = threadIdx.x; base < nvec; base += kThreads * U) {
-    u32x4 r[U];
+struct VRound {
+  u32x4 r[U];
+  __device__ __forceinline__ void load(rsrc_t rs, int base, int nvec) {
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int i = base + k * kThreads;
-      if (i < nvec) r[k] = bload(rs, i << 4);
+      r[k] = i < nvec ? bload(rs, i << 4) : u32x4{0u, 0u, 0u, 0u};
     }
+  }
+  __device__ __forceinline__ void store(rsrc_t rd, int base, int nvec) {
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int i = base + k * kThreads;
       if (i < nvec) bstore(rd, i << 4, r[k]);
     }
   }
-}
+};
 
 // One workgroup per (page, layer) unit in page-list order. V, and K of pages
 // without a table (rope_idx < 0), are copied bit-exactly; K of the others is
-// re-rotated row by row with the page's (cos, sin) table staged in LDS.
+// re-rotated row by row with the page's (cos, sin) table staged in LDS. The
+// first round of V and K loads is issued before the table is fetched and the
+// workgroup synchronises, so the table latency overlaps the page reads.
 template <int DT, int STYLE>
 __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs ra) {
   __shared__ float2 tab[kMaxRotHalf];
@@ -396,6 +419,18 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
     copy_halves<kScatterUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
     return;
   }
+  const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
+  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const int nvec = (int)(pb >> 4);
+  const int row_bytes = ra.row_vecs << 4;
+  const int ntask = (int)(pb / row_bytes) * ra.tasks_per_row;
+  const int half_off = ra.rot_half * 16 / Codec<DT>::VE;
+
+  VRound<kScatterUnroll> v;
+  KRound<DT, STYLE> k;
+  v.load(vs, threadIdx.x, nvec);
+  k.load(ra, ks, threadIdx.x, ntask, row_bytes, half_off);
+
   const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
   for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
   float scale = 1.0f, inv_scale = 1.0f;
@@ -404,8 +439,128 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
     inv_scale = 1.0f / scale;
   }
   __syncthreads();
-  copy_run<kScatterUnroll>(rec + pb, cache + ra.u.kv_stride, pb);
-  rotate_k_page<DT, STYLE>(ra, rec, cache, tab, scale, inv_scale);
+
+  v.store(vd, threadIdx.x, nvec);
+  k.store(kd, tab, half_off, scale, inv_scale);
+  for (int base = threadIdx.x + kThreads * kScatterUnroll; base < nvec;
+       base += kThreads * kScatterUnroll) {
+    v.load(vs, base, nvec);
+    v.store(vd, base, nvec);
+  }
+  for (int base = threadIdx.x + kThreads * kRotUnroll; base < ntask;
+       base += kThreads * kRotUnroll) {
+    k.load(ra, ks, base, ntask, row_bytes, half_off);
+    k.store(kd, tab, half_off, scale, inv_scale);
+  }
+}
+
+// Contiguous variant: lane-consecutive 16-byte vectors over the whole K page
+// (every load instruction of a wave covers 1 KiB of contiguous page), with
+// the neox partner vector fetched from lane ^ half_vecs by a cross-lane
+// shuffle. Valid when half_vecs is a power of two <= 32 dividing the row
+// evenly (rows then start on 2*half_vecs lane boundaries), and always for
+// gptj, whose pairs sit inside one vector.
+template <int DT, int STYLE, int U>
+__device__ __forceinline__ void rotate_contig_round(const RotArgs& ra, VRound<U>& kk,
+                                                    int base, int nvec, rsrc_t kd,
+                                                    const float2* tab, float scale,
+                                                    float inv_scale) {
+  using C = Codec<DT>;
+  constexpr int VE = C::VE;
+  constexpr bool kScaled = DT == DSR_DTYPE_FP8_E4M3;
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const int i = base + k * kThreads;
+    u32x4 q = kk.r[k];
+    if (STYLE == DSR_ROPE_NEOX) {  // whole wave takes part in the shuffle
+#pragma unroll
+      for (int w = 0; w < 4; ++w) q[w] = (unsigned)__shfl_xor((int)kk.r[k][w], ra.half_vecs);
+    }
+    if (i >= nvec) continue;
+    const int c = i % ra.row_vecs;
+    if (c >= ra.rot_vecs) {
+      bstore(kd, i << 4, kk.r[k]);
+      continue;
+    }
+    float x[VE];
+    C::decode(kk.r[k], x);
+    if (STYLE == DSR_ROPE_NEOX) {
+      float z[VE];
+      C::decode(q, z);
+      const bool first = c < ra.half_vecs;
+      const int j0 = (first ? c : c - ra.half_vecs) * VE;
+      const float sg = first ? -1.0f : 1.0f;
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        const float2 cs = tab[j0 + e];
+        const float xo = kScaled ? x[e] * scale : x[e];
+        const float xp = kScaled ? z[e] * scale : z[e];
+        // first half: x c - p s; second half: x c + p s
+        const float y = xo * cs.x + sg * (xp * cs.y);
+        x[e] = kScaled ? y * inv_scale : y;
+      }
+    } else {
+      const int j0 = c * (VE / 2);
+#pragma unroll
+      for (int e = 0; e < VE / 2; ++e) {
+        const float2 cs = tab[j0 + e];
+        const float x1 = kScaled ? x[2 * e] * scale : x[2 * e];
+        const float x2 = kScaled ? x[2 * e + 1] * scale : x[2 * e + 1];
+        const float y1 = x1 * cs.x - x2 * cs.y;
+        const float y2 = x2 * cs.x + x1 * cs.y;
+        x[2 * e] = kScaled ? y1 * inv_scale : y1;
+        x[2 * e + 1] = kScaled ? y2 * inv_scale : y2;
+      }
+    }
+    bstore(kd, i << 4, C::encode(x));
+  }
+}
+
+// K and V vectors per lane per round: one round covers a 32 KiB bf16 or a
+// 16 KiB e4m3 Llama page.
+template <int DT>
+constexpr int rot_contig_unroll() {
+  return DT == DSR_DTYPE_FP8_E4M3 ? 4 : 8;
+}
+
+template <int DT, int STYLE>
+__global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(RotArgs ra) {
+  __shared__ float2 tab[kMaxRotHalf];
+  uint8_t *cache, *rec;
+  int l;
+  if (!unit_addresses(ra.u, blockIdx.x, &cache, &rec, &l)) return;
+  const int64_t p = (int64_t)blockIdx.x / ra.u.n_layers;
+  const int ti = ra.rope_idx[p];
+  const int64_t pb = ra.u.page_bytes;
+  if (ti < 0 || ti >= ra.n_tables) {
+    copy_halves<kScatterUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    return;
+  }
+  constexpr int U = rot_contig_unroll<DT>();
+  const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
+  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const int nvec = (int)(pb >> 4);
+  VRound<U> v, kk;
+  v.load(vs, threadIdx.x, nvec);
+  kk.load(ks, threadIdx.x, nvec);
+  const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
+  for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
+  float scale = 1.0f, inv_scale = 1.0f;
+  if (DT == DSR_DTYPE_FP8_E4M3) {
+    scale = ra.k_scale[ra.u.layer0 + l];
+    inv_scale = 1.0f / scale;
+  }
+  __syncthreads();
+  const int rounds = (nvec + kThreads * U - 1) / (kThreads * U);
+  for (int r = 0; r < rounds; ++r) {  // uniform trip count: shuffles stay converged
+    const int base = r * kThreads * U + threadIdx.x;
+    if (r > 0) {
+      v.load(vs, base, nvec);
+      kk.load(ks, base, nvec);
+    }
+    v.store(vd, base, nvec);
+    rotate_contig_round<DT, STYLE, U>(ra, kk, base, nvec, kd, tab, scale, inv_scale);
+  }
 }
 
 bool aligned16(int64_t v) { return (v & 15) == 0; }
@@ -452,12 +607,32 @@ UnitArgs make_unit(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   return a;
 }
 
+// Dynamic LDS that limits the re-rotation kernel to kRotWgPerCu workgroups
+// per CU on the current device (0 if the capacity cannot be read).
+size_t rot_occupancy_lds() {
+  int dev = 0, lds = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                            dev) != hipSuccess || lds <= 0)
+    return 0;
+  const int64_t want = (int64_t)lds / kRotWgPerCu - (int64_t)sizeof(float2) * kMaxRotHalf;
+  return want > 0 ? (size_t)want : 0;
+}
+
 template <int DT>
 int launch_rerotate(const RotArgs& ra, int style, unsigned grid, hipStream_t s) {
-  if (style == DSR_ROPE_NEOX)
-    kv_scatter_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, 0, s>>>(ra);
-  else
-    kv_scatter_rerotate_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, 0, s>>>(ra);
+  const int h = ra.half_vecs;
+  const size_t dyn = rot_occupancy_lds();
+  const bool contig = style == DSR_ROPE_GPTJ ||
+                      (h > 0 && h <= 32 && (h & (h - 1)) == 0 && ra.row_vecs % (2 * h) == 0);
+  if (contig) {
+    if (style == DSR_ROPE_NEOX)
+      kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(ra);
+    else
+      kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(ra);
+  } else {
+    kv_scatter_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(ra);
+  }
   return (int)hipGetLastError();
 }
 
@@ -576,6 +751,8 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
   ra.task_vecs = task_vecs;
   ra.tail_vec0 = rot_dim * esize / 16;
   ra.tasks_per_row = task_vecs + (head_dim - rot_dim) * esize / 16;
+  ra.rot_vecs = rot_dim * esize / 16;
+  ra.half_vecs = rope_style == DSR_ROPE_NEOX ? rot_dim / 2 * esize / 16 : 0;
   ra.k_scale = k_scale;
   const unsigned grid = (unsigned)ra.u.n_units;
   hipStream_t s = (hipStream_t)stream;

@@ -203,6 +203,10 @@ def _rerotate_case(gpu, dt, style, head_dim, rot_dim, heads=4, layers=3, seed=0,
         ("fp16", "gptj", 256, 128),
         ("e4m3", "neox", 128, 128),
         ("e4m3", "gptj", 128, 96),
+        # partner distance not a power of two: the pair-task kernel
+        ("bf16", "neox", 80, 80),
+        ("fp16", "neox", 96, 96),
+        ("e4m3", "neox", 192, 192),
     ],
 )
 def test_rerotate_matches_oracle(gpu, dt, style, head_dim, rot_dim):
