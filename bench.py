@@ -201,6 +201,20 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
     }
 
 
+def pmc_traffic(kernel: str, config: int, pages: int):
+    """HBM bytes per launch recorded from rocprofv3 PMC runs of this same
+    workload (profiles/pmc_traffic.txt), or None if not recorded."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.split()
+        if len(f) == 8 and not line.startswith("#") and f[0] == kernel \
+                and int(f[1]) == config and int(f[2]) == pages:
+            return int(f[7])
+    return None
+
+
 def cpu_baseline(budget_s: float = 12.0) -> dict:
     """C oracle (single thread) gather+scatter on a sample of config 2's
     shape: 256 pages of a 1024-block host pool, repeated to ~budget_s."""
@@ -239,6 +253,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--configs", default="2,3")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run a plain 4 GiB device copy (the reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the KV path shards per rank with no "
@@ -253,6 +270,16 @@ def main() -> int:
     torch.cuda.set_device(dev)
     configs = [int(c) for c in args.configs.split(",") if c]
     res = {}
+    if args.calibrate:
+        n = 4 << 30
+        a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(2):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+        torch.cuda.empty_cache()
+        log(f"[bench] calibration: 2 plain copies of {n} bytes")
     for c in configs:
         log(f"[bench] config {c}: {workloads.CONFIG_NAMES[c]}")
         wl = workloads.config(c)
@@ -280,11 +307,13 @@ def main() -> int:
         })
         dom = "gather" if r["gather_ms"] >= r["scatter_ms"] else "scatter"
         achieved = r[f"{dom}_GBps"]
+        kname = f"kv_{dom}_kernel"
         out["roofline"] = {
-            "kernel": f"kv_page_copy_kernel<{'true' if dom == 'gather' else 'false'}> ({dom})",
+            "kernel": kname,
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic(kname, 2, r["pages"]),
+            "algorithmic_bytes": 2 * r["payload_bytes"],
         }
         out["kernels"] = {
             "gather": {"ms": round(r["gather_ms"], 4), "GBps": round(r["gather_GBps"], 1),
@@ -301,7 +330,9 @@ def main() -> int:
                 "tokens_per_s": round(r["tokens_per_s"]),
                 "GBps": round(r["GBps"], 1), "frac": round(r["frac_hbm_peak"], 4),
                 "kernel_ms": round(r["kernel_ms"], 4), "tokens": r["tokens"],
-                "same_pages_plain_scatter_GBps": round(r["plain_scatter_GBps"], 1)}
+                "same_pages_plain_scatter_GBps": round(r["plain_scatter_GBps"], 1),
+                "traffic": pmc_traffic("kv_scatter_rerotate_contig_kernel", c, r["pages"]),
+                "algorithmic_bytes": 2 * r["payload_bytes"]}
     if 4 in res:
         r = res[4]
         out["fp8_cfg4"] = {"gather_GBps": round(r["gather_GBps"], 1),
