@@ -1,0 +1,520 @@
+"""DaseR's vLLM connector (``KVConnectorBase_V1``) on the MI355X data path.
+
+Same class name, constructor, hooks and metadata types as the reference
+(daser/connector/daser_connector.py:60-711); the worker hooks run the HIP
+kernels of libdaser_kv instead of per-(request, block, layer) torch copies:
+
+  save_kv_layer   one gather launch per layer over every store request
+                  (reference :574-632: 2 copies per block per layer);
+  wait_for_save   device -> pinned ring -> store file, one transfer per
+                  request, then commit_chunk (reference :634-684);
+  start_load_kv   store file -> pinned ring -> device staging, then one
+                  scatter launch for every load request, re-rotating K of
+                  chunks whose position changed (reference :455-558, which
+                  has no re-rotation).
+
+Additions, all optional and defaulted so that reference metadata still
+works: ``ReqLoadSpec.pos_offset`` (position the chunk was stored at,
+``ChunkMeta.pos_offset``), ``ReqLoadSpec.new_pos`` (position of its first
+token in this request) and ``ReqLoadSpec.segments`` (several cached chunks
+assembled into one request, each with its own positions).
+
+Extra ``kv_connector_extra_config`` keys: ``rope_theta`` (default 10000),
+``rope_style`` ("neox" | "gptj"), ``rotary_dim`` (default head_dim),
+``save_mode`` ("per_layer" | "deferred": one all-layer gather in
+wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry).
+"""
+
+from __future__ import annotations
+
+import array
+import asyncio
+import logging
+import math
+import threading
+from dataclasses import dataclass, field
+from typing import Any, Optional, Sequence
+
+import numpy as np
+import torch
+
+try:  # vLLM's base classes when vLLM is installed
+    from vllm.distributed.kv_transfer.kv_connector.v1.base import (  # type: ignore
+        KVConnectorBase_V1,
+        KVConnectorMetadata,
+        KVConnectorRole,
+    )
+except ImportError:  # pragma: no cover - exercised where vLLM is absent
+    from daser_amd._vllm_base import KVConnectorBase_V1, KVConnectorMetadata, KVConnectorRole
+
+logger = logging.getLogger("daser_amd.connector")
+
+
+def hash_tokens(tokens: list[int]) -> str:
+    """xxh3_128 hex of the int32 token array (reference :41-57)."""
+    import xxhash
+
+    return xxhash.xxh3_128(bytes(array.array("i", tokens))).hexdigest()
+
+
+# ---------------------------------------------------------------------------
+# metadata (reference :60-112, plus optional position fields)
+
+
+@dataclass
+class LoadSegment:
+    """One cached chunk inside a load: ``num_slots`` records starting at
+    store slot ``start_slot``, landing in ``block_ids[block_offset:
+    block_offset + num_slots]``, stored at position ``pos_offset`` and
+    placed at ``new_pos`` (None = as stored)."""
+
+    start_slot: int
+    num_slots: int
+    block_offset: int
+    pos_offset: int = 0
+    new_pos: Optional[int] = None
+
+
+@dataclass
+class ReqLoadSpec:
+    chunk_key: str
+    start_slot: int
+    num_slots: int
+    block_ids: list[int]
+    file_offset: int
+    token_count: int
+    pos_offset: int = 0
+    new_pos: Optional[int] = None
+    segments: list[LoadSegment] = field(default_factory=list)
+
+    def resolved_segments(self) -> list[LoadSegment]:
+        if self.segments:
+            return self.segments
+        return [LoadSegment(self.start_slot, len(self.block_ids), 0, self.pos_offset,
+                            self.new_pos)]
+
+
+@dataclass
+class ReqStoreSpec:
+    chunk_key: str
+    start_slot: int
+    num_slots: int
+    block_ids: list[int]
+    file_offset: int
+    token_count: int
+
+
+@dataclass
+class DaserConnectorMeta(KVConnectorMetadata):
+    reqs_to_load: dict[str, ReqLoadSpec] = field(default_factory=dict)
+    reqs_to_store: dict[str, ReqStoreSpec] = field(default_factory=dict)
+
+
+# ---------------------------------------------------------------------------
+# planning (host side, no device work): which pages move where
+
+
+@dataclass
+class StorePlan:
+    """Pages of every store request packed back to back in one arena."""
+
+    page_ids: np.ndarray  # int32 block ids
+    slot_offsets: np.ndarray  # int64 record offsets in the arena
+    transfers: list[tuple[str, int, int, int]]  # (chunk_key, arena_off, nbytes, file_off)
+    arena_bytes: int
+
+
+@dataclass
+class LoadPlan:
+    """Records read into one arena, then scattered into pages."""
+
+    page_ids: np.ndarray
+    src_offsets: np.ndarray
+    rope_idx: np.ndarray  # int32, -1 = no rotation
+    deltas: list[int]  # table order
+    reads: list[tuple[int, int, int]]  # (arena_off, nbytes, file_off)
+    arena_bytes: int
+
+
+def plan_store(reqs: dict[str, ReqStoreSpec], slot_bytes: int) -> StorePlan:
+    """Record of request r's slot i at arena_r + i * SLOT, written to the file
+    at start_slot * SLOT (reference :616-632, :652)."""
+    ids, offs, transfers = [], [], []
+    base = 0
+    for spec in reqs.values():
+        n = len(spec.block_ids)
+        if n == 0:
+            continue
+        ids.extend(spec.block_ids)
+        offs.extend(base + i * slot_bytes for i in range(n))
+        transfers.append((spec.chunk_key, base, n * slot_bytes, spec.start_slot * slot_bytes))
+        base += n * slot_bytes
+    return StorePlan(np.asarray(ids, np.int32), np.asarray(offs, np.int64), transfers, base)
+
+
+def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
+    """Each segment's records are read once into the arena; page j of a
+    segment scatters record j into block_ids[block_offset + j]. A segment
+    whose new position differs from its stored one gets a rotation table for
+    delta = new_pos - pos_offset (reference :498-551 for the unrotated part)."""
+    ids, offs, ridx, reads = [], [], [], []
+    table: dict[int, int] = {}
+    base = 0
+    for spec in reqs.values():
+        blocks = spec.block_ids
+        if not blocks:
+            continue
+        for seg in spec.resolved_segments():
+            n = seg.num_slots
+            if n <= 0:
+                continue
+            if seg.block_offset < 0 or seg.block_offset + n > len(blocks):
+                raise ValueError(f"segment of {spec.chunk_key[:8]} exceeds its block list")
+            reads.append((base, n * slot_bytes, seg.start_slot * slot_bytes))
+            delta = 0 if seg.new_pos is None else int(seg.new_pos) - int(seg.pos_offset)
+            t = -1 if delta == 0 else table.setdefault(delta, len(table))
+            for j in range(n):
+                ids.append(blocks[seg.block_offset + j])
+                offs.append(base + j * slot_bytes)
+                ridx.append(t)
+            base += n * slot_bytes
+    return LoadPlan(np.asarray(ids, np.int32), np.asarray(offs, np.int64),
+                    np.asarray(ridx, np.int32), list(table.keys()), reads, base)
+
+
+# ---------------------------------------------------------------------------
+# worker data plane
+
+
+class KVDataPlane:
+    """Worker-side movement of KV pages between vLLM's caches and the store.
+
+    Owns the layer table of the registered caches, the per-step staging
+    arenas and the store I/O; every device operation is enqueued on torch's
+    current stream of the caches' device.
+    """
+
+    def __init__(self, store_path: str, *, rope_theta: float = 10000.0,
+                 rope_style: str = "neox", rotary_dim: Optional[int] = None,
+                 inv_freq: Optional[np.ndarray] = None, save_mode: str = "per_layer",
+                 io_slot_bytes: int = 64 << 20, io_slots: int = 4,
+                 k_scales: Optional[torch.Tensor] = None) -> None:
+        if save_mode not in ("per_layer", "deferred"):
+            raise ValueError("save_mode must be 'per_layer' or 'deferred'")
+        self.store_path = store_path
+        self.rope_theta = float(rope_theta)
+        self.rope_style = rope_style
+        self.rotary_dim = rotary_dim
+        self.inv_freq = inv_freq
+        self.save_mode = save_mode
+        self._io_slot_bytes = io_slot_bytes
+        self._io_slots = io_slots
+        self.k_scales = k_scales
+        self.table = None
+        self.layer_names: list[str] = []
+        self.layer_idx: dict[str, int] = {}
+        self.slot_bytes = 0
+        self.io = None
+
+    # -- registration (reference register_kv_caches :383-429)
+    def register(self, kv_caches: dict[str, torch.Tensor], slot_size: int = 0) -> int:
+        from daser_amd import ops
+        from daser_amd.store_io import PinnedRingIO, preallocate_store
+
+        self.layer_names = list(kv_caches.keys())
+        self.layer_idx = {n: i for i, n in enumerate(self.layer_names)}
+        self.table = ops.LayerTable([kv_caches[n] for n in self.layer_names])
+        lay = self.table.layout
+        derived = lay.slot_bytes
+        if slot_size and slot_size != derived:
+            raise ValueError(f"configured slot_size {slot_size} != derived {derived}")
+        self.slot_bytes = derived
+        if self.rotary_dim is None:
+            self.rotary_dim = lay.head_dim
+        preallocate_store(self.store_path, max(self.slot_bytes * 1024, 64 << 20))
+        if self.io is None:
+            self.io = PinnedRingIO(self.store_path, lay.device,
+                                   slot_bytes=self._io_slot_bytes, n_slots=self._io_slots)
+        return self.slot_bytes
+
+    @property
+    def device(self) -> torch.device:
+        return self.table.layout.device
+
+    # -- save
+    def new_store_arena(self, plan: StorePlan) -> torch.Tensor:
+        return torch.empty(max(plan.arena_bytes, 16), dtype=torch.uint8, device=self.device)
+
+    def save_layer(self, layer_name: str, plan: StorePlan, arena: torch.Tensor) -> None:
+        from daser_amd import ops
+
+        if plan.page_ids.size == 0:
+            return
+        l = self.layer_idx[layer_name]
+        ops.gather(self.table, plan.page_ids, plan.slot_offsets, arena, layers=(l, 1))
+
+    def save_all(self, plan: StorePlan, arena: torch.Tensor) -> None:
+        from daser_amd import ops
+
+        if plan.page_ids.size:
+            ops.gather(self.table, plan.page_ids, plan.slot_offsets, arena)
+
+    def flush(self, plan: StorePlan, arena: torch.Tensor) -> list[str]:
+        """Writes each request's records at its file offset; returns the
+        chunk keys written (to commit)."""
+        keys = []
+        for key, off, nbytes, file_off in plan.transfers:
+            self.io.write_from_device(arena[off:off + nbytes], file_off)
+            keys.append(key)
+        return keys
+
+    # -- load
+    def load(self, plan: LoadPlan) -> None:
+        from daser_amd import ops, position
+
+        if plan.page_ids.size == 0:
+            return
+        arena = torch.empty(plan.arena_bytes, dtype=torch.uint8, device=self.device)
+        for off, nbytes, file_off in plan.reads:
+            self.io.read_into_device(arena[off:off + nbytes], file_off)
+        if not plan.deltas:
+            ops.scatter(self.table, plan.page_ids, plan.src_offsets, arena)
+            return
+        tabs = position.delta_tables(plan.deltas, self.rotary_dim, self.rope_theta,
+                                     inv_freq=self.inv_freq, device=self.device)
+        ops.scatter_rerotate(self.table, plan.page_ids, plan.src_offsets, arena, tabs,
+                             plan.rope_idx, rot_dim=self.rotary_dim, style=self.rope_style,
+                             k_scale=self.k_scales)
+
+    def close(self) -> None:
+        if self.io is not None:
+            self.io.close()
+            self.io = None
+
+
+# ---------------------------------------------------------------------------
+# the connector
+
+
+class _BgLoop:
+    """Background asyncio loop for the async IPC client (reference :176-186)."""
+
+    def __init__(self) -> None:
+        self.loop = asyncio.new_event_loop()
+        self.thread = threading.Thread(target=self._run, daemon=True, name="daser-io")
+        self.thread.start()
+
+    def _run(self) -> None:
+        asyncio.set_event_loop(self.loop)
+        self.loop.run_forever()
+
+    def run(self, coro, timeout: Optional[float] = None):
+        return asyncio.run_coroutine_threadsafe(coro, self.loop).result(timeout=timeout)
+
+    def stop(self) -> None:
+        self.loop.call_soon_threadsafe(self.loop.stop)
+        self.thread.join(timeout=5)
+
+
+def _default_ipc(kind: str, socket_path: str):
+    """The reference's IPC clients, when its package is importable."""
+    from daser.connector.ipc_client import IPCClientAsync, IPCClientSync  # type: ignore
+
+    return (IPCClientSync if kind == "sync" else IPCClientAsync)(socket_path)
+
+
+class DaserConnector(KVConnectorBase_V1):
+    """vLLM ``KVConnectorBase_V1`` backed by DaseR, MI355X data path.
+
+    ``ipc_client`` (scheduler role) and ``ipc_async`` (worker role) may be
+    injected; by default the reference's IPC clients are used.
+    """
+
+    def __init__(self, vllm_config: Any, role: KVConnectorRole, kv_cache_config: Any = None,
+                 *, ipc_client: Any = None, ipc_async: Any = None) -> None:
+        super().__init__(vllm_config, role, kv_cache_config)
+        extra: dict[str, Any] = {}
+        ktc = getattr(vllm_config, "kv_transfer_config", None)
+        if ktc is not None:
+            extra = getattr(ktc, "kv_connector_extra_config", None) or {}
+        self._socket_path: str = extra.get("socket_path", "/tmp/daser.sock")
+        self._store_path: str = extra.get("store_path", "/tmp/daser/daser.store")
+        self._slot_size: int = int(extra.get("slot_size", 0))
+        self._block_tokens: int = int(extra.get("block_tokens", 16))
+        self._model_id: str = extra.get("model_id", "default")
+        self._role_kind = role
+        if role == KVConnectorRole.SCHEDULER:
+            self._ipc_sync = ipc_client if ipc_client is not None else _default_ipc(
+                "sync", self._socket_path)
+            self._pending_loads: dict[str, dict[str, Any]] = {}
+            self._pending_stores: dict[str, dict[str, Any]] = {}
+            self._pending_alloc: dict[str, dict[str, Any]] = {}
+            self._req_tokens: dict[str, list[int]] = {}
+        else:
+            self._ipc_async = ipc_async if ipc_async is not None else _default_ipc(
+                "async", self._socket_path)
+            self._plane = KVDataPlane(
+                self._store_path,
+                rope_theta=float(extra.get("rope_theta", 10000.0)),
+                rope_style=extra.get("rope_style", "neox"),
+                rotary_dim=extra.get("rotary_dim"),
+                save_mode=extra.get("save_mode", "per_layer"),
+                io_slot_bytes=int(float(extra.get("io_slot_mb", 64)) * (1 << 20)),
+                io_slots=int(extra.get("io_slots", 4)),
+            )
+            self._meta: Optional[DaserConnectorMeta] = None
+            self._store_plan: Optional[StorePlan] = None
+            self._store_arena: Optional[torch.Tensor] = None
+            self._saved_layers: set[int] = set()
+            self._pending_commits: set[str] = set()
+            self._bg = _BgLoop()
+
+    # ------------------------------------------------------------ scheduler
+    def get_num_new_matched_tokens(self, request: Any, num_computed_tokens: int):
+        """Reference :194-258 (match_and_alloc in one RPC), unchanged."""
+        tokens = list(request.prompt_token_ids)
+        self._req_tokens[request.request_id] = tokens
+        available = len(tokens) - num_computed_tokens
+        if available < self._block_tokens:
+            return 0, False
+        aligned = (available // self._block_tokens) * self._block_tokens
+        prefix = tokens[: num_computed_tokens + aligned]
+        full_aligned = (len(tokens) // self._block_tokens) * self._block_tokens
+        store_key = hash_tokens(tokens[:full_aligned]) if full_aligned > 0 else ""
+        try:
+            resp = self._ipc_sync.match_and_alloc(prefix, store_key, self._model_id)
+        except Exception as exc:  # a failed lookup degrades to a miss
+            logger.warning("[CONNECTOR] match_and_alloc failed: %s", exc)
+            return 0, False
+        chunks = resp.get("chunks", [])
+        alloc = resp.get("alloc")
+        if alloc is not None:
+            self._pending_alloc[request.request_id] = alloc
+        if not chunks:
+            return 0, False
+        best = chunks[0]
+        extra_tokens = best["token_count"] - num_computed_tokens
+        if extra_tokens <= 0:
+            return 0, False
+        self._pending_loads[request.request_id] = best
+        return extra_tokens, False
+
+    def update_state_after_alloc(self, request: Any, blocks: Any, num_external_tokens: int) -> None:
+        """Reference :260-298."""
+        req_id = request.request_id
+        block_ids = [blk.block_id for blk in blocks.blocks[0]]
+        if num_external_tokens > 0 and req_id in self._pending_loads:
+            chunk = self._pending_loads[req_id]
+            chunk["block_ids"] = block_ids[: math.ceil(num_external_tokens / self._block_tokens)]
+        else:
+            alloc = self._pending_alloc.pop(req_id, None)
+            if alloc is None:
+                return
+            alloc["block_ids"] = block_ids[: math.ceil(alloc["token_count"] / self._block_tokens)]
+            self._pending_stores[req_id] = alloc
+
+    def build_connector_meta(self, scheduler_output: Any) -> DaserConnectorMeta:
+        """Reference :300-357; also forwards the chunk's stored position
+        (``pos_offset`` of the lookup reply) and, when the reply names one, the
+        position to place it at (``new_pos``) and its segments."""
+        meta = DaserConnectorMeta()
+        scheduled = set(scheduler_output.num_scheduled_tokens.keys())
+        for req_id, chunk in list(self._pending_loads.items()):
+            if req_id in scheduled and "block_ids" in chunk:
+                segs = [LoadSegment(**s) for s in chunk.get("segments", [])]
+                meta.reqs_to_load[req_id] = ReqLoadSpec(
+                    chunk_key=chunk["chunk_key"], start_slot=chunk["start_slot"],
+                    num_slots=chunk["num_slots"], block_ids=chunk["block_ids"],
+                    file_offset=chunk["file_offset"], token_count=chunk["token_count"],
+                    pos_offset=int(chunk.get("pos_offset", 0)), new_pos=chunk.get("new_pos"),
+                    segments=segs)
+                del self._pending_loads[req_id]
+        for req_id, alloc in list(self._pending_stores.items()):
+            if req_id in scheduled and "block_ids" in alloc:
+                meta.reqs_to_store[req_id] = ReqStoreSpec(
+                    chunk_key=alloc["chunk_key"], start_slot=alloc["start_slot"],
+                    num_slots=alloc["num_slots"], block_ids=alloc["block_ids"],
+                    file_offset=alloc["file_offset"], token_count=alloc["token_count"])
+                del self._pending_stores[req_id]
+        return meta
+
+    def request_finished(self, request: Any, block_ids: list[int]):
+        for d in (self._req_tokens, self._pending_loads, self._pending_stores, self._pending_alloc):
+            d.pop(request.request_id, None)
+        return False, None
+
+    # --------------------------------------------------------------- worker
+    def register_kv_caches(self, kv_caches: dict[str, torch.Tensor]) -> None:
+        self._slot_size = self._plane.register(kv_caches, self._slot_size)
+        logger.info("[CONNECTOR] %d layers, slot_size=%d", len(kv_caches), self._slot_size)
+
+    def bind_connector_metadata(self, connector_metadata: DaserConnectorMeta) -> None:
+        super().bind_connector_metadata(connector_metadata)
+        self._meta = connector_metadata
+        self._store_plan = None
+        self._store_arena = None
+        self._saved_layers = set()
+        self._pending_commits = set()
+
+    def clear_connector_metadata(self) -> None:
+        super().clear_connector_metadata()
+        self._meta = None
+
+    def start_load_kv(self, forward_context: Any, **kwargs: Any) -> None:
+        """Reads every load request's records, then one scatter (with
+        re-rotation where positions moved). All device work is enqueued on
+        the current stream before returning, so it precedes the forward pass
+        (also under full graph replay, which skips per-layer hooks)."""
+        if self._meta is None or not self._meta.reqs_to_load or self._plane.table is None:
+            return
+        plan = plan_load(self._meta.reqs_to_load, self._slot_size)
+        self._plane.load(plan)
+
+    def wait_for_layer_load(self, layer_name: str) -> None:
+        return
+
+    def _ensure_store_plan(self) -> bool:
+        if self._meta is None or not self._meta.reqs_to_store or self._plane.table is None:
+            return False
+        if self._store_plan is None:
+            self._store_plan = plan_store(self._meta.reqs_to_store, self._slot_size)
+            self._store_arena = self._plane.new_store_arena(self._store_plan)
+        return True
+
+    def save_kv_layer(self, layer_name: str, kv_layer: torch.Tensor, attn_metadata: Any,
+                      **kwargs: Any) -> None:
+        """Enqueues this layer's gather for every store request."""
+        if not self._ensure_store_plan():
+            return
+        for spec in self._meta.reqs_to_store.values():
+            self._pending_commits.add(spec.chunk_key)
+        if layer_name not in self._plane.layer_idx:
+            logger.warning("[CONNECTOR] save_kv_layer: unknown layer %s, skipping", layer_name)
+            return
+        if self._plane.save_mode == "per_layer":
+            self._plane.save_layer(layer_name, self._store_plan, self._store_arena)
+        self._saved_layers.add(self._plane.layer_idx[layer_name])
+
+    def wait_for_save(self) -> None:
+        """Writes each request's records to the store, then commits."""
+        if self._store_plan is None or self._store_arena is None:
+            return
+        if self._plane.save_mode == "deferred":
+            self._plane.save_all(self._store_plan, self._store_arena)
+        self._plane.flush(self._store_plan, self._store_arena)
+        self._store_plan = None
+        self._store_arena = None
+        if self._pending_commits:
+            keys = list(self._pending_commits)
+
+            async def _commit_all() -> None:
+                await asyncio.gather(*(self._ipc_async.commit_chunk(k) for k in keys))
+
+            self._bg.run(_commit_all(), timeout=120.0)
+        self._pending_commits.clear()
+
+    def shutdown(self) -> None:
+        if self._role_kind != KVConnectorRole.WORKER:
+            return
+        self._plane.close()
+        self._bg.stop()

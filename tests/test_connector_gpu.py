@@ -1,0 +1,160 @@
+"""Worker hooks end to end on the GPU: save_kv_layer / wait_for_save write
+the reference's record layout to the store file; start_load_kv reads it back
+into other blocks, re-rotating K where the chunk's position changed."""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from daser_amd import connector as C
+from daser_amd.store_io import PinnedRingIO, preallocate_store
+from daser_amd.workloads import KVShape
+from oracle import oracle
+from tests.helpers import rand_caches, to_bits_np
+
+pytestmark = pytest.mark.gpu
+
+SHAPE = KVShape(3, 2, 64, 16, 2)  # SLOT = 3 x 8 KiB
+
+
+class FakeAsyncIPC:
+    def __init__(self):
+        self.committed = []
+
+    async def commit_chunk(self, key):
+        self.committed.append(key)
+        return {"ok": True}
+
+
+def _worker(tmp_path, **extra):
+    cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(kv_connector_extra_config=dict(
+        store_path=str(tmp_path / "daser.store"), io_slot_mb=0.03125, io_slots=3, **extra)))
+    ipc = FakeAsyncIPC()
+    return C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=ipc), ipc
+
+
+def _named(caches):
+    return {f"model.layers.{i}.self_attn.attn": c for i, c in enumerate(caches)}
+
+
+def _save(w, named, reqs):
+    w.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_store=reqs))
+    for name, t in named.items():
+        w.save_kv_layer(name, t, None)
+    w.wait_for_save()
+    w.clear_connector_metadata()
+
+
+def _store_reqs():
+    slot = SHAPE.slot_bytes
+    return {
+        "a": C.ReqStoreSpec("ka", 3, 3, [5, 9, 2], 3 * slot, 40),
+        "b": C.ReqStoreSpec("kb", 10, 1, [7], 10 * slot, 16),
+    }
+
+
+def _file_records(path, start_slot, n):
+    slot = SHAPE.slot_bytes
+    with open(path, "rb") as f:
+        f.seek(start_slot * slot)
+        return np.frombuffer(f.read(n * slot), dtype=np.uint8)
+
+
+@pytest.mark.parametrize("mode", ["per_layer", "deferred"])
+def test_save_writes_reference_layout(gpu, tmp_path, mode):
+    print(f"case: connector save {mode}", flush=True)
+    w, ipc = _worker(tmp_path, save_mode=mode)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=31)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    assert w._slot_size == SHAPE.slot_bytes
+    _save(w, named, _store_reqs())
+    host = [to_bits_np(c, "bf16") for c in caches]
+    for start, blocks in ((3, [5, 9, 2]), (10, [7])):
+        ref = np.zeros(len(blocks) * SHAPE.slot_bytes, dtype=np.uint8)
+        oracle.gather(host, blocks, np.arange(len(blocks)) * SHAPE.slot_bytes, ref,
+                      SHAPE.layer_bytes)
+        assert np.array_equal(_file_records(tmp_path / "daser.store", start, len(blocks)), ref)
+    assert sorted(ipc.committed) == ["ka", "kb"]
+    w.shutdown()
+
+
+def test_load_round_trip_into_other_blocks(gpu, tmp_path):
+    print("case: connector load", flush=True)
+    w, _ = _worker(tmp_path)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=32)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    _save(w, named, _store_reqs())
+    w.shutdown()
+
+    r, _ = _worker(tmp_path)
+    fresh = [torch.zeros_like(c) for c in caches]
+    r.register_kv_caches(_named(fresh))
+    slot = SHAPE.slot_bytes
+    meta = C.DaserConnectorMeta(reqs_to_load={
+        "x": C.ReqLoadSpec("ka", 3, 3, [1, 12, 4], 3 * slot, 40),
+        "y": C.ReqLoadSpec("kb", 10, 1, [0], 10 * slot, 16),
+    })
+    r.bind_connector_metadata(meta)
+    r.start_load_kv(None)
+    torch.cuda.synchronize()
+    for c, f in zip(caches, fresh):
+        assert torch.equal(f[:, [1, 12, 4, 0]], c[:, [5, 9, 2, 7]])
+        untouched = [i for i in range(16) if i not in (1, 12, 4, 0)]
+        assert not f[:, untouched].view(torch.int16).any()
+    r.shutdown()
+
+
+def test_load_with_new_position_rerotates_k(gpu, tmp_path):
+    print("case: connector load rerotate", flush=True)
+    w, _ = _worker(tmp_path, rope_theta=500000.0)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=33)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    _save(w, named, _store_reqs())
+    slot = SHAPE.slot_bytes
+    recs = _file_records(tmp_path / "daser.store", 3, 3).copy()
+
+    fresh = [torch.zeros_like(c) for c in caches]
+    w2, _ = _worker(tmp_path, rope_theta=500000.0)
+    w2.register_kv_caches(_named(fresh))
+    # stored at 100, placed at 4196: delta 4096; second request as stored
+    meta = C.DaserConnectorMeta(reqs_to_load={
+        "x": C.ReqLoadSpec("ka", 3, 3, [1, 12, 4], 3 * slot, 40, pos_offset=100, new_pos=4196),
+        "y": C.ReqLoadSpec("kb", 10, 1, [0], 10 * slot, 16, pos_offset=5, new_pos=5),
+    })
+    w2.bind_connector_metadata(meta)
+    w2.start_load_kv(None)
+    torch.cuda.synchronize()
+    ref = [np.zeros_like(to_bits_np(c, "bf16")) for c in caches]
+    oracle.scatter_rerotate(ref, [1, 12, 4], np.arange(3) * slot, recs, SHAPE.layer_bytes,
+                            dtype=oracle.BF16, rot_dim=64, style=oracle.NEOX,
+                            stored_pos=np.full(3, 100), new_pos=np.full(3, 4196),
+                            rotate=np.ones(3), theta=500000.0)
+    for l, f in enumerate(fresh):
+        got = to_bits_np(f, "bf16")
+        assert np.array_equal(got[1][[1, 12, 4]], ref[l][1][[1, 12, 4]])
+        ok, msg = oracle.rotation_within_tolerance(got[0][[1, 12, 4]], ref[l][0][[1, 12, 4]],
+                                                   oracle.BF16)
+        assert ok, msg
+        assert torch.equal(f[:, 0], caches[l][:, 7])  # unchanged position: bit-exact
+    w.shutdown()
+    w2.shutdown()
+
+
+def test_pinned_ring_device_round_trip(gpu, tmp_path):
+    print("case: pinned ring", flush=True)
+    path = str(tmp_path / "s.store")
+    preallocate_store(path, 8 << 20)
+    src = torch.randint(0, 256, (3_000_000,), dtype=torch.uint8, device=gpu)
+    with PinnedRingIO(path, gpu, slot_bytes=1 << 18, n_slots=3) as io:
+        io.write_from_device(src, 4096)
+        dst = torch.zeros_like(src)
+        io.read_into_device(dst, 4096)
+        torch.cuda.synchronize()
+    assert torch.equal(src, dst)

@@ -1,0 +1,236 @@
+"""Host logic of the connector (no GPU): page planning, the scheduler role
+against a fake IPC client, and the pinned-ring store I/O run on CPU tensors
+(ordering, slow and failing I/O, short reads)."""
+
+from __future__ import annotations
+
+import asyncio
+import os
+import threading
+import time
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from daser_amd import connector as C
+from daser_amd.store_io import PinnedRingIO, StoreIOError, preallocate_store
+
+SLOT = 4096
+
+
+def test_plan_store_layout_matches_reference_offsets():
+    reqs = {
+        "a": C.ReqStoreSpec("ka", start_slot=10, num_slots=3, block_ids=[7, 2, 5],
+                            file_offset=10 * SLOT, token_count=48),
+        "empty": C.ReqStoreSpec("ke", 0, 0, [], 0, 0),
+        "b": C.ReqStoreSpec("kb", start_slot=3, num_slots=1, block_ids=[9],
+                            file_offset=3 * SLOT, token_count=16),
+    }
+    p = C.plan_store(reqs, SLOT)
+    assert p.page_ids.tolist() == [7, 2, 5, 9]
+    assert p.slot_offsets.tolist() == [0, SLOT, 2 * SLOT, 3 * SLOT]
+    # one transfer per request at start_slot * SLOT (reference :652)
+    assert p.transfers == [("ka", 0, 3 * SLOT, 10 * SLOT), ("kb", 3 * SLOT, SLOT, 3 * SLOT)]
+    assert p.arena_bytes == 4 * SLOT
+
+
+def test_plan_load_without_positions_is_plain_scatter():
+    reqs = {"r": C.ReqLoadSpec("k", start_slot=4, num_slots=2, block_ids=[11, 3],
+                               file_offset=4 * SLOT, token_count=20)}
+    p = C.plan_load(reqs, SLOT)
+    assert p.page_ids.tolist() == [11, 3]
+    assert p.src_offsets.tolist() == [0, SLOT]
+    assert p.rope_idx.tolist() == [-1, -1] and p.deltas == []
+    assert p.reads == [(0, 2 * SLOT, 4 * SLOT)]
+
+
+def test_plan_load_positions_and_segments():
+    reqs = {
+        "r1": C.ReqLoadSpec("k1", 0, 2, [1, 2], 0, 32, pos_offset=100, new_pos=612),
+        "r2": C.ReqLoadSpec("k2", 0, 0, [5, 6, 7], 0, 48, segments=[
+            C.LoadSegment(start_slot=20, num_slots=2, block_offset=0, pos_offset=0, new_pos=512),
+            C.LoadSegment(start_slot=8, num_slots=1, block_offset=2, pos_offset=0, new_pos=0),
+        ]),
+        "r3": C.ReqLoadSpec("k3", 0, 1, [9], 0, 16, pos_offset=7, new_pos=7),
+    }
+    p = C.plan_load(reqs, SLOT)
+    assert p.page_ids.tolist() == [1, 2, 5, 6, 7, 9]
+    assert p.deltas == [512]  # 612 - 100 and 512 - 0 share one table
+    assert p.rope_idx.tolist() == [0, 0, 0, 0, -1, -1]
+    assert p.reads == [(0, 2 * SLOT, 0), (2 * SLOT, 2 * SLOT, 20 * SLOT),
+                       (4 * SLOT, SLOT, 8 * SLOT), (5 * SLOT, SLOT, 0)]
+    with pytest.raises(ValueError):
+        C.plan_load({"x": C.ReqLoadSpec("k", 0, 0, [1], 0, 16, segments=[
+            C.LoadSegment(0, 2, 0)])}, SLOT)
+
+
+# ---------------------------------------------------------------- scheduler
+
+
+class FakeIPC:
+    def __init__(self, chunks=None, alloc=None, fail=False):
+        self.chunks, self.alloc, self.fail, self.calls = chunks or [], alloc, fail, []
+
+    def match_and_alloc(self, prefix, store_key, model_id):
+        self.calls.append((list(prefix), store_key, model_id))
+        if self.fail:
+            raise ConnectionError("server down")
+        return {"chunks": self.chunks, "alloc": self.alloc}
+
+
+def _cfg(**extra):
+    return SimpleNamespace(kv_transfer_config=SimpleNamespace(kv_connector_extra_config=extra))
+
+
+def _req(rid, n):
+    return SimpleNamespace(request_id=rid, prompt_token_ids=list(range(n)))
+
+
+def _blocks(ids):
+    return SimpleNamespace(blocks=[[SimpleNamespace(block_id=i) for i in ids]])
+
+
+def test_scheduler_hit_carries_positions():
+    chunk = {"chunk_key": "ck", "start_slot": 5, "num_slots": 3, "file_offset": 5 * SLOT,
+             "token_count": 40, "pos_offset": 0, "new_pos": 1000}
+    ipc = FakeIPC(chunks=[chunk])
+    conn = C.DaserConnector(_cfg(block_tokens=16), C.KVConnectorRole.SCHEDULER, ipc_client=ipc)
+    n, is_async = conn.get_num_new_matched_tokens(_req("r", 50), 0)
+    assert (n, is_async) == (40, False)
+    assert len(ipc.calls[0][0]) == 48  # block-aligned prefix
+    conn.update_state_after_alloc(_req("r", 50), _blocks([8, 1, 4, 6]), 40)
+    meta = conn.build_connector_meta(SimpleNamespace(num_scheduled_tokens={"r": 50}))
+    spec = meta.reqs_to_load["r"]
+    assert spec.block_ids == [8, 1, 4]  # ceil(40 / 16)
+    assert (spec.pos_offset, spec.new_pos) == (0, 1000)
+    assert meta.reqs_to_store == {}
+
+
+def test_scheduler_miss_allocates_store():
+    alloc = {"chunk_key": "new", "start_slot": 2, "num_slots": 2, "file_offset": 2 * SLOT,
+             "token_count": 32}
+    conn = C.DaserConnector(_cfg(), C.KVConnectorRole.SCHEDULER, ipc_client=FakeIPC(alloc=alloc))
+    assert conn.get_num_new_matched_tokens(_req("r", 40), 0) == (0, False)
+    conn.update_state_after_alloc(_req("r", 40), _blocks([3, 9, 4]), 0)
+    meta = conn.build_connector_meta(SimpleNamespace(num_scheduled_tokens={"r": 40}))
+    assert meta.reqs_to_store["r"].block_ids == [3, 9]
+    assert conn.request_finished(_req("r", 40), []) == (False, None)
+
+
+def test_scheduler_ipc_failure_is_a_miss():
+    conn = C.DaserConnector(_cfg(), C.KVConnectorRole.SCHEDULER, ipc_client=FakeIPC(fail=True))
+    assert conn.get_num_new_matched_tokens(_req("r", 64), 0) == (0, False)
+    assert conn.get_num_new_matched_tokens(_req("s", 8), 0) == (0, False)  # < one block
+
+
+def test_hash_tokens_deterministic():
+    assert C.hash_tokens([1, 2, 3]) == C.hash_tokens([1, 2, 3])
+    assert C.hash_tokens([1, 2, 3]) != C.hash_tokens([1, 2, 4])
+    assert len(C.hash_tokens([5])) == 32
+
+
+# ---------------------------------------------------------------- store I/O
+
+
+@pytest.fixture()
+def store(tmp_path):
+    path = str(tmp_path / "daser.store")
+    preallocate_store(path, 1 << 20)
+    return path
+
+
+def test_preallocate_and_missing_file(tmp_path, store):
+    assert os.path.getsize(store) == 1 << 20
+    preallocate_store(store, 5)  # existing file untouched
+    assert os.path.getsize(store) == 1 << 20
+    with pytest.raises(FileNotFoundError):
+        PinnedRingIO(str(tmp_path / "nope"), "cpu")
+
+
+def test_ring_round_trip_more_pieces_than_slots(store):
+    rng = np.random.default_rng(0)
+    src = torch.from_numpy(rng.integers(0, 256, 100_000, dtype=np.uint8))
+    with PinnedRingIO(store, "cpu", slot_bytes=4096, n_slots=3) as io:
+        assert io.write_from_device(src, 12_288) == src.numel()
+        dst = torch.zeros_like(src)
+        assert io.read_into_device(dst, 12_288) == src.numel()
+    assert torch.equal(src, dst)
+    with open(store, "rb") as f:
+        f.seek(12_288)
+        assert f.read(100_000) == src.numpy().tobytes()
+
+
+def test_ring_slow_writer_keeps_order(store):
+    """A writer that stalls must not let a slot be overwritten early."""
+    def hook(kind, off, n):
+        if kind == "write":
+            time.sleep(0.01)
+
+    a = torch.full((40_000,), 1, dtype=torch.uint8)
+    b = torch.full((40_000,), 2, dtype=torch.uint8)
+    with PinnedRingIO(store, "cpu", slot_bytes=4096, n_slots=2, io_hook=hook) as io:
+        io.write_from_device(a, 0)
+        io.write_from_device(b, 40_000)
+        out = torch.zeros(80_000, dtype=torch.uint8)
+        io.read_into_device(out, 0)
+    assert torch.equal(out[:40_000], a) and torch.equal(out[40_000:], b)
+
+
+def test_ring_failed_write_raises(store):
+    def hook(kind, off, n):
+        if kind == "write" and off >= 8192:
+            raise OSError("disk full")
+
+    with PinnedRingIO(store, "cpu", slot_bytes=4096, n_slots=2, io_hook=hook) as io:
+        with pytest.raises(OSError, match="disk full"):
+            io.write_from_device(torch.ones(20_000, dtype=torch.uint8), 0)
+        # the ring stays usable for later transfers below the failing range
+        io._hook = None
+        io.write_from_device(torch.ones(10, dtype=torch.uint8), 0)
+
+
+def test_ring_short_read_raises(store):
+    with PinnedRingIO(store, "cpu", slot_bytes=4096, n_slots=2) as io:
+        with pytest.raises(StoreIOError, match="short read"):
+            io.read_into_device(torch.zeros(8192, dtype=torch.uint8), (1 << 20) - 100)
+
+
+def test_ring_async_api_and_close(store):
+    io = PinnedRingIO(store, "cpu", slot_bytes=1024, n_slots=2)
+    src = torch.arange(5000, dtype=torch.int32)
+
+    async def go():
+        await io.write_async(src, 4096)
+        dst = torch.zeros_like(src)
+        await io.read_into_async(dst, 4096)
+        return dst
+
+    assert torch.equal(asyncio.run(go()), src)
+    io.close()
+    io.close()
+    with pytest.raises(StoreIOError):
+        io.write_from_device(src, 0)
+
+
+def test_ring_concurrent_callers_serialise(store):
+    """Transfers from two threads do not interleave inside the ring."""
+    errs = []
+
+    def work(val, off):
+        try:
+            t = torch.full((30_000,), val, dtype=torch.uint8)
+            for _ in range(5):
+                io.write_from_device(t, off)
+        except Exception as e:  # pragma: no cover
+            errs.append(e)
+
+    with PinnedRingIO(store, "cpu", slot_bytes=2048, n_slots=3) as io:
+        th = [threading.Thread(target=work, args=(v, v * 40_000)) for v in (1, 2)]
+        [t.start() for t in th]
+        [t.join() for t in th]
+        out = torch.zeros(80_000, dtype=torch.uint8)
+        io.read_into_device(out, 40_000)
+    assert not errs
+    assert (out[:30_000] == 1).all() and (out[40_000:70_000] == 2).all()
