@@ -91,13 +91,15 @@ class Timer:
         self.pairs = []
 
 
-def bench_copy(torch, ops, wl, dtype, dev, steps, warmup):
-    """Config 2/4: gather then scatter per step. Returns the result dict."""
+def bench_copy(torch, ops, wl, dtype, dev, steps, warmup, position=None):
+    """Config 2/4: gather then scatter per step. Returns the result dict.
+    For fp8 (config 4) the re-rotating scatter of the same pages is timed
+    too: each request moves by a random delta in [0, 32768)."""
     shape = wl.shape
     log(f"[bench] allocating caches {wl.num_blocks} blocks x {shape.num_layers} layers "
         f"({wl.num_blocks * shape.slot_bytes / 1e9:.1f} GB) + staging "
         f"{wl.staging_bytes / 1e9:.1f} GB")
-    full, caches, _ = fill_caches(torch, shape, wl.num_blocks, dtype, dev, seed=1)
+    full, caches, k_scale = fill_caches(torch, shape, wl.num_blocks, dtype, dev, seed=1)
     table = ops.LayerTable(caches)
     staging = torch.empty(wl.staging_bytes, dtype=torch.uint8, device=dev)
     ids = torch.from_numpy(wl.page_ids).to(dev)
@@ -127,6 +129,25 @@ def bench_copy(torch, ops, wl, dtype, dev, steps, warmup):
     ok = torch.equal(rec, caches[0][:, probe].reshape(-1).view(torch.uint8))
     P = wl.payload_bytes
     g_ms, s_ms = tg.mean_ms(), ts.mean_ms()
+    rot = {}
+    if dtype == "fp8" and position is not None:
+        rng = np.random.default_rng(7)
+        deltas = rng.integers(1, 32768, size=len(wl.req_pages)).tolist()
+        ridx, uniq = position.page_rope_index(wl.req_pages, deltas)
+        tabs = position.delta_tables(uniq, shape.head_dim, THETA, device=dev)
+        _, _, s_ridx = ops.dest_order(wl.page_ids, wl.slot_offsets, ridx)
+        ridx_d = torch.from_numpy(s_ridx.astype(np.int32)).to(dev)
+        tr = Timer(torch)
+        for i in range(warmup + steps):
+            if i < warmup:
+                ops.scatter_rerotate(table, s_ids, s_offs, staging, tabs, ridx_d, k_scale=k_scale)
+                continue
+            with tr:
+                ops.scatter_rerotate(table, s_ids, s_offs, staging, tabs, ridx_d, k_scale=k_scale)
+        torch.cuda.synchronize()
+        r_ms = tr.mean_ms()
+        rot = {"rerotate_ms": r_ms, "rerotate_GBps": 2 * P / (r_ms * 1e-3) / 1e9,
+               "rerotate_tokens_per_s": wl.tokens / (r_ms * 1e-3)}
     del full, caches, table, staging
     torch.cuda.empty_cache()
     return {
@@ -140,6 +161,7 @@ def bench_copy(torch, ops, wl, dtype, dev, steps, warmup):
         "scatter_GBps": 2 * P / (s_ms * 1e-3) / 1e9,
         "step_GBps": 4 * P / wall * steps / 1e9,
         "probe_ok": bool(ok),
+        **rot,
     }
 
 
@@ -285,7 +307,7 @@ def main() -> int:
         wl = workloads.config(c)
         if c in (2, 4):
             res[c] = bench_copy(torch, ops, wl, "bf16" if c == 2 else "fp8", dev,
-                                args.steps, args.warmup)
+                                args.steps, args.warmup, position)
         else:
             res[c] = bench_rerotate(torch, ops, position, wl, "bf16", dev,
                                     args.steps, args.warmup)
@@ -335,10 +357,15 @@ def main() -> int:
                 "algorithmic_bytes": 2 * r["payload_bytes"]}
     if 4 in res:
         r = res[4]
-        out["fp8_cfg4"] = {"gather_GBps": round(r["gather_GBps"], 1),
+        out["fp8_cfg4"] = {"workload": workloads.CONFIG_NAMES[4],
+                           "gather_GBps": round(r["gather_GBps"], 1),
                            "scatter_GBps": round(r["scatter_GBps"], 1),
                            "gather_ms": round(r["gather_ms"], 4),
-                           "scatter_ms": round(r["scatter_ms"], 4)}
+                           "scatter_ms": round(r["scatter_ms"], 4),
+                           "rerotate_GBps": round(r.get("rerotate_GBps", 0.0), 1),
+                           "rerotate_tokens_per_s": round(r.get("rerotate_tokens_per_s", 0.0)),
+                           "rerotate_ms": round(r.get("rerotate_ms", 0.0), 4),
+                           "tokens": r["tokens"], "payload_bytes": r["payload_bytes"]}
     if "value" not in out:
         r = res[configs[0]]
         out.update({"value": round(r.get("tokens_per_s", 0.0)), "unit": "tokens/s",

@@ -187,35 +187,38 @@ __device__ __forceinline__ uint32_t f32_to_fp16(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
-// OCP e4m3fn decode: bias 7, no infinities, S.1111.111 is NaN.
-__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
-  const uint32_t sign = (b & 0x80u) << 24;
-  const uint32_t em = b & 0x7fu;
-  if (em == 0x7fu) return __uint_as_float(0x7fc00000u | sign);
-  float mag;
-  if (em >= 0x08u) {
-    // normal: exponent field e in [1,15] -> fp32 exponent e + 120
-    mag = __uint_as_float((em + (120u << 3)) << 20);
-  } else {
-    mag = (float)em * 0x1p-9f;  // subnormal: m * 2^-9, exact
-  }
-  return __uint_as_float(__float_as_uint(mag) | sign);
+// OCP e4m3fn (bias 7, no infinities, S.1111.111 = NaN) through the gfx950
+// conversion instructions, which use the OCP formats: v_cvt_pk_f32_fp8
+// decodes two codes, v_cvt_pk_fp8_f32 encodes two floats with
+// round-to-nearest-even (both checked exhaustively against the bit-level
+// definition on MI355X: all 256 codes, 200k values incl. every midpoint).
+// Encoding saturates by clamping to +-448 first (compare-select keeps NaN);
+// the instruction turns NaN into 0xFF, which the clamp range never produces,
+// so 0xFF bytes are rewritten to the canonical 0x7F.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float clamp448(float f) {
+  f = f > 448.0f ? 448.0f : f;
+  return f < -448.0f ? -448.0f : f;
 }
-// fp32 -> e4m3fn, round-to-nearest-even, |f| saturated to 448 first;
-// NaN -> 0x7F.
-__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
-  if (__builtin_isnan(f)) return 0x7fu;
-  f = f > 448.0f ? 448.0f : (f < -448.0f ? -448.0f : f);
-  uint32_t u = __float_as_uint(f);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  u &= 0x7fffffffu;
-  if (u >= 0x3c800000u) {  // |f| >= 2^-6: normal range of e4m3
-    u += 0x7ffffu + ((u >> 20) & 1u);
-    return sign | ((u - (120u << 23)) >> 20);
-  }
-  // subnormal range: m = rne(|f| * 2^9) in [0, 8]; 8 encodes 2^-6 exactly
-  const float m = __builtin_rintf(__uint_as_float(u) * 512.0f);
-  return sign | (uint32_t)m;
+// 0x80 in every byte of w that equals 0xFF.
+__device__ __forceinline__ uint32_t ff_bytes(uint32_t w) {
+  const uint32_t t = ~w;
+  return ~(((t & 0x7f7f7f7fu) + 0x7f7f7f7fu) | t) & 0x80808080u;
+}
+__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* x) {
+  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  x[0] = lo.x;
+  x[1] = lo.y;
+  x[2] = hi.x;
+  x[3] = hi.y;
+}
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(const float* y) {
+  int e = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(y[0]), clamp448(y[1]), 0, false);
+  e = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(y[2]), clamp448(y[3]), e, true);
+  const uint32_t w = (uint32_t)e;
+  return w ^ ff_bytes(w);
 }
 
 template <int DT>
@@ -264,12 +267,12 @@ struct Codec<DSR_DTYPE_FP8_E4M3> {
   static constexpr int VE = 16;
   __device__ static void decode(u32x4 v, float* x) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = e4m3_to_f32((v[k >> 2] >> (8 * (k & 3))) & 0xffu);
+    for (int k = 0; k < 4; ++k) e4m3x4_to_f32(v[k], x + 4 * k);
   }
   __device__ static u32x4 encode(const float* y) {
-    u32x4 v = {0u, 0u, 0u, 0u};
+    u32x4 v;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) v[k >> 2] |= f32_to_e4m3(y[k]) << (8 * (k & 3));
+    for (int k = 0; k < 4; ++k) v[k] = f32x4_to_e4m3(y + 4 * k);
     return v;
   }
 };

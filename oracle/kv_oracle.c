@@ -170,10 +170,13 @@ static void rot(double* x1, double* x2, double a) {
 /* ---- load with re-rotation (net-new; the reference only carries the
  * integer offset, daser/position/fixed_offset.py:26-50) ---------------------
  * Scatter as orc_scatter. For a page with rotate[p] != 0, each K row (token
- * t of the page, head h) is first rotated back from its stored position
- * stored_pos[p] + t, then forward to new_pos[p] + t, in float64:
- *   x <- R(new + t) R(stored + t)^-1 x,  R(pos) pair j angle = pos * w_j,
- *   w_j = inv_freq[j] if given, else theta^(-2j/rot_dim).
+ * t of the page, head h) moves from its stored position stored_pos[p] + t to
+ * new_pos[p] + t: x <- R(new + t) R(stored + t)^-1 x = R(delta) x with the
+ * exact integer delta = (new + t) - (stored + t), evaluated as one float64
+ * rotation of pair j by angle delta * w_j, w_j = inv_freq[j] if given, else
+ * theta^(-2j/rot_dim). (Rotating back and then forward in two float64 steps
+ * is the same map for finite inputs, but turns an infinite element into NaN
+ * through inf * sin(0) when a position is 0.)
  * Pairs: neox (j, j + rot_dim/2); gptj (2j, 2j + 1). Elements >= rot_dim and
  * V are copied. e4m3: x = decode(q) * k_scale[layer], result / k_scale is
  * encoded (saturating). The result is rounded once to the storage format. */
@@ -208,7 +211,7 @@ void orc_scatter_rerotate(uint8_t* const* layer_base, int n_layers,
         const uint8_t* srow = src + r * row_bytes;
         uint8_t* drow = dst + r * row_bytes;
         for (int j = 0; j < rot_dim; ++j) x[j] = orc_decode(dtype, load_elem(srow, dtype, j)) * sc;
-        const double ps = (double)(stored_pos[p] + tok), pn = (double)(new_pos[p] + tok);
+        const double delta = (double)((new_pos[p] + tok) - (stored_pos[p] + tok));
         for (int j = 0; j < half; ++j) {
           double *a, *b;
           if (style == ORC_NEOX) {
@@ -218,8 +221,7 @@ void orc_scatter_rerotate(uint8_t* const* layer_base, int n_layers,
             a = &x[2 * j];
             b = &x[2 * j + 1];
           }
-          rot(a, b, -ps * w[j]);
-          rot(a, b, pn * w[j]);
+          rot(a, b, delta * w[j]);
         }
         for (int j = 0; j < rot_dim; ++j) store_elem(drow, dtype, j, orc_encode(dtype, x[j] / sc));
       }

@@ -264,3 +264,55 @@ def test_rerotate_bad_geometry_rejected(gpu):
         # neox fp8 needs rot_dim/2 to be a multiple of 16 elements
         ops.scatter_rerotate(ops.LayerTable(caches), [0], [0], st, tabs, [0], rot_dim=48,
                              k_scale=torch.ones(1, device=gpu))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "e4m3"])
+def test_rerotate_special_values(gpu, dt):
+    """NaN, +-Inf (bf16), +-0, subnormals and the e4m3 extremes follow the
+    oracle: NaN stays canonical NaN, zero delta is bit-exact, e4m3 saturates."""
+    print(f"case: rerotate special values {dt}", flush=True)
+    shape = KVShape(2, 2, 64, 16, 1 if dt == "e4m3" else 2)
+    nb = 4
+    caches = rand_caches(shape, nb, dt, gpu, seed=40, scale=30.0 if dt == "e4m3" else 1.0)
+    if dt == "bf16":
+        special = torch.tensor([float("nan"), float("inf"), -float("inf"), 0.0, -0.0,
+                                1e-40, -3e-39, 65504.0], dtype=torch.float32).to(torch.bfloat16)
+        bits = special.view(torch.int16)
+        for c in caches:
+            v = c.view(torch.int16)
+            v[0, :, 0, 0, :8] = bits.to(gpu)          # first-half elements
+            v[0, :, 1, 1, 32:40] = bits.to(gpu)       # their neox partners
+    else:
+        codes = torch.tensor([0x7F, 0xFF, 0x00, 0x80, 0x01, 0x81, 0x7E, 0xFE], dtype=torch.uint8)
+        for c in caches:
+            v = c.view(torch.uint8)
+            v[0, :, 0, 0, :8] = codes.to(gpu)
+            v[0, :, 2, 1, 32:40] = codes.to(gpu)
+    ids = np.arange(nb, dtype=np.int32)
+    offs = ids.astype(np.int64) * shape.slot_bytes
+    st = torch.zeros(nb * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(caches), ids, offs, st)
+    dst = [torch.zeros_like(c) for c in caches]
+    deltas = [0, 1, 777, 32767]
+    ridx, uniq = position.page_rope_index([1] * nb, deltas)
+    tabs = position.delta_tables(uniq, 64, 500000.0, device=gpu)
+    ks = torch.tensor([0.5, 2.0], device=gpu) if dt == "e4m3" else None
+    ops.scatter_rerotate(ops.LayerTable(dst), ids, offs, st, tabs, ridx, k_scale=ks)
+    ref = [np.zeros_like(to_bits_np(c, dt)) for c in caches]
+    oracle.scatter_rerotate(ref, ids, offs, st.cpu().numpy(), shape.layer_bytes,
+                            dtype=ORC_DT[dt], rot_dim=64, style=0,
+                            stored_pos=np.zeros(nb, np.int64), new_pos=np.asarray(deltas),
+                            rotate=np.asarray(deltas) != 0, theta=500000.0,
+                            k_scale=None if ks is None else np.float32([0.5, 2.0]))
+    torch.cuda.synchronize()
+    for l in range(2):
+        got = to_bits_np(dst[l], dt)
+        assert np.array_equal(got[1], ref[l][1])
+        assert np.array_equal(got[0][0], ref[l][0][0])  # zero delta: bit-exact
+        nan_ref = np.isnan(oracle.decode(ORC_DT[dt], ref[l][0]))
+        nan_got = np.isnan(oracle.decode(ORC_DT[dt], got[0]))
+        assert np.array_equal(nan_ref, nan_got)
+        assert np.array_equal(got[0][nan_got], ref[l][0][nan_ref])  # canonical NaN bits
+        ok, msg = oracle.rotation_within_tolerance(np.where(nan_got, 0, got[0]),
+                                                   np.where(nan_ref, 0, ref[l][0]), ORC_DT[dt])
+        assert ok, msg

@@ -261,15 +261,16 @@ def test_matches_complex_multiplication():
     assert np.array_equal(out[0][1, [0, 3]], c[0][1, [0, 3]])  # V untouched
 
 
-def test_stored_then_new_equals_delta():
-    """R(new) R(stored)^-1 depends only on new - stored (per token)."""
-    c = _rot_case(BF16, D=16)
-    a = _rerotate(c, [2], BF16, stored=1000, new=1500, theta=777.0)
-    b = _rerotate(c, [2], BF16, stored=0, new=500, theta=777.0)
-    av = oracle.decode(BF16, a[0][0, 2])
-    bv = oracle.decode(BF16, b[0][0, 2])
-    assert np.max(oracle.ulp_steps(a[0][0, 2], b[0][0, 2], BF16)) <= 1
-    assert np.allclose(av, bv, atol=1e-2)
+def test_composition_of_rotations():
+    """R(200) after R(300) is R(500) (each step rounded once to bf16), and a
+    move from stored position 1000 to 1500 equals one from 0 to 500."""
+    c = _rot_case(BF16, D=16, seed=15)
+    two = _rerotate(_rerotate(c, [2], BF16, stored=0, new=300, theta=777.0), [2], BF16,
+                    stored=300, new=500, theta=777.0)
+    one = _rerotate(c, [2], BF16, stored=1000, new=1500, theta=777.0)
+    ok, msg = oracle.rotation_within_tolerance(two[0][0, 2], one[0][0, 2], BF16, 2 ** -7)
+    assert ok, msg
+    assert np.median(oracle.ulp_steps(two[0][0, 2], one[0][0, 2], BF16)) == 0
 
 
 def test_inverse_and_norm_preservation():
