@@ -24,6 +24,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "daser_kv.h"
 
@@ -35,12 +36,16 @@ constexpr int kThreads = 256;     // 4 wave64 per workgroup
 constexpr int kGatherUnroll = 16;  // 16-byte vectors per lane per half per round
 constexpr int kScatterUnroll = 8;
 constexpr int kRotUnroll = 4;      // rotation tasks per lane per round (pair-task kernel)
-// Re-rotation runs fastest with two workgroups per CU (measured 5.54 TB/s
-// vs 5.31 TB/s at the register-limited 4 per CU, Llama-3-8B shape): the
-// rotation leaves each workgroup without loads in flight between its read
-// and write phases, and fewer, fuller workgroups per CU keep HBM busier.
-// The cap is applied with dynamic LDS sized from the CU's LDS capacity.
-constexpr int kRotWgPerCu = 2;
+// Workgroups per CU for the re-rotation kernel, applied with dynamic LDS
+// sized from the CU's LDS capacity (env DSR_ROT_WG_PER_CU overrides, for
+// tuning). Measured at the Llama-3-8B shape, interleaved A/B on one MI355X:
+// 16-bit K (64 KiB per unit) runs best at 2 per CU (7.79-7.86 ms vs
+// 8.13-8.18 ms at 6 or uncapped); e4m3 (32 KiB per unit) at 6 per CU
+// (22.3 ms vs 28.4 ms at 2).
+template <int DT>
+constexpr int rot_wg_per_cu() {
+  return DT == DSR_DTYPE_FP8_E4M3 ? 6 : 2;
+}
 constexpr int kMaxRotHalf = 512;   // LDS table capacity: rot_dim <= 1024
 constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
 
@@ -612,20 +617,22 @@ UnitArgs make_unit(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
 
 // Dynamic LDS that limits the re-rotation kernel to kRotWgPerCu workgroups
 // per CU on the current device (0 if the capacity cannot be read).
-size_t rot_occupancy_lds() {
+size_t rot_occupancy_lds(int wg_per_cu) {
   int dev = 0, lds = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
                             dev) != hipSuccess || lds <= 0)
     return 0;
-  const int64_t want = (int64_t)lds / kRotWgPerCu - (int64_t)sizeof(float2) * kMaxRotHalf;
+  const int64_t want = (int64_t)lds / wg_per_cu - (int64_t)sizeof(float2) * kMaxRotHalf;
   return want > 0 ? (size_t)want : 0;
 }
 
 template <int DT>
 int launch_rerotate(const RotArgs& ra, int style, unsigned grid, hipStream_t s) {
   const int h = ra.half_vecs;
-  const size_t dyn = rot_occupancy_lds();
+  int wg = rot_wg_per_cu<DT>();
+  if (const char* e = getenv("DSR_ROT_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
+  const size_t dyn = rot_occupancy_lds(wg);
   const bool contig = style == DSR_ROPE_GPTJ ||
                       (h > 0 && h <= 32 && (h & (h - 1)) == 0 && ra.row_vecs % (2 * h) == 0);
   if (contig) {
