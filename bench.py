@@ -130,6 +130,37 @@ def bench_copy(torch, ops, wl, dtype, dev, steps, warmup, position=None):
     P = wl.payload_bytes
     g_ms, s_ms = tg.mean_ms(), ts.mean_ms()
     rot = {}
+    if dtype == "bf16":
+        # the same requests through vLLM's slot_mapping (token-granular form):
+        # moves only the valid tokens' rows
+        tables, k = [], 0
+        for n in wl.req_pages:
+            tables.append(wl.page_ids[k:k + n].tolist())
+            k += n
+        row = shape.num_heads * shape.head_dim * shape.elem_bytes
+        sm_np = ops.slot_mapping_for(tables, wl.req_tokens, shape.block_size)
+        ro_np = ops.token_row_offsets(wl.req_tokens, shape.slot_bytes, shape.block_size, row)
+        sm = torch.from_numpy(sm_np).to(dev)
+        ro = torch.from_numpy(ro_np).to(dev)
+        order = np.argsort(sm_np, kind="stable")  # scatter in destination order
+        sm_s = torch.from_numpy(sm_np[order]).to(dev)
+        ro_s = torch.from_numpy(ro_np[order]).to(dev)
+        tsg, tss = Timer(torch), Timer(torch)
+        for i in range(warmup + steps):
+            if i < warmup:
+                ops.gather_slots(table, sm, ro, staging)
+                ops.scatter_slots(table, sm_s, ro_s, staging)
+                continue
+            with tsg:
+                ops.gather_slots(table, sm, ro, staging)
+            with tss:
+                ops.scatter_slots(table, sm_s, ro_s, staging)
+        torch.cuda.synchronize()
+        tokP = wl.tokens * row * 2 * shape.num_layers
+        rot = {"slots_gather_ms": tsg.mean_ms(), "slots_scatter_ms": tss.mean_ms(),
+               "slots_payload_bytes": tokP,
+               "slots_gather_GBps": 2 * tokP / (tsg.mean_ms() * 1e-3) / 1e9,
+               "slots_scatter_GBps": 2 * tokP / (tss.mean_ms() * 1e-3) / 1e9}
     if dtype == "fp8" and position is not None:
         rng = np.random.default_rng(7)
         deltas = rng.integers(1, 32768, size=len(wl.req_pages)).tolist()
@@ -343,6 +374,12 @@ def main() -> int:
             "scatter": {"ms": round(r["scatter_ms"], 4), "GBps": round(r["scatter_GBps"], 1),
                         "frac": round(r["scatter_GBps"] / HBM_PEAK_GBS, 4)},
         }
+        out["kernels"]["gather_slots"] = {
+            "ms": round(r["slots_gather_ms"], 4), "GBps": round(r["slots_gather_GBps"], 1),
+            "frac": round(r["slots_gather_GBps"] / HBM_PEAK_GBS, 4)}
+        out["kernels"]["scatter_slots"] = {
+            "ms": round(r["slots_scatter_ms"], 4), "GBps": round(r["slots_scatter_GBps"], 1),
+            "frac": round(r["slots_scatter_GBps"] / HBM_PEAK_GBS, 4)}
         out["check"] = {"round_trip_probe": r["probe_ok"]}
     for c in (3, 5):
         if c in res:

@@ -39,11 +39,14 @@ _I64 = ctypes.c_int64
 
 # Argument lists, one per exported entry point, in header order.
 _COPY_ARGS = [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _P, _I64, _I64, _I, _P]
+_SLOT_ARGS = [_P, _I, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _I, _P, _I64, _I64, _I, _P]
 SIGNATURES = {
     "dsr_abi_version": ([], _I),
     "dsr_error_string": ([_I], ctypes.c_char_p),
     "dsr_gather": (_COPY_ARGS, _I),
     "dsr_scatter": (_COPY_ARGS, _I),
+    "dsr_gather_slots": (_SLOT_ARGS, _I),
+    "dsr_scatter_slots": (_SLOT_ARGS, _I),
     "dsr_scatter_rerotate": (
         _COPY_ARGS[:-1] + [_P, _P, _I, _I, _I, _I, _I, _P, _P],
         _I,

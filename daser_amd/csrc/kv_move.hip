@@ -571,6 +571,92 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
   }
 }
 
+// ---------------------------------------------------------------------------
+// Token-granular (slot_mapping-driven) gather / scatter.
+
+struct SlotArgs {
+  const uint64_t* layer_base;
+  int64_t kv_stride;
+  int64_t page_stride;
+  int64_t page_bytes;
+  int64_t num_blocks;
+  int64_t row_bytes;
+  const int64_t* slot_mapping;
+  const int64_t* row_offsets;
+  uint8_t* staging;
+  int64_t staging_bytes;
+  int64_t layer_bytes;
+  int32_t n_tokens;
+  int32_t n_layers;
+  int32_t layer0;
+  int32_t block_size;
+};
+
+constexpr int kWaveSize = 64;
+constexpr int kTokPerWave = 4;  // tokens whose rows a wave has in flight at once
+constexpr int kTokPerWg = kTokPerWave * (kThreads / kWaveSize);
+constexpr int kRowUnroll = 2;   // 64-vector slices of a row per round
+
+// One workgroup per (16 consecutive tokens, layer); each wave owns 4 of the
+// tokens. Token addresses are wave-uniform (scalar loads of slot_mapping and
+// row_offsets); the lanes cover a row's 16-byte vectors, so a wave moves a
+// token's whole K and V rows, and 4 tokens' rows are in flight together.
+template <bool kGather>
+__global__ __launch_bounds__(kThreads) void kv_slots_kernel(SlotArgs a) {
+  const int64_t unit = blockIdx.x;
+  const int64_t tb = unit / a.n_layers;
+  const int l = (int)(unit - tb * a.n_layers);
+  const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
+  const int vpr = (int)(a.row_bytes >> 4);
+  rsrc_t ck[kTokPerWave], cv[kTokPerWave], rk[kTokPerWave], rv[kTokPerWave];
+  bool ok[kTokPerWave];
+#pragma unroll
+  for (int j = 0; j < kTokPerWave; ++j) {
+    const int64_t t = tb * kTokPerWg + wave * kTokPerWave + j;
+    ok[j] = false;
+    if (t < a.n_tokens) {
+      const int64_t slot = a.slot_mapping[t];
+      const int64_t blk = slot >= 0 ? slot / a.block_size : -1;
+      const int64_t off = a.row_offsets[t] + (int64_t)(a.layer0 + l) * a.layer_bytes;
+      ok[j] = blk >= 0 && blk < a.num_blocks && off >= 0 &&
+              off + a.page_bytes + a.row_bytes <= a.staging_bytes;
+      if (ok[j]) {
+        const uint8_t* row = reinterpret_cast<const uint8_t*>(a.layer_base[l]) +
+                             blk * a.page_stride + (slot - blk * a.block_size) * a.row_bytes;
+        ck[j] = make_rsrc(row, a.row_bytes);
+        cv[j] = make_rsrc(row + a.kv_stride, a.row_bytes);
+        rk[j] = make_rsrc(a.staging + off, a.row_bytes);
+        rv[j] = make_rsrc(a.staging + off + a.page_bytes, a.row_bytes);
+      }
+    }
+  }
+  for (int vb = 0; vb < vpr; vb += kWaveSize * kRowUnroll) {
+    u32x4 xk[kTokPerWave][kRowUnroll], xv[kTokPerWave][kRowUnroll];
+#pragma unroll
+    for (int j = 0; j < kTokPerWave; ++j) {
+#pragma unroll
+      for (int m = 0; m < kRowUnroll; ++m) {
+        const int v = vb + m * kWaveSize + lane;
+        if (ok[j] && v < vpr) {
+          xk[j][m] = bload(kGather ? ck[j] : rk[j], v << 4);
+          xv[j][m] = bload(kGather ? cv[j] : rv[j], v << 4);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kTokPerWave; ++j) {
+#pragma unroll
+      for (int m = 0; m < kRowUnroll; ++m) {
+        const int v = vb + m * kWaveSize + lane;
+        if (ok[j] && v < vpr) {
+          bstore(kGather ? rk[j] : ck[j], v << 4, xk[j][m]);
+          bstore(kGather ? rv[j] : cv[j], v << 4, xv[j][m]);
+        }
+      }
+    }
+  }
+}
+
 bool aligned16(int64_t v) { return (v & 15) == 0; }
 bool aligned16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -774,6 +860,74 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
     default:
       return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, rope_style, grid, s);
   }
+}
+
+namespace {
+
+int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                 int64_t page_stride, int64_t page_bytes, int64_t num_blocks, int block_size,
+                 int64_t row_bytes, const int64_t* slot_mapping, const int64_t* row_offsets,
+                 int n_tokens, const void* staging, int64_t staging_bytes,
+                 int64_t layer_bytes, int layer0, dsr_stream_t stream) {
+  if (n_tokens < 0 || n_layers < 0 || layer0 < 0 || num_blocks < 0 || staging_bytes < 0 ||
+      block_size <= 0 || row_bytes <= 0 || page_bytes <= 0)
+    return DSR_ERR_ARG;
+  if (n_tokens == 0 || n_layers == 0) return DSR_OK;
+  if (!layer_base || !slot_mapping || !row_offsets || !staging) return DSR_ERR_ARG;
+  if (page_bytes < (int64_t)block_size * row_bytes || layer_bytes < 2 * page_bytes ||
+      row_bytes > 0x7fffffffLL)
+    return DSR_ERR_SHAPE;
+  if (!aligned16(kv_stride) || !aligned16(page_stride) || !aligned16(page_bytes) ||
+      !aligned16(row_bytes) || !aligned16(layer_bytes) || !aligned16p(staging))
+    return DSR_ERR_ALIGN;
+  const int64_t blocks = ((int64_t)n_tokens + kTokPerWg - 1) / kTokPerWg;
+  if (blocks * n_layers > 0x7fffffffLL) return DSR_ERR_ARG;
+  SlotArgs a;
+  a.layer_base = layer_base;
+  a.kv_stride = kv_stride;
+  a.page_stride = page_stride;
+  a.page_bytes = page_bytes;
+  a.num_blocks = num_blocks;
+  a.row_bytes = row_bytes;
+  a.slot_mapping = slot_mapping;
+  a.row_offsets = row_offsets;
+  a.staging = const_cast<uint8_t*>(static_cast<const uint8_t*>(staging));
+  a.staging_bytes = staging_bytes;
+  a.layer_bytes = layer_bytes;
+  a.n_tokens = n_tokens;
+  a.n_layers = n_layers;
+  a.layer0 = layer0;
+  a.block_size = block_size;
+  const unsigned grid = (unsigned)(blocks * n_layers);
+  if (gather)
+    kv_slots_kernel<true><<<grid, kThreads, 0, (hipStream_t)stream>>>(a);
+  else
+    kv_slots_kernel<false><<<grid, kThreads, 0, (hipStream_t)stream>>>(a);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+int dsr_gather_slots(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                     int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                     int block_size, int64_t row_bytes, const int64_t* slot_mapping,
+                     const int64_t* row_offsets, int n_tokens, void* staging,
+                     int64_t staging_bytes, int64_t layer_bytes, int layer0,
+                     dsr_stream_t stream) {
+  return slots_launch(true, layer_base, n_layers, kv_stride, page_stride, page_bytes,
+                      num_blocks, block_size, row_bytes, slot_mapping, row_offsets, n_tokens,
+                      staging, staging_bytes, layer_bytes, layer0, stream);
+}
+
+int dsr_scatter_slots(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                      int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                      int block_size, int64_t row_bytes, const int64_t* slot_mapping,
+                      const int64_t* row_offsets, int n_tokens, const void* staging,
+                      int64_t staging_bytes, int64_t layer_bytes, int layer0,
+                      dsr_stream_t stream) {
+  return slots_launch(false, layer_base, n_layers, kv_stride, page_stride, page_bytes,
+                      num_blocks, block_size, row_bytes, slot_mapping, row_offsets, n_tokens,
+                      staging, staging_bytes, layer_bytes, layer0, stream);
 }
 
 }  // extern "C"

@@ -314,6 +314,96 @@ def scatter_rerotate(
     _lib.check("dsr_scatter_rerotate", rc)
 
 
+def _slots_args(table: LayerTable, slot_mapping, row_offsets, staging, layer0, layers,
+                records_written: bool):
+    lay = table.layout
+    first, count = (0, lay.num_layers) if layers is None else layers
+    if first < 0 or count < 0 or first + count > lay.num_layers:
+        raise IndexError("layer range outside the registered caches")
+    if staging.device != lay.device or not staging.is_contiguous():
+        raise ValueError("staging must be a contiguous tensor on the caches' device")
+    row_bytes = lay.num_heads * lay.head_dim * lay.elem_bytes
+    sm = _host_array(slot_mapping, np.int64)
+    ro = _host_array(row_offsets, np.int64)
+    if sm is not None and ro is not None:
+        if sm.shape != ro.shape:
+            raise ValueError("slot_mapping and row_offsets differ in length")
+        valid = sm >= 0
+        if valid.any():
+            if sm[valid].max() >= lay.num_blocks * lay.block_size:
+                raise IndexError("slot outside the block pool")
+            r = ro[valid]
+            end = r.max() + (layer0 + first + count - 1) * lay.layer_bytes + lay.page_bytes \
+                + row_bytes
+            if r.min() < 0 or end > staging.numel() * staging.element_size():
+                raise IndexError("token row outside the staging buffer")
+            if np.any(r % 16):
+                raise ValueError("row offsets must be multiples of 16 bytes")
+            if records_written and np.unique(r).size != r.size:
+                raise ValueError("two tokens write the same record row")
+            if not records_written and np.unique(sm[valid]).size != int(valid.sum()):
+                raise ValueError("a destination slot appears twice in one scatter")
+    sm_d = _as_device_table(slot_mapping, torch.int64, lay.device, "slot_mapping")
+    ro_d = _as_device_table(row_offsets, torch.int64, lay.device, "row_offsets")
+    if sm_d.numel() != ro_d.numel():
+        raise ValueError("slot_mapping and row_offsets differ in length")
+    return (table.ptr(first), count, lay.kv_stride, lay.page_stride, lay.page_bytes,
+            lay.num_blocks, lay.block_size, row_bytes, sm_d.data_ptr(), ro_d.data_ptr(),
+            sm_d.numel(), staging.data_ptr(), staging.numel() * staging.element_size(),
+            lay.layer_bytes, layer0 + first), (sm_d, ro_d)
+
+
+def gather_slots(table: LayerTable, slot_mapping, row_offsets, staging: torch.Tensor, *,
+                 layer0: int = 0, layers: Optional[tuple[int, int]] = None) -> None:
+    """Token-granular gather driven by vLLM's slot_mapping (-1 = padding):
+    each valid token's K and V rows of every layer go to its record rows at
+    ``row_offsets[t]`` (see :func:`token_row_offsets`)."""
+    args, keep = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, True)
+    rc = _lib.lib().dsr_gather_slots(*args, _stream_handle(table.layout.device))
+    _lib.check("dsr_gather_slots", rc)
+
+
+def scatter_slots(table: LayerTable, slot_mapping, row_offsets, staging: torch.Tensor, *,
+                  layer0: int = 0, layers: Optional[tuple[int, int]] = None) -> None:
+    """Inverse of :func:`gather_slots`. Host tables are processed in
+    destination-slot order (near-sequential writes), like :func:`scatter`."""
+    sm = _host_array(slot_mapping, np.int64)
+    ro = _host_array(row_offsets, np.int64)
+    if sm is not None and ro is not None and sm.size:
+        order = np.argsort(sm, kind="stable")
+        slot_mapping, row_offsets = sm[order], ro[order]
+    args, keep = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, False)
+    rc = _lib.lib().dsr_scatter_slots(*args, _stream_handle(table.layout.device))
+    _lib.check("dsr_scatter_slots", rc)
+
+
+def token_row_offsets(req_tokens: Sequence[int], slot_bytes: int, block_size: int,
+                      row_bytes: int, base: int = 0) -> np.ndarray:
+    """Record offset of each token's K row for requests whose records are
+    packed back to back (request r's slot i at base + (slots before r + i) *
+    slot_bytes): token t of a request sits in its slot t // block_size at row
+    t % block_size, the position dsr_gather puts it at."""
+    out = []
+    slot0 = 0
+    for n in req_tokens:
+        t = np.arange(int(n), dtype=np.int64)
+        out.append(base + (slot0 + t // block_size) * slot_bytes + (t % block_size) * row_bytes)
+        slot0 += -(-int(n) // block_size)
+    return np.concatenate(out) if out else np.zeros(0, np.int64)
+
+
+def slot_mapping_for(block_tables: Sequence[Sequence[int]], req_tokens: Sequence[int],
+                     block_size: int) -> np.ndarray:
+    """vLLM's slot_mapping of the requests' tokens:
+    slot = block_ids[t // block_size] * block_size + t % block_size."""
+    out = []
+    for blocks, n in zip(block_tables, req_tokens):
+        t = np.arange(int(n), dtype=np.int64)
+        b = np.asarray(blocks, dtype=np.int64)
+        out.append(b[t // block_size] * block_size + t % block_size)
+    return np.concatenate(out) if out else np.zeros(0, np.int64)
+
+
 def slot_offsets_for(num_pages: Sequence[int], slot_bytes: int, base: int = 0) -> np.ndarray:
     """Record offsets for requests packed back to back in one staging buffer:
     request r's slot i lives at ``base + (pages before r + i) * slot_bytes``."""

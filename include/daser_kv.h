@@ -148,6 +148,45 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          int rot_dim, int rope_style, int dtype,
                          const float* k_scale, dsr_stream_t stream);
 
+/*
+ * Token-granular offload gather driven by vLLM's slot_mapping: for every
+ * token t in [0, n_tokens) with slot = slot_mapping[t] >= 0 and every layer
+ * l, copy its K row (all heads: row_bytes = H * D * elem_bytes) from
+ *     layer_base[l] + (slot / block_size) * page_stride
+ *                   + (slot % block_size) * row_bytes
+ * to  staging + row_offsets[t] + (layer0 + l) * layer_bytes,
+ * and its V row (+ kv_stride in the cache) to the same place + page_bytes.
+ * Tokens with slot < 0 (vLLM's padding) are skipped. With row_offsets[t] =
+ * record(t / block_size) + (t % block_size) * row_bytes this writes exactly
+ * the slot records of dsr_gather, restricted to the valid tokens (a partial
+ * last page leaves its tail rows untouched).
+ *
+ * Per-token form of the save loop of daser/connector/daser_connector.py:
+ * 625-632 (which copies whole pages, :280); slot = block_ids[t / bs] * bs +
+ * t % bs is vLLM's slot_mapping for the same tokens.
+ *
+ *   slot_mapping  [device] n_tokens int64 slots (block * block_size + offset)
+ *   row_offsets   [device] n_tokens int64 record offsets of each token's K row
+ */
+int dsr_gather_slots(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                     int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                     int block_size, int64_t row_bytes, const int64_t* slot_mapping,
+                     const int64_t* row_offsets, int n_tokens, void* staging,
+                     int64_t staging_bytes, int64_t layer_bytes, int layer0,
+                     dsr_stream_t stream);
+
+/*
+ * Inverse of dsr_gather_slots: each valid token's K and V rows are copied
+ * from its record rows back to slot slot_mapping[t] of every layer. Per-token
+ * form of the load loop of daser/connector/daser_connector.py:536-551.
+ */
+int dsr_scatter_slots(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                      int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                      int block_size, int64_t row_bytes, const int64_t* slot_mapping,
+                      const int64_t* row_offsets, int n_tokens, const void* staging,
+                      int64_t staging_bytes, int64_t layer_bytes, int layer0,
+                      dsr_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

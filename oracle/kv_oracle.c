@@ -237,3 +237,45 @@ void orc_decode_array(int dtype, const uint32_t* bits, double* out, int64_t n) {
 void orc_encode_array(int dtype, const double* v, uint32_t* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = orc_encode(dtype, v[i]);
 }
+
+/* ---- token-granular forms (vLLM slot_mapping) ------------------------------
+ * Token t with slot = slot_mapping[t] >= 0: its K row (row_bytes, all heads)
+ * sits at layer_base[l] + (slot / bs) * page_stride + (slot % bs) * row_bytes
+ * and V at + kv_stride; its record rows at staging + row_offsets[t] +
+ * (layer0 + l) * layer_bytes and + page_bytes. Padding tokens (slot < 0) are
+ * skipped. Per-token form of daser_connector.py:625-632 / :536-551. */
+void orc_gather_slots(const uint8_t* const* layer_base, int n_layers, int64_t kv_stride,
+                      int64_t page_stride, int64_t page_bytes, int block_size,
+                      int64_t row_bytes, const int64_t* slot_mapping,
+                      const int64_t* row_offsets, int n_tokens, uint8_t* staging,
+                      int64_t layer_bytes, int layer0) {
+  for (int t = 0; t < n_tokens; ++t) {
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0) continue;
+    for (int l = 0; l < n_layers; ++l) {
+      const uint8_t* src = layer_base[l] + (slot / block_size) * page_stride +
+                           (slot % block_size) * row_bytes;
+      uint8_t* dst = staging + row_offsets[t] + (int64_t)(layer0 + l) * layer_bytes;
+      memcpy(dst, src, (size_t)row_bytes);
+      memcpy(dst + page_bytes, src + kv_stride, (size_t)row_bytes);
+    }
+  }
+}
+
+void orc_scatter_slots(uint8_t* const* layer_base, int n_layers, int64_t kv_stride,
+                       int64_t page_stride, int64_t page_bytes, int block_size,
+                       int64_t row_bytes, const int64_t* slot_mapping,
+                       const int64_t* row_offsets, int n_tokens, const uint8_t* staging,
+                       int64_t layer_bytes, int layer0) {
+  for (int t = 0; t < n_tokens; ++t) {
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0) continue;
+    for (int l = 0; l < n_layers; ++l) {
+      uint8_t* dst = layer_base[l] + (slot / block_size) * page_stride +
+                     (slot % block_size) * row_bytes;
+      const uint8_t* src = staging + row_offsets[t] + (int64_t)(layer0 + l) * layer_bytes;
+      memcpy(dst, src, (size_t)row_bytes);
+      memcpy(dst + kv_stride, src + page_bytes, (size_t)row_bytes);
+    }
+  }
+}

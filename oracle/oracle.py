@@ -45,9 +45,13 @@ def lib() -> ctypes.CDLL:
         h.orc_scatter_rerotate.argtypes = copy + [
             I, I, I, I, I, P, P, P, P, ctypes.c_double, P,
         ]
+        slots = [P, I, I64, I64, I64, I, I64, P, P, I, P, I64, I]
+        h.orc_gather_slots.argtypes = slots
+        h.orc_scatter_slots.argtypes = slots
         h.orc_decode_array.argtypes = [I, P, P, I64]
         h.orc_encode_array.argtypes = [I, P, P, I64]
-        for f in ("orc_gather", "orc_scatter", "orc_scatter_rerotate",
+        for f in ("orc_gather", "orc_scatter", "orc_scatter_rerotate", "orc_gather_slots",
+                  "orc_scatter_slots",
                   "orc_decode_array", "orc_encode_array"):
             getattr(h, f).restype = None
         _lib = h
@@ -111,6 +115,30 @@ def scatter_rerotate(layers, page_ids, slot_offsets, staging: np.ndarray,
         _ptr(stg), layer_bytes, layer0, h, d, rot_dim, style, dtype,
         None if ks is None else _ptr(ks), _ptr(sp), _ptr(npos), _ptr(rot),
         float(theta), None if inv is None else _ptr(inv))
+
+
+def _slots_call(fn, layers, slot_mapping, row_offsets, staging, layer_bytes, layer0):
+    tab, kvs, ps, pb = _layer_table(layers)
+    _, _, bs, h, d = layers[0].shape
+    row = h * d * layers[0].itemsize
+    sm = np.ascontiguousarray(slot_mapping, dtype=np.int64)
+    ro = np.ascontiguousarray(row_offsets, dtype=np.int64)
+    assert sm.shape == ro.shape
+    fn(_ptr(tab), len(layers), kvs, ps, pb, bs, row, _ptr(sm), _ptr(ro), sm.size,
+       _ptr(staging), layer_bytes, layer0)
+
+
+def gather_slots(layers, slot_mapping, row_offsets, staging: np.ndarray, layer_bytes: int,
+                 layer0: int = 0) -> None:
+    assert staging.dtype == np.uint8 and staging.flags["C_CONTIGUOUS"]
+    _slots_call(lib().orc_gather_slots, layers, slot_mapping, row_offsets, staging,
+                layer_bytes, layer0)
+
+
+def scatter_slots(layers, slot_mapping, row_offsets, staging: np.ndarray, layer_bytes: int,
+                  layer0: int = 0) -> None:
+    _slots_call(lib().orc_scatter_slots, layers, slot_mapping, row_offsets,
+                np.ascontiguousarray(staging), layer_bytes, layer0)
 
 
 def decode(dtype: int, bits) -> np.ndarray:

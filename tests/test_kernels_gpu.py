@@ -316,3 +316,55 @@ def test_rerotate_special_values(gpu, dt):
         ok, msg = oracle.rotation_within_tolerance(np.where(nan_got, 0, got[0]),
                                                    np.where(nan_ref, 0, ref[l][0]), ORC_DT[dt])
         assert ok, msg
+
+
+def test_slots_gather_scatter_match_oracle(gpu):
+    """slot_mapping-driven token gather/scatter at the Qwen2-0.5B shape with
+    ragged requests, partial last pages and padding tokens."""
+    print("case: slots gather/scatter", flush=True)
+    wl = workloads.config(1)
+    shape = wl.shape
+    caches = rand_caches(shape, wl.num_blocks, "bf16", gpu, seed=50)
+    tables, k = [], 0
+    for n in wl.req_pages:
+        tables.append(wl.page_ids[k:k + n].tolist())
+        k += n
+    row = shape.num_heads * shape.head_dim * 2
+    sm = ops.slot_mapping_for(tables, wl.req_tokens, shape.block_size)
+    ro = ops.token_row_offsets(wl.req_tokens, shape.slot_bytes, shape.block_size, row)
+    pad = np.arange(0, sm.size, 97)
+    sm[pad] = -1
+    st = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather_slots(ops.LayerTable(caches), sm, ro, st)
+    ref = np.zeros(wl.staging_bytes, dtype=np.uint8)
+    host = [to_bits_np(c, "bf16") for c in caches]
+    oracle.gather_slots(host, sm, ro, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    assert np.array_equal(st.cpu().numpy(), ref)
+    dst = [torch.zeros_like(c) for c in caches]
+    ops.scatter_slots(ops.LayerTable(dst), sm, ro, st)
+    dref = [np.zeros_like(h) for h in host]
+    oracle.scatter_slots(dref, sm, ro, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    for d, r in zip(dst, dref):
+        assert np.array_equal(to_bits_np(d, "bf16"), r)
+
+
+def test_slots_gather_equals_page_gather_for_full_pages(gpu):
+    print("case: slots == pages", flush=True)
+    shape = KVShape(4, 8, 128, 16, 2)
+    wl = workloads.ragged(shape, 6, 1, 40, seed=51, pool_slack=1.3)
+    toks = [n * 16 for n in wl.req_pages]  # whole pages
+    caches = rand_caches(shape, wl.num_blocks, "bf16", gpu, seed=52)
+    table = ops.LayerTable(caches)
+    tables, k = [], 0
+    for n in wl.req_pages:
+        tables.append(wl.page_ids[k:k + n].tolist())
+        k += n
+    a = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+    b = torch.zeros_like(a)
+    ops.gather(table, wl.page_ids, wl.slot_offsets, a)
+    ops.gather_slots(table, ops.slot_mapping_for(tables, toks, 16),
+                     ops.token_row_offsets(toks, shape.slot_bytes, 16, 8 * 128 * 2), b)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

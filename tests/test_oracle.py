@@ -351,3 +351,48 @@ def test_page_rope_index():
     idx, uniq = position.page_rope_index([2, 1, 3, 2], [5, 0, 5, 9])
     assert uniq == [5, 9]
     assert idx.tolist() == [0, 0, -1, 0, 0, 0, 1, 1]
+
+
+# ---------------------------------------------------------------------------
+# token-granular (slot_mapping) forms
+
+
+def test_slot_gather_equals_page_gather_on_valid_tokens():
+    """With slot = block_ids[t // bs] * bs + t % bs and each token's record
+    row at slot t // bs, row t % bs, the token form writes the page form's
+    bytes for every valid token and leaves the tail rows of a partial last
+    page untouched; padding tokens (slot -1) are skipped."""
+    rng = np.random.default_rng(20)
+    L, nb, bs, H, D = 3, 10, 4, 2, 8
+    caches = [rng.integers(1, 65535, size=(2, nb, bs, H, D), dtype=np.uint16) for _ in range(L)]
+    tables = [[7, 1, 4], [9, 0]]
+    toks = [10, 8]  # request 0 ends inside its third page
+    slot = _slot_size(caches)
+    row = H * D * 2
+    ids = np.concatenate([np.asarray(t) for t in tables]).astype(np.int32)
+    page = np.zeros(ids.size * slot, dtype=np.uint8)
+    oracle.gather(caches, ids, np.arange(ids.size) * slot, page, slot // L)
+    sm = ops.slot_mapping_for(tables, toks, bs)
+    ro = ops.token_row_offsets(toks, slot, bs, row)
+    sm = np.concatenate([sm, [-1, -1]])  # padding
+    ro = np.concatenate([ro, [0, 0]])
+    tok = np.zeros_like(page)
+    oracle.gather_slots(caches, sm, ro, tok, slot // L)
+    mask = np.zeros_like(page, dtype=bool)
+    for r in ro[:-2]:
+        for l in range(L):
+            o = r + l * (slot // L)
+            mask[o:o + row] = True
+            mask[o + bs * row:o + bs * row + row] = True
+    assert np.array_equal(tok[mask], page[mask])
+    assert not tok[~mask].any()
+    # the partial page's tail rows (tokens 10, 11 of request 0) stay zero
+    back = [np.zeros_like(c) for c in caches]
+    oracle.scatter_slots(back, sm, ro, tok, slot // L)
+    for b, c in zip(back, caches):
+        bt = b[:, :, :, :, :].reshape(2, nb * bs, H, D)
+        ct = c.reshape(2, nb * bs, H, D)
+        valid = sm[sm >= 0]
+        assert np.array_equal(bt[:, valid], ct[:, valid])
+        others = np.setdiff1d(np.arange(nb * bs), valid)
+        assert not bt[:, others].any()
