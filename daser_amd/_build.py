@@ -14,7 +14,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRC = os.path.join(HERE, "csrc", "kv_move.hip")
+SRCS = [os.path.join(HERE, "csrc", "kv_move.hip"), os.path.join(HERE, "csrc", "store_ring.cpp")]
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "libdaser_kv.so")
 
@@ -45,7 +45,7 @@ def hipcc() -> str:
 def build(verbose: bool = False) -> str:
     """Compiles the kernels and C ABI into ``daser_amd/libdaser_kv.so``."""
     tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", SRC, "-o", tmp]
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *SRCS, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -25,6 +25,12 @@ DSR_OK = 0
 DSR_ERR_ARG = -1
 DSR_ERR_ALIGN = -2
 DSR_ERR_SHAPE = -3
+DSR_ERR_IO = -4
+DSR_ERR_NOFILE = -5
+
+DSR_RING_HOST = 1
+DSR_RING_DIRECT = 2
+DSR_RING_NO_URING = 4
 
 DSR_DTYPE_BF16 = 0
 DSR_DTYPE_FP16 = 1
@@ -47,6 +53,12 @@ SIGNATURES = {
     "dsr_scatter": (_COPY_ARGS, _I),
     "dsr_gather_slots": (_SLOT_ARGS, _I),
     "dsr_scatter_slots": (_SLOT_ARGS, _I),
+    "dsr_ring_open": ([ctypes.c_char_p, _I64, _I, _I, ctypes.POINTER(_P)], _I),
+    "dsr_ring_write": ([_P, _P, _I64, _I64, _P], _I),
+    "dsr_ring_read": ([_P, _P, _I64, _I64, _P], _I),
+    "dsr_ring_uses_io_uring": ([_P], _I),
+    "dsr_ring_last_errno": ([_P], _I),
+    "dsr_ring_close": ([_P], _I),
     "dsr_scatter_rerotate": (
         _COPY_ARGS[:-1] + [_P, _P, _I, _I, _I, _I, _I, _P, _P],
         _I,

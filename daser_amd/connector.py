@@ -22,7 +22,9 @@ assembled into one request, each with its own positions).
 Extra ``kv_connector_extra_config`` keys: ``rope_theta`` (default 10000),
 ``rope_style`` ("neox" | "gptj"), ``rotary_dim`` (default head_dim),
 ``save_mode`` ("per_layer" | "deferred": one all-layer gather in
-wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry).
+wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry),
+``io_backend`` ("native": the C++ io_uring ring of libdaser_kv, default;
+"python": the threaded ring of store_io.PinnedRingIO).
 """
 
 from __future__ import annotations
@@ -198,9 +200,13 @@ class KVDataPlane:
                  rope_style: str = "neox", rotary_dim: Optional[int] = None,
                  inv_freq: Optional[np.ndarray] = None, save_mode: str = "per_layer",
                  io_slot_bytes: int = 64 << 20, io_slots: int = 4,
+                 io_backend: str = "native",
                  k_scales: Optional[torch.Tensor] = None) -> None:
         if save_mode not in ("per_layer", "deferred"):
             raise ValueError("save_mode must be 'per_layer' or 'deferred'")
+        if io_backend not in ("native", "python"):
+            raise ValueError("io_backend must be 'native' or 'python'")
+        self.io_backend = io_backend
         self.store_path = store_path
         self.rope_theta = float(rope_theta)
         self.rope_style = rope_style
@@ -219,7 +225,7 @@ class KVDataPlane:
     # -- registration (reference register_kv_caches :383-429)
     def register(self, kv_caches: dict[str, torch.Tensor], slot_size: int = 0) -> int:
         from daser_amd import ops
-        from daser_amd.store_io import PinnedRingIO, preallocate_store
+        from daser_amd.store_io import NativeRingIO, PinnedRingIO, preallocate_store
 
         self.layer_names = list(kv_caches.keys())
         self.layer_idx = {n: i for i, n in enumerate(self.layer_names)}
@@ -233,8 +239,9 @@ class KVDataPlane:
             self.rotary_dim = lay.head_dim
         preallocate_store(self.store_path, max(self.slot_bytes * 1024, 64 << 20))
         if self.io is None:
-            self.io = PinnedRingIO(self.store_path, lay.device,
-                                   slot_bytes=self._io_slot_bytes, n_slots=self._io_slots)
+            ring = NativeRingIO if self.io_backend == "native" else PinnedRingIO
+            self.io = ring(self.store_path, lay.device, slot_bytes=self._io_slot_bytes,
+                           n_slots=self._io_slots)
         return self.slot_bytes
 
     @property
@@ -361,6 +368,7 @@ class DaserConnector(KVConnectorBase_V1):
                 save_mode=extra.get("save_mode", "per_layer"),
                 io_slot_bytes=int(float(extra.get("io_slot_mb", 64)) * (1 << 20)),
                 io_slots=int(extra.get("io_slots", 4)),
+                io_backend=extra.get("io_backend", "native"),
             )
             self._meta: Optional[DaserConnectorMeta] = None
             self._store_plan: Optional[StorePlan] = None

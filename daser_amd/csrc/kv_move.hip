@@ -748,6 +748,10 @@ const char* dsr_error_string(int code) {
       return "pointer, stride or size is not a multiple of 16 bytes";
     case DSR_ERR_SHAPE:
       return "inconsistent page/row/rotation geometry";
+    case DSR_ERR_IO:
+      return "store file read or write failed (see dsr_ring_last_errno)";
+    case DSR_ERR_NOFILE:
+      return "store file not found";
     default:
       return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }

@@ -277,3 +277,127 @@ class PinnedRingIO:
 
     def __exit__(self, *_: object) -> None:
         self.close()
+
+
+class NativeRingIO:
+    """The same transfers as :class:`PinnedRingIO`, done by the native ring of
+    libdaser_kv (pinned slots, hipMemcpyAsync on a ring-owned stream,
+    io_uring or pread/pwrite from the calling thread; ``dsr_ring_*`` in
+    include/daser_kv.h). With ``device="cpu"`` the ring runs in host mode
+    (memcpy, no HIP calls).
+    """
+
+    def __init__(self, path: str, device: torch.device | str = "cuda",
+                 slot_bytes: int = 64 << 20, n_slots: int = 4, use_io_uring: bool = True,
+                 direct: bool = False) -> None:
+        import ctypes
+
+        from daser_amd import _lib
+
+        self._lib = _lib
+        self.path = path
+        self.device = torch.device(device)
+        flags = 0
+        if self.device.type != "cuda":
+            flags |= _lib.DSR_RING_HOST
+        if not use_io_uring:
+            flags |= _lib.DSR_RING_NO_URING
+        if direct:
+            flags |= _lib.DSR_RING_DIRECT
+        h = ctypes.c_void_p()
+        rc = _lib.lib().dsr_ring_open(path.encode(), int(slot_bytes), int(n_slots), flags,
+                                      ctypes.byref(h))
+        if rc == _lib.DSR_ERR_NOFILE:
+            raise FileNotFoundError(f"Store file not found: {path}")
+        _lib.check("dsr_ring_open", rc)
+        self._h = h
+        self._slot_bytes = int(slot_bytes)
+
+    @property
+    def slot_bytes(self) -> int:
+        return self._slot_bytes
+
+    @property
+    def uses_io_uring(self) -> bool:
+        return bool(self._lib.lib().dsr_ring_uses_io_uring(self._handle()))
+
+    def _handle(self):
+        if self._h is None:
+            raise StoreIOError("store I/O is closed")
+        return self._h
+
+    def _stream(self, s: Optional[torch.cuda.Stream]) -> Optional[int]:
+        if self.device.type != "cuda":
+            return None
+        return (s or torch.cuda.current_stream(self.device)).cuda_stream
+
+    def _raise(self, fn: str, rc: int) -> None:
+        if rc == self._lib.DSR_ERR_IO:
+            err = self._lib.lib().dsr_ring_last_errno(self._h)
+            raise StoreIOError(f"{fn}: {os.strerror(err) if err else 'I/O error'} on {self.path}")
+        self._lib.check(fn, rc)
+
+    def write_from_device(self, src: torch.Tensor, file_offset: int,
+                          producer: Optional[torch.cuda.Stream] = None) -> int:
+        flat = src.reshape(-1).view(torch.uint8)
+        if not flat.is_contiguous():
+            raise ValueError("source must be contiguous")
+        n = flat.numel()
+        rc = self._lib.lib().dsr_ring_write(self._handle(), flat.data_ptr(), n, int(file_offset),
+                                            self._stream(producer))
+        if rc:
+            self._raise("dsr_ring_write", rc)
+        return n
+
+    def read_into_device(self, dst: torch.Tensor, file_offset: int,
+                         consumer: Optional[torch.cuda.Stream] = None) -> int:
+        flat = dst.reshape(-1).view(torch.uint8)
+        if not flat.is_contiguous():
+            raise ValueError("destination must be contiguous")
+        n = flat.numel()
+        rc = self._lib.lib().dsr_ring_read(self._handle(), flat.data_ptr(), n, int(file_offset),
+                                           self._stream(consumer))
+        if rc:
+            self._raise("dsr_ring_read", rc)
+        return n
+
+    async def write_async(self, buf: torch.Tensor, file_offset: int,
+                          nbytes: Optional[int] = None) -> int:
+        import asyncio
+
+        src = buf.reshape(-1).view(torch.uint8)
+        if nbytes is not None:
+            src = src[:nbytes]
+        return await asyncio.get_running_loop().run_in_executor(
+            None, self.write_from_device, src, file_offset)
+
+    async def read_into_async(self, buf: torch.Tensor, file_offset: int,
+                              nbytes: Optional[int] = None) -> int:
+        import asyncio
+
+        dst = buf.reshape(-1).view(torch.uint8)
+        if nbytes is not None:
+            dst = dst[:nbytes]
+        return await asyncio.get_running_loop().run_in_executor(
+            None, self.read_into_device, dst, file_offset)
+
+    def flush(self) -> None:
+        """Writes complete before write_from_device returns; nothing pends."""
+
+    def close(self) -> None:
+        if self._h is not None:
+            rc = self._lib.lib().dsr_ring_close(self._h)
+            self._h = None
+            self._lib.check("dsr_ring_close", rc)
+
+    def __enter__(self) -> "NativeRingIO":
+        return self
+
+    def __exit__(self, *_: object) -> None:
+        self.close()
+
+    def __del__(self) -> None:  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass

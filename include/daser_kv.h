@@ -50,6 +50,8 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 #define DSR_ERR_ARG (-1)   /* null pointer, negative count, bad enum     */
 #define DSR_ERR_ALIGN (-2) /* a pointer/stride/size is not 16-byte aligned */
 #define DSR_ERR_SHAPE (-3) /* rot_dim/head_dim/page geometry inconsistent */
+#define DSR_ERR_IO (-4)    /* store-file read/write failed or came up short */
+#define DSR_ERR_NOFILE (-5) /* store file does not exist                  */
 
 /* Element types understood by the re-rotation kernel. Plain gather/scatter
  * is dtype-agnostic (raw bytes, bit-exact for every dtype incl. fp8). */
@@ -186,6 +188,54 @@ int dsr_scatter_slots(const uint64_t* layer_base, int n_layers, int64_t kv_strid
                       const int64_t* row_offsets, int n_tokens, const void* staging,
                       int64_t staging_bytes, int64_t layer_bytes, int layer0,
                       dsr_stream_t stream);
+
+/*
+ * Pinned-host staging ring between device records and the store file.
+ *
+ * Replaces the reference's kvikio layer, daser/connector/gds_transfer.py:
+ * 22-127 (GDSTransferLayer: __init__ opens an existing store file and raises
+ * FileNotFoundError otherwise, :49-50; write_async / read_into_async move a
+ * GPU buffer to / from a file offset, :72-116; close, :118-121).
+ *
+ * A transfer of n bytes is cut into slot_bytes pieces that cycle through
+ * n_slots pinned host buffers: device <-> slot copies run as
+ * hipMemcpyAsync on a ring-owned stream, file I/O as io_uring READ/WRITE
+ * submitted from the calling thread (pread/pwrite when io_uring is
+ * unavailable). Pieces overlap: while piece k is written, piece k+1 is
+ * being copied. Calls on one ring serialise on an internal mutex.
+ */
+typedef struct dsr_ring dsr_ring;
+
+#define DSR_RING_HOST 1     /* src/dst are host memory: memcpy, no HIP calls */
+#define DSR_RING_DIRECT 2   /* open the file with O_DIRECT                   */
+#define DSR_RING_NO_URING 4 /* use pread/pwrite even if io_uring works       */
+
+/* Opens `path` (must exist: DSR_ERR_NOFILE otherwise) and allocates the
+ * ring. slot_bytes <= 2^31 - 1, 1 <= n_slots <= 65535. */
+int dsr_ring_open(const char* path, int64_t slot_bytes, int n_slots, int flags,
+                  dsr_ring** out);
+
+/* Writes nbytes of `src` (device memory unless DSR_RING_HOST) at
+ * file_offset. Work enqueued on `producer` before the call is complete
+ * before the copy. Returns when every byte has been written to the file
+ * (or an error: DSR_ERR_IO, errno in dsr_ring_last_errno). */
+int dsr_ring_write(dsr_ring* ring, const void* src, int64_t nbytes, int64_t file_offset,
+                   dsr_stream_t producer);
+
+/* Reads nbytes at file_offset into `dst`. On return the file reads are done
+ * and `consumer` is ordered after the last copy into dst. A read past the end
+ * of the file is DSR_ERR_IO. */
+int dsr_ring_read(dsr_ring* ring, void* dst, int64_t nbytes, int64_t file_offset,
+                  dsr_stream_t consumer);
+
+/* 1 if transfers go through io_uring, 0 if through pread/pwrite. */
+int dsr_ring_uses_io_uring(const dsr_ring* ring);
+
+/* errno of the last failed file operation on this ring (0 if none). */
+int dsr_ring_last_errno(const dsr_ring* ring);
+
+/* Waits for the ring's copies, frees its buffers and closes the file. */
+int dsr_ring_close(dsr_ring* ring);
 
 #ifdef __cplusplus
 }

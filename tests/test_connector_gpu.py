@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from daser_amd import connector as C
-from daser_amd.store_io import PinnedRingIO, preallocate_store
+from daser_amd.store_io import NativeRingIO, PinnedRingIO, preallocate_store
 from daser_amd.workloads import KVShape
 from oracle import oracle
 from tests.helpers import rand_caches, to_bits_np
@@ -64,10 +64,11 @@ def _file_records(path, start_slot, n):
         return np.frombuffer(f.read(n * slot), dtype=np.uint8)
 
 
-@pytest.mark.parametrize("mode", ["per_layer", "deferred"])
-def test_save_writes_reference_layout(gpu, tmp_path, mode):
-    print(f"case: connector save {mode}", flush=True)
-    w, ipc = _worker(tmp_path, save_mode=mode)
+@pytest.mark.parametrize("mode,backend", [("per_layer", "native"), ("deferred", "native"),
+                                          ("per_layer", "python")])
+def test_save_writes_reference_layout(gpu, tmp_path, mode, backend):
+    print(f"case: connector save {mode} {backend}", flush=True)
+    w, ipc = _worker(tmp_path, save_mode=mode, io_backend=backend)
     caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=31)
     named = _named(caches)
     w.register_kv_caches(named)
@@ -158,3 +159,22 @@ def test_pinned_ring_device_round_trip(gpu, tmp_path):
         io.read_into_device(dst, 4096)
         torch.cuda.synchronize()
     assert torch.equal(src, dst)
+
+
+@pytest.mark.parametrize("uring", [True, False])
+def test_native_ring_device_round_trip(gpu, tmp_path, uring):
+    print(f"case: native ring uring={uring}", flush=True)
+    path = str(tmp_path / "n.store")
+    preallocate_store(path, 16 << 20)
+    src = torch.randint(0, 256, (5_000_001,), dtype=torch.uint8, device=gpu)
+    with NativeRingIO(path, gpu, slot_bytes=1 << 20, n_slots=3, use_io_uring=uring) as io:
+        src.add_(1)  # producer-stream work the ring must wait for
+        io.write_from_device(src, 65536)
+        dst = torch.zeros_like(src)
+        io.read_into_device(dst, 65536)
+        dst.add_(0)  # consumer-stream work ordered after the copies
+        torch.cuda.synchronize()
+    assert torch.equal(src, dst)
+    with open(path, "rb") as f:
+        f.seek(65536)
+        assert f.read(1000) == src[:1000].cpu().numpy().tobytes()

@@ -1,0 +1,78 @@
+"""The native staging ring (dsr_ring_*) in host mode on the CPU: io_uring and
+pread/pwrite paths, more pieces than slots, and its error reporting. The
+device path is covered by tests/test_connector_gpu.py."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from daser_amd.store_io import NativeRingIO, StoreIOError, preallocate_store
+
+
+@pytest.fixture()
+def store(tmp_path):
+    path = str(tmp_path / "daser.store")
+    preallocate_store(path, 4 << 20)
+    return path
+
+
+@pytest.mark.parametrize("uring", [True, False])
+def test_round_trip_many_pieces(store, uring):
+    rng = np.random.default_rng(uring)
+    src = torch.from_numpy(rng.integers(0, 256, 1_000_003, dtype=np.uint8))
+    with NativeRingIO(store, "cpu", slot_bytes=65536, n_slots=3, use_io_uring=uring) as io:
+        if uring:
+            assert io.uses_io_uring
+        assert io.write_from_device(src, 8192) == src.numel()
+        dst = torch.zeros_like(src)
+        io.read_into_device(dst, 8192)
+    assert torch.equal(src, dst)
+    with open(store, "rb") as f:
+        f.seek(8192)
+        assert f.read(src.numel()) == src.numpy().tobytes()
+
+
+def test_interleaved_transfers_and_single_slot(store):
+    with NativeRingIO(store, "cpu", slot_bytes=4096, n_slots=1) as io:
+        a = torch.arange(10_000, dtype=torch.int32)
+        b = -torch.arange(7_000, dtype=torch.int32)
+        io.write_from_device(a, 0)
+        io.write_from_device(b, 65536)
+        ra, rb = torch.zeros_like(a), torch.zeros_like(b)
+        io.read_into_device(rb, 65536)
+        io.read_into_device(ra, 0)
+    assert torch.equal(a, ra) and torch.equal(b, rb)
+
+
+def test_missing_file(tmp_path):
+    with pytest.raises(FileNotFoundError):
+        NativeRingIO(str(tmp_path / "absent"), "cpu")
+
+
+def test_read_past_end_is_an_error(store):
+    with NativeRingIO(store, "cpu", slot_bytes=8192, n_slots=2) as io:
+        with pytest.raises(StoreIOError):
+            io.read_into_device(torch.zeros(100_000, dtype=torch.uint8), (4 << 20) - 5000)
+        # the ring keeps working afterwards
+        t = torch.ones(10, dtype=torch.uint8)
+        io.write_from_device(t, 0)
+
+
+@pytest.mark.skipif(not os.path.exists("/dev/full"), reason="needs /dev/full")
+@pytest.mark.parametrize("uring", [True, False])
+def test_write_failure_reports_errno(uring):
+    with NativeRingIO("/dev/full", "cpu", slot_bytes=4096, n_slots=2, use_io_uring=uring) as io:
+        with pytest.raises(StoreIOError, match="space"):
+            io.write_from_device(torch.ones(20_000, dtype=torch.uint8), 0)
+
+
+def test_closed_ring_refuses(store):
+    io = NativeRingIO(store, "cpu")
+    io.close()
+    io.close()
+    with pytest.raises(StoreIOError):
+        io.write_from_device(torch.ones(4, dtype=torch.uint8), 0)
