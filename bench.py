@@ -254,6 +254,62 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
     }
 
 
+def bench_io(torch, dev, budget_bytes: int = 2 << 30, reps: int = 3) -> dict:
+    """PCIe- and file-inclusive rates of the connector's data plane on a
+    sample of config 2's shape: save = gather + device->pinned ring->file,
+    load = file->pinned ring->device + scatter, through KVDataPlane with the
+    native ring, into a store file under $TMPDIR. Not the headline value."""
+    import shutil
+    import tempfile
+
+    from daser_amd import workloads
+    from daser_amd.connector import KVDataPlane, ReqLoadSpec, ReqStoreSpec, plan_load, plan_store
+
+    shape = workloads.LLAMA3_8B
+    n_pages = max(1, budget_bytes // shape.slot_bytes)
+    nb = n_pages + 64
+    full, caches, _ = fill_caches(torch, shape, nb, "bf16", dev, seed=9)
+    named = {f"layer.{i}": c for i, c in enumerate(caches)}
+    d = tempfile.mkdtemp(prefix="daser_bench_")
+    try:
+        plane = KVDataPlane(os.path.join(d, "daser.store"), io_slot_bytes=64 << 20, io_slots=4)
+        plane.register(named)
+        rng = np.random.default_rng(3)
+        blocks = rng.permutation(nb)[:n_pages].tolist()
+        per = 16  # 256-token chunks, one transfer each
+        store = {f"r{i}": ReqStoreSpec(f"k{i}", i, min(per, n_pages - i), blocks[i:i + per],
+                                       i * shape.slot_bytes, per * 16)
+                 for i in range(0, n_pages, per)}
+        sp = plan_store(store, shape.slot_bytes)
+        arena = plane.new_store_arena(sp)
+        load = {k: ReqLoadSpec(v.chunk_key, v.start_slot, v.num_slots, v.block_ids,
+                               v.file_offset, v.token_count) for k, v in store.items()}
+        lp = plan_load(load, shape.slot_bytes)
+        ts, tl = [], []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            plane.save_all(sp, arena)
+            plane.flush(sp, arena)
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            plane.load(lp)
+            torch.cuda.synchronize()
+            tl.append(time.perf_counter() - t0)
+        uring = plane.io.uses_io_uring
+        plane.close()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+        del full, caches
+        torch.cuda.empty_cache()
+    P = n_pages * shape.slot_bytes
+    return {"payload_bytes": P, "save_GBps": round(P / min(ts) / 1e9, 2),
+            "load_GBps": round(P / min(tl) / 1e9, 2), "io_uring": bool(uring),
+            "sample": f"{n_pages} Llama-3-8B pages ({P / 1e9:.2f} GB) in 256-token chunks, "
+                      f"best of {reps}, store file under {tempfile.gettempdir()}"}
+
+
 def pmc_traffic(kernel: str, config: int, pages: int):
     """HBM bytes per launch recorded from rocprofv3 PMC runs of this same
     workload (profiles/pmc_traffic.txt), or None if not recorded."""
@@ -306,6 +362,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--configs", default="2,3")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--io", action="store_true",
+                    help="also time the PCIe/file-inclusive save and load of the "
+                         "connector's data plane on a 2 GiB sample")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 4 GiB device copy (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -408,6 +467,10 @@ def main() -> int:
         out.update({"value": round(r.get("tokens_per_s", 0.0)), "unit": "tokens/s",
                     "ms_per_step": round(r.get("kernel_ms", 0.0), 3), "dtype": "bf16",
                     "config": {"workload": workloads.CONFIG_NAMES[configs[0]]}})
+    if args.io:
+        log("[bench] io: PCIe/file-inclusive save and load")
+        out["pcie_inclusive"] = bench_io(torch, dev)
+        log(f"[bench] io: {json.dumps(out['pcie_inclusive'])}")
     if not args.no_cpu:
         log("[bench] cpu baseline (C oracle, one thread)")
         out["cpu_baseline"] = cpu_baseline()
