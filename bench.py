@@ -461,7 +461,9 @@ def main() -> int:
                            "rerotate_GBps": round(r.get("rerotate_GBps", 0.0), 1),
                            "rerotate_tokens_per_s": round(r.get("rerotate_tokens_per_s", 0.0)),
                            "rerotate_ms": round(r.get("rerotate_ms", 0.0), 4),
-                           "tokens": r["tokens"], "payload_bytes": r["payload_bytes"]}
+                           "tokens": r["tokens"], "payload_bytes": r["payload_bytes"],
+                           "traffic_rerotate": pmc_traffic("kv_scatter_rerotate_contig_kernel", 4,
+                                                           r["pages"])}
     if "value" not in out:
         r = res[configs[0]]
         out.update({"value": round(r.get("tokens_per_s", 0.0)), "unit": "tokens/s",
