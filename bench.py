@@ -310,6 +310,56 @@ def bench_io(torch, dev, budget_bytes: int = 2 << 30, reps: int = 3) -> dict:
                       f"best of {reps}, store file under {tempfile.gettempdir()}"}
 
 
+def reference_loop(torch, dev, budget_s: float = 6.0) -> dict:
+    """The reference's own copy path, timed on `dev` (the GPU, or "cpu"):
+    save = for each page, for each layer,
+        staging[off:off+n].copy_(kv[:, b].reshape(-1).view(uint8))
+    (daser/connector/daser_connector.py:625-632), load = for each page and
+    layer kv[:, b].copy_(staging[off:off+n].view(dtype).view(shape)) (:536-551),
+    over 256 Llama-3-8B pages of a 1024-block pool, repeated to ~budget_s."""
+    from daser_amd import workloads
+
+    shape = workloads.LLAMA3_8B
+    wl = workloads.ragged(shape, 4, 1024, 1024, seed=0, num_blocks=1024)
+    kv = [torch.zeros((2, 1024, 16, 8, 128), dtype=torch.bfloat16, device=dev)
+          for _ in range(shape.num_layers)]
+    staging = torch.empty(wl.staging_bytes, dtype=torch.uint8, device=dev)
+    layer = shape.layer_bytes
+    blocks = wl.page_ids.tolist()
+    offs = wl.slot_offsets.tolist()
+
+    def save():
+        for b, o in zip(blocks, offs):
+            for l, t in enumerate(kv):
+                src = t[:, b]
+                staging[o + l * layer:o + l * layer + src.nbytes].copy_(
+                    src.reshape(-1).view(torch.uint8))
+
+    def load():
+        for b, o in zip(blocks, offs):
+            for l, t in enumerate(kv):
+                dst = t[:, b]
+                dst.copy_(staging[o + l * layer:o + l * layer + dst.nbytes]
+                          .view(t.dtype).view(dst.shape))
+
+    sync = torch.cuda.synchronize if dev.type == "cuda" else (lambda: None)
+    save()
+    load()
+    sync()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        save()
+        load()
+        sync()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    P = wl.payload_bytes
+    return {"GBps": round(4 * P * n / el / 1e9, 2), "step_ms": round(el / n * 1e3, 2),
+            "sample": f"{wl.n_pages} pages x 32 layers, {n} save+load rounds in {el:.1f} s"}
+
+
 def pmc_traffic(kernel: str, config: int, pages: int):
     """HBM bytes per launch recorded from rocprofv3 PMC runs of this same
     workload (profiles/pmc_traffic.txt), or None if not recorded."""
@@ -362,6 +412,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--configs", default="2,3")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-ref-loop", action="store_true",
+                    help="skip timing the reference's per-page torch copy loop on the GPU")
     ap.add_argument("--io", action="store_true",
                     help="also time the PCIe/file-inclusive save and load of the "
                          "connector's data plane on a 2 GiB sample")
@@ -473,9 +525,18 @@ def main() -> int:
         log("[bench] io: PCIe/file-inclusive save and load")
         out["pcie_inclusive"] = bench_io(torch, dev)
         log(f"[bench] io: {json.dumps(out['pcie_inclusive'])}")
+    if not args.no_ref_loop:
+        log("[bench] reference copy loop on the GPU")
+        out["reference_loop_gpu"] = reference_loop(torch, dev)
     if not args.no_cpu:
         log("[bench] cpu baseline (C oracle, one thread)")
         out["cpu_baseline"] = cpu_baseline()
+        ncpu = len(os.sched_getaffinity(0))
+        torch.set_num_threads(ncpu)
+        log(f"[bench] reference copy loop on the CPU ({ncpu} threads)")
+        r = reference_loop(torch, torch.device("cpu"), budget_s=10.0)
+        r["threads"] = ncpu
+        out["cpu_reference_loop"] = r
     print(json.dumps(out), flush=True)
     return 0
 

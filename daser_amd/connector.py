@@ -136,6 +136,7 @@ class LoadPlan:
     deltas: list[int]  # table order
     reads: list[tuple[int, int, int]]  # (arena_off, nbytes, file_off)
     arena_bytes: int
+    page_read: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int64))  # read of each page
 
 
 def plan_store(reqs: dict[str, ReqStoreSpec], slot_bytes: int) -> StorePlan:
@@ -159,7 +160,7 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
     segment scatters record j into block_ids[block_offset + j]. A segment
     whose new position differs from its stored one gets a rotation table for
     delta = new_pos - pos_offset (reference :498-551 for the unrotated part)."""
-    ids, offs, ridx, reads = [], [], [], []
+    ids, offs, ridx, reads, page_read = [], [], [], [], []
     table: dict[int, int] = {}
     base = 0
     for spec in reqs.values():
@@ -179,9 +180,11 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
                 ids.append(blocks[seg.block_offset + j])
                 offs.append(base + j * slot_bytes)
                 ridx.append(t)
+                page_read.append(len(reads) - 1)
             base += n * slot_bytes
     return LoadPlan(np.asarray(ids, np.int32), np.asarray(offs, np.int64),
-                    np.asarray(ridx, np.int32), list(table.keys()), reads, base)
+                    np.asarray(ridx, np.int32), list(table.keys()), reads, base,
+                    np.asarray(page_read, np.int64))
 
 
 # ---------------------------------------------------------------------------
@@ -276,22 +279,38 @@ class KVDataPlane:
         return keys
 
     # -- load
-    def load(self, plan: LoadPlan) -> None:
+    def load(self, plan: LoadPlan, batch_bytes: int = 256 << 20) -> None:
+        """Reads the plan's records and scatters them. Reads are grouped into
+        batches of about ``batch_bytes``; each batch is scattered as soon as
+        it has landed, so the GPU scatters batch i while the ring reads
+        batch i+1."""
         from daser_amd import ops, position
 
         if plan.page_ids.size == 0:
             return
         arena = torch.empty(plan.arena_bytes, dtype=torch.uint8, device=self.device)
-        for off, nbytes, file_off in plan.reads:
+        tabs = None
+        if plan.deltas:
+            tabs = position.delta_tables(plan.deltas, self.rotary_dim, self.rope_theta,
+                                         inv_freq=self.inv_freq, device=self.device)
+        page_read = plan.page_read if plan.page_read.size else np.zeros(plan.page_ids.size,
+                                                                         np.int64)
+        first, acc = 0, 0
+        for r, (off, nbytes, file_off) in enumerate(plan.reads):
             self.io.read_into_device(arena[off:off + nbytes], file_off)
-        if not plan.deltas:
-            ops.scatter(self.table, plan.page_ids, plan.src_offsets, arena)
-            return
-        tabs = position.delta_tables(plan.deltas, self.rotary_dim, self.rope_theta,
-                                     inv_freq=self.inv_freq, device=self.device)
-        ops.scatter_rerotate(self.table, plan.page_ids, plan.src_offsets, arena, tabs,
-                             plan.rope_idx, rot_dim=self.rotary_dim, style=self.rope_style,
-                             k_scale=self.k_scales)
+            acc += nbytes
+            if acc < batch_bytes and r + 1 < len(plan.reads):
+                continue
+            sel = np.nonzero((page_read >= first) & (page_read <= r))[0]
+            first, acc = r + 1, 0
+            if sel.size == 0:
+                continue
+            if tabs is None:
+                ops.scatter(self.table, plan.page_ids[sel], plan.src_offsets[sel], arena)
+            else:
+                ops.scatter_rerotate(self.table, plan.page_ids[sel], plan.src_offsets[sel],
+                                     arena, tabs, plan.rope_idx[sel], rot_dim=self.rotary_dim,
+                                     style=self.rope_style, k_scale=self.k_scales)
 
     def close(self) -> None:
         if self.io is not None:
@@ -504,11 +523,17 @@ class DaserConnector(KVConnectorBase_V1):
         self._saved_layers.add(self._plane.layer_idx[layer_name])
 
     def wait_for_save(self) -> None:
-        """Writes each request's records to the store, then commits."""
+        """Writes each request's records to the store, then commits. Layers
+        whose save_kv_layer never ran this step are gathered here, so no
+        record is written with unset bytes."""
         if self._store_plan is None or self._store_arena is None:
             return
         if self._plane.save_mode == "deferred":
             self._plane.save_all(self._store_plan, self._store_arena)
+        else:
+            for name, idx in self._plane.layer_idx.items():
+                if idx not in self._saved_layers:
+                    self._plane.save_layer(name, self._store_plan, self._store_arena)
         self._plane.flush(self._store_plan, self._store_arena)
         self._store_plan = None
         self._store_arena = None

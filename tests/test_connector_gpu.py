@@ -178,3 +178,51 @@ def test_native_ring_device_round_trip(gpu, tmp_path, uring):
     with open(path, "rb") as f:
         f.seek(65536)
         assert f.read(1000) == src[:1000].cpu().numpy().tobytes()
+
+
+def test_missing_layer_saves_are_completed(gpu, tmp_path):
+    """A layer whose save_kv_layer never ran is gathered in wait_for_save."""
+    print("case: connector missing layer", flush=True)
+    w, _ = _worker(tmp_path)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=34)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    w.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_store=_store_reqs()))
+    for i, (name, t) in enumerate(named.items()):
+        if i != 1:
+            w.save_kv_layer(name, t, None)
+    w.wait_for_save()
+    host = [to_bits_np(c, "bf16") for c in caches]
+    ref = np.zeros(3 * SHAPE.slot_bytes, dtype=np.uint8)
+    oracle.gather(host, [5, 9, 2], np.arange(3) * SHAPE.slot_bytes, ref, SHAPE.layer_bytes)
+    assert np.array_equal(_file_records(tmp_path / "daser.store", 3, 3), ref)
+    w.shutdown()
+
+
+def test_batched_load_matches_single_batch(gpu, tmp_path):
+    """Scattering per batch while later batches are read gives the same
+    caches as one scatter after all reads."""
+    print("case: batched load", flush=True)
+    w, _ = _worker(tmp_path, rope_theta=500000.0)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=35)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    _save(w, named, _store_reqs())
+    slot = SHAPE.slot_bytes
+    reqs = {
+        "x": C.ReqLoadSpec("ka", 3, 3, [1, 12, 4], 3 * slot, 40, pos_offset=0, new_pos=300),
+        "y": C.ReqLoadSpec("kb", 10, 1, [0], 10 * slot, 16),
+    }
+    outs = []
+    for batch in (1, 1 << 30):
+        fresh = [torch.zeros_like(c) for c in caches]
+        p = C.KVDataPlane(str(tmp_path / "daser.store"), rope_theta=500000.0)
+        p.register(_named(fresh))
+        p.load(C.plan_load(reqs, slot), batch_bytes=batch)
+        torch.cuda.synchronize()
+        outs.append(fresh)
+        p.close()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert torch.equal(outs[0][0][:, 0], caches[0][:, 7])
+    w.shutdown()
