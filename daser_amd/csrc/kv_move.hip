@@ -34,7 +34,8 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;     // 4 wave64 per workgroup
 constexpr int kGatherUnroll = 16;  // 16-byte vectors per lane per half per round
-constexpr int kScatterUnroll = 8;
+constexpr int kScatterUnroll = 16;
+constexpr int kRotCopyUnroll = 8;  // copy of unrotated pages inside the re-rotation kernels
 constexpr int kRotUnroll = 4;      // rotation tasks per lane per round (pair-task kernel)
 // Workgroups per CU for the re-rotation kernel, applied with dynamic LDS
 // sized from the CU's LDS capacity (env DSR_ROT_WG_PER_CU overrides, for
@@ -424,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
   const int ti = ra.rope_idx[p];
   const int64_t pb = ra.u.page_bytes;
   if (ti < 0 || ti >= ra.n_tables) {
-    copy_halves<kScatterUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
     return;
   }
   const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
@@ -541,7 +542,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
   const int ti = ra.rope_idx[p];
   const int64_t pb = ra.u.page_bytes;
   if (ti < 0 || ti >= ra.n_tables) {
-    copy_halves<kScatterUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
     return;
   }
   constexpr int U = rot_contig_unroll<DT>();
