@@ -368,3 +368,31 @@ def test_slots_gather_equals_page_gather_for_full_pages(gpu):
                      ops.token_row_offsets(toks, shape.slot_bytes, 16, 8 * 128 * 2), b)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_large_page_geometry(gpu):
+    """512 KiB pages (block_size 32, 32 heads, head_dim 256): multi-round
+    copies and a 32-lane neox partner distance."""
+    print("case: large pages", flush=True)
+    shape = KVShape(2, 32, 256, 32, 2)
+    wl = workloads.ragged(shape, 3, 1, 100, seed=70, pool_slack=1.5)
+    caches = rand_caches(shape, wl.num_blocks, "bf16", gpu, seed=71)
+    staging, ref = _gather_both(wl, caches, "bf16", gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(staging.cpu().numpy(), ref)
+    dst = [torch.zeros_like(c) for c in caches]
+    ridx = np.zeros(wl.n_pages, np.int32)
+    tabs = position.delta_tables([999], 256, 500000.0, device=gpu)
+    ops.scatter_rerotate(ops.LayerTable(dst), wl.page_ids, wl.slot_offsets, staging, tabs, ridx)
+    dref = [np.zeros_like(to_bits_np(c, "bf16")) for c in caches]
+    oracle.scatter_rerotate(dref, wl.page_ids, wl.slot_offsets, ref, shape.layer_bytes,
+                            dtype=oracle.BF16, rot_dim=256, style=oracle.NEOX,
+                            stored_pos=np.zeros(wl.n_pages, np.int64),
+                            new_pos=np.full(wl.n_pages, 999), rotate=np.ones(wl.n_pages),
+                            theta=500000.0)
+    torch.cuda.synchronize()
+    for d, r in zip(dst, dref):
+        got = to_bits_np(d, "bf16")
+        assert np.array_equal(got[1], r[1])
+        ok, msg = oracle.rotation_within_tolerance(got[0], r[0], oracle.BF16)
+        assert ok, msg
