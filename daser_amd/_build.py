@@ -17,6 +17,8 @@ ROOT = os.path.dirname(HERE)
 SRCS = [os.path.join(HERE, "csrc", "kv_move.hip"), os.path.join(HERE, "csrc", "store_ring.cpp")]
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "libdaser_kv.so")
+PROBE_SRC = os.path.join(HERE, "csrc", "hbm_probe.hip")
+PROBE_OUT = os.path.join(HERE, "hbm_probe")
 
 ARCH = "gfx950"
 
@@ -52,6 +54,15 @@ def build(verbose: bool = False) -> str:
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
     os.replace(tmp, OUT)
+    # the HBM ceiling probe (a stand-alone executable, not part of the library)
+    flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
+    cmd = [hipcc(), *flags, PROBE_SRC, "-o", PROBE_OUT + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(PROBE_OUT + ".tmp", PROBE_OUT)
     return OUT
 
 
