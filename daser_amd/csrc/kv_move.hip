@@ -86,6 +86,22 @@ __device__ __forceinline__ int64_t xcd_unit(int64_t n_units) {
   return u < n_units ? u : -1;
 }
 
+// Workgroup -> unit for the kernels that write the paged cache (scatter and
+// re-rotation). The unit list is walked layer-major (all pages of layer 0,
+// then layer 1, ...) and each XCD takes one contiguous eighth of it, so each
+// XCD writes the (destination-ordered) pages of a few layers in sequence
+// instead of interleaving 32 layer regions. Measured in-process against the
+// page-major order: -1.6% scatter and -1.8% re-rotation time at the
+// Llama-3-8B shapes. Returns the page-major unit index (page * n_layers +
+// layer), or -1 past the end.
+__device__ __forceinline__ int64_t layer_major_unit(int64_t n_units, int n_layers) {
+  const int64_t v = xcd_unit(n_units);
+  if (v < 0) return -1;
+  const int64_t n_pages = n_units / n_layers;
+  const int64_t l = v / n_pages;
+  return (v - l * n_pages) * n_layers + l;
+}
+
 // Resolves the cache-side and record-side addresses of unit (page, layer),
 // page-major. Returns false when the unit's block id or record range is out
 // of bounds (the unit is then skipped, never touched).
@@ -159,12 +175,14 @@ __global__ __launch_bounds__(kThreads) void kv_gather_kernel(UnitArgs a) {
                              a.page_bytes);
 }
 
-// Scatter: one workgroup per unit in page-list order (the host orders the
-// list by destination block, which keeps the page writes near-sequential).
+// Scatter: one workgroup per unit, layer-major per XCD (the host orders the
+// page list by destination block, which keeps each layer's page writes
+// near-sequential).
 __global__ __launch_bounds__(kThreads) void kv_scatter_kernel(UnitArgs a) {
   uint8_t *cache, *rec;
   int l;
-  if (!unit_addresses(a, blockIdx.x, &cache, &rec, &l)) return;
+  const int64_t u = layer_major_unit(a.n_units, a.n_layers);
+  if (u < 0 || !unit_addresses(a, u, &cache, &rec, &l)) return;
   copy_halves<kScatterUnroll>(rec, rec + a.page_bytes, cache, cache + a.kv_stride,
                               a.page_bytes);
 }
@@ -420,8 +438,9 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
   __shared__ float2 tab[kMaxRotHalf];
   uint8_t *cache, *rec;
   int l;
-  if (!unit_addresses(ra.u, blockIdx.x, &cache, &rec, &l)) return;
-  const int64_t p = (int64_t)blockIdx.x / ra.u.n_layers;
+  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
+  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  const int64_t p = u / ra.u.n_layers;
   const int ti = ra.rope_idx[p];
   const int64_t pb = ra.u.page_bytes;
   if (ti < 0 || ti >= ra.n_tables) {
@@ -537,8 +556,9 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
   __shared__ float2 tab[kMaxRotHalf];
   uint8_t *cache, *rec;
   int l;
-  if (!unit_addresses(ra.u, blockIdx.x, &cache, &rec, &l)) return;
-  const int64_t p = (int64_t)blockIdx.x / ra.u.n_layers;
+  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
+  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  const int64_t p = u / ra.u.n_layers;
   const int ti = ra.rope_idx[p];
   const int64_t pb = ra.u.page_bytes;
   if (ti < 0 || ti >= ra.n_tables) {
@@ -788,7 +808,8 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   UnitArgs a = make_unit(layer_base, n_layers, kv_stride, page_stride, page_bytes,
                          num_blocks, page_ids, slot_offsets, n_pages, staging,
                          staging_bytes, layer_bytes, layer0);
-  kv_scatter_kernel<<<(unsigned)a.n_units, kThreads, 0, (hipStream_t)stream>>>(a);
+  const unsigned grid = (unsigned)((a.n_units + kXcds - 1) / kXcds * kXcds);
+  kv_scatter_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(a);
   return (int)hipGetLastError();
 }
 
@@ -855,7 +876,7 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
   ra.rot_vecs = rot_dim * esize / 16;
   ra.half_vecs = rope_style == DSR_ROPE_NEOX ? rot_dim / 2 * esize / 16 : 0;
   ra.k_scale = k_scale;
-  const unsigned grid = (unsigned)ra.u.n_units;
+  const unsigned grid = (unsigned)((ra.u.n_units + kXcds - 1) / kXcds * kXcds);
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case DSR_DTYPE_BF16:
