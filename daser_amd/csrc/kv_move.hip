@@ -624,7 +624,14 @@ constexpr int kRowUnroll = 2;   // 64-vector slices of a row per round
 // token's whole K and V rows, and 4 tokens' rows are in flight together.
 template <bool kGather>
 __global__ __launch_bounds__(kThreads) void kv_slots_kernel(SlotArgs a) {
-  const int64_t unit = blockIdx.x;
+  // the scatter writes the paged cache: layer-major per XCD, as the page
+  // scatter (-2.4% in-process); the gather keeps the identity order
+  int64_t unit = blockIdx.x;
+  if (!kGather) {
+    const int64_t nu = ((int64_t)a.n_tokens + kTokPerWg - 1) / kTokPerWg * a.n_layers;
+    unit = layer_major_unit(nu, a.n_layers);
+    if (unit < 0) return;
+  }
   const int64_t tb = unit / a.n_layers;
   const int l = (int)(unit - tb * a.n_layers);
   const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
@@ -924,7 +931,8 @@ int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t 
   a.n_layers = n_layers;
   a.layer0 = layer0;
   a.block_size = block_size;
-  const unsigned grid = (unsigned)(blocks * n_layers);
+  const int64_t units = blocks * n_layers;
+  const unsigned grid = (unsigned)(gather ? units : (units + kXcds - 1) / kXcds * kXcds);
   if (gather)
     kv_slots_kernel<true><<<grid, kThreads, 0, (hipStream_t)stream>>>(a);
   else
