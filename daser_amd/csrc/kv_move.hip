@@ -39,13 +39,13 @@ constexpr int kRotCopyUnroll = 8;  // copy of unrotated pages inside the re-rota
 constexpr int kRotUnroll = 4;      // rotation tasks per lane per round (pair-task kernel)
 // Workgroups per CU for the re-rotation kernel, applied with dynamic LDS
 // sized from the CU's LDS capacity (env DSR_ROT_WG_PER_CU overrides, for
-// tuning). Measured at the Llama-3-8B shape, interleaved A/B on one MI355X:
-// 16-bit K (64 KiB per unit) runs best at 2 per CU (7.79-7.86 ms vs
-// 8.13-8.18 ms at 6 or uncapped); e4m3 (32 KiB per unit) at 6 per CU
-// (22.3 ms vs 28.4 ms at 2).
+// tuning). Measured in-process at the Llama-3-8B shapes: 16-bit K (64 KiB
+// per unit) runs best at 2-3 per CU (7.67 ms vs 7.87 ms at 4-8 and 11.0 ms
+// at 1); e4m3 (32 KiB per unit) at 4 per CU (24.17 ms; 24.4-24.5 ms at 6-12,
+// 30.1 ms at 2).
 template <int DT>
 constexpr int rot_wg_per_cu() {
-  return DT == DSR_DTYPE_FP8_E4M3 ? 6 : 2;
+  return DT == DSR_DTYPE_FP8_E4M3 ? 4 : 2;
 }
 constexpr int kMaxRotHalf = 512;   // LDS table capacity: rot_dim <= 1024
 constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
