@@ -24,7 +24,9 @@ Extra ``kv_connector_extra_config`` keys: ``rope_theta`` (default 10000),
 ``save_mode`` ("per_layer" | "deferred": one all-layer gather in
 wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry),
 ``io_backend`` ("native": the C++ io_uring ring of libdaser_kv, default;
-"python": the threaded ring of store_io.PinnedRingIO).
+"python": the threaded ring of store_io.PinnedRingIO), ``save_stream``
+("side": per-layer gathers on a side stream after the layer's KV writes,
+overlapping later layers, default; "current": on the model's stream).
 """
 
 from __future__ import annotations
@@ -124,6 +126,7 @@ class StorePlan:
     slot_offsets: np.ndarray  # int64 record offsets in the arena
     transfers: list[tuple[str, int, int, int]]  # (chunk_key, arena_off, nbytes, file_off)
     arena_bytes: int
+    device_tables: Optional[tuple] = None  # (page_ids, slot_offsets) on the device
 
 
 @dataclass
@@ -203,13 +206,17 @@ class KVDataPlane:
                  rope_style: str = "neox", rotary_dim: Optional[int] = None,
                  inv_freq: Optional[np.ndarray] = None, save_mode: str = "per_layer",
                  io_slot_bytes: int = 64 << 20, io_slots: int = 4,
-                 io_backend: str = "native",
+                 io_backend: str = "native", save_stream: str = "side",
                  k_scales: Optional[torch.Tensor] = None) -> None:
         if save_mode not in ("per_layer", "deferred"):
             raise ValueError("save_mode must be 'per_layer' or 'deferred'")
         if io_backend not in ("native", "python"):
             raise ValueError("io_backend must be 'native' or 'python'")
+        if save_stream not in ("side", "current"):
+            raise ValueError("save_stream must be 'side' or 'current'")
         self.io_backend = io_backend
+        self.save_stream = save_stream
+        self._side: Optional[torch.cuda.Stream] = None
         self.store_path = store_path
         self.rope_theta = float(rope_theta)
         self.rope_style = rope_style
@@ -241,6 +248,8 @@ class KVDataPlane:
         if self.rotary_dim is None:
             self.rotary_dim = lay.head_dim
         preallocate_store(self.store_path, max(self.slot_bytes * 1024, 64 << 20))
+        if self.save_stream == "side" and lay.device.type == "cuda" and self._side is None:
+            self._side = torch.cuda.Stream(lay.device)  # default priority
         if self.io is None:
             ring = NativeRingIO if self.io_backend == "native" else PinnedRingIO
             self.io = ring(self.store_path, lay.device, slot_bytes=self._io_slot_bytes,
@@ -253,28 +262,60 @@ class KVDataPlane:
 
     # -- save
     def new_store_arena(self, plan: StorePlan) -> torch.Tensor:
-        return torch.empty(max(plan.arena_bytes, 16), dtype=torch.uint8, device=self.device)
+        """Staging arena of a step's store requests. The plan's page tables are
+        validated and uploaded once here and reused by every layer's gather."""
+        from daser_amd import ops
+
+        arena = torch.empty(max(plan.arena_bytes, 16), dtype=torch.uint8, device=self.device)
+        if plan.page_ids.size:
+            ops._validate(self.table.layout, plan.page_ids, plan.slot_offsets, arena, 0,
+                          self.table.layout.num_layers, True)
+            plan.device_tables = (torch.from_numpy(plan.page_ids).to(self.device),
+                                  torch.from_numpy(plan.slot_offsets).to(self.device))
+        return arena
+
+    def _on_save_stream(self, arena: torch.Tensor):
+        """Context for the gathers: the side stream, ordered after the work
+        the model's stream has enqueued so far (the layer's KV writes)."""
+        import contextlib
+
+        if self._side is None:
+            return contextlib.nullcontext()
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self._side.wait_event(ev)
+        arena.record_stream(self._side)
+        return torch.cuda.stream(self._side)
 
     def save_layer(self, layer_name: str, plan: StorePlan, arena: torch.Tensor) -> None:
+        """Gathers one layer's pages of every store request. With
+        save_stream="side" the gather runs on a side stream after the KV
+        writes already enqueued, overlapping the model's later layers."""
         from daser_amd import ops
 
         if plan.page_ids.size == 0:
             return
         l = self.layer_idx[layer_name]
-        ops.gather(self.table, plan.page_ids, plan.slot_offsets, arena, layers=(l, 1))
+        ids, offs = plan.device_tables
+        with self._on_save_stream(arena):
+            ops.gather(self.table, ids, offs, arena, layers=(l, 1))
 
     def save_all(self, plan: StorePlan, arena: torch.Tensor) -> None:
         from daser_amd import ops
 
-        if plan.page_ids.size:
-            ops.gather(self.table, plan.page_ids, plan.slot_offsets, arena)
+        if plan.page_ids.size == 0:
+            return
+        ids, offs = plan.device_tables
+        with self._on_save_stream(arena):
+            ops.gather(self.table, ids, offs, arena)
 
     def flush(self, plan: StorePlan, arena: torch.Tensor) -> list[str]:
         """Writes each request's records at its file offset; returns the
         chunk keys written (to commit)."""
         keys = []
+        producer = self._side  # None: the current stream
         for key, off, nbytes, file_off in plan.transfers:
-            self.io.write_from_device(arena[off:off + nbytes], file_off)
+            self.io.write_from_device(arena[off:off + nbytes], file_off, producer)
             keys.append(key)
         return keys
 
@@ -388,6 +429,7 @@ class DaserConnector(KVConnectorBase_V1):
                 io_slot_bytes=int(float(extra.get("io_slot_mb", 64)) * (1 << 20)),
                 io_slots=int(extra.get("io_slots", 4)),
                 io_backend=extra.get("io_backend", "native"),
+                save_stream=extra.get("save_stream", "side"),
             )
             self._meta: Optional[DaserConnectorMeta] = None
             self._store_plan: Optional[StorePlan] = None

@@ -64,11 +64,13 @@ def _file_records(path, start_slot, n):
         return np.frombuffer(f.read(n * slot), dtype=np.uint8)
 
 
-@pytest.mark.parametrize("mode,backend", [("per_layer", "native"), ("deferred", "native"),
-                                          ("per_layer", "python")])
-def test_save_writes_reference_layout(gpu, tmp_path, mode, backend):
-    print(f"case: connector save {mode} {backend}", flush=True)
-    w, ipc = _worker(tmp_path, save_mode=mode, io_backend=backend)
+@pytest.mark.parametrize("mode,backend,stream", [
+    ("per_layer", "native", "side"), ("deferred", "native", "side"),
+    ("per_layer", "python", "side"), ("per_layer", "native", "current"),
+    ("deferred", "python", "current")])
+def test_save_writes_reference_layout(gpu, tmp_path, mode, backend, stream):
+    print(f"case: connector save {mode} {backend} {stream}", flush=True)
+    w, ipc = _worker(tmp_path, save_mode=mode, io_backend=backend, save_stream=stream)
     caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=31)
     named = _named(caches)
     w.register_kv_caches(named)
