@@ -436,6 +436,7 @@ class DaserConnector(KVConnectorBase_V1):
             self._store_arena: Optional[torch.Tensor] = None
             self._saved_layers: set[int] = set()
             self._pending_commits: set[str] = set()
+            self._flushed = False
             self._bg = _BgLoop()
 
     # ------------------------------------------------------------ scheduler
@@ -524,6 +525,7 @@ class DaserConnector(KVConnectorBase_V1):
         self._store_arena = None
         self._saved_layers = set()
         self._pending_commits = set()
+        self._flushed = False
 
     def clear_connector_metadata(self) -> None:
         super().clear_connector_metadata()
@@ -543,7 +545,8 @@ class DaserConnector(KVConnectorBase_V1):
         return
 
     def _ensure_store_plan(self) -> bool:
-        if self._meta is None or not self._meta.reqs_to_store or self._plane.table is None:
+        if (self._meta is None or not self._meta.reqs_to_store or self._plane.table is None
+                or self._flushed):
             return False
         if self._store_plan is None:
             self._store_plan = plan_store(self._meta.reqs_to_store, self._slot_size)
@@ -566,10 +569,13 @@ class DaserConnector(KVConnectorBase_V1):
 
     def wait_for_save(self) -> None:
         """Writes each request's records to the store, then commits. Layers
-        whose save_kv_layer never ran this step are gathered here, so no
+        whose save_kv_layer never ran this step (all of them under full
+        graph replay, which skips per-layer hooks) are gathered here, so no
         record is written with unset bytes."""
-        if self._store_plan is None or self._store_arena is None:
+        if self._flushed or not self._ensure_store_plan():
             return
+        for spec in self._meta.reqs_to_store.values():
+            self._pending_commits.add(spec.chunk_key)
         if self._plane.save_mode == "deferred":
             self._plane.save_all(self._store_plan, self._store_arena)
         else:
@@ -579,6 +585,7 @@ class DaserConnector(KVConnectorBase_V1):
         self._plane.flush(self._store_plan, self._store_arena)
         self._store_plan = None
         self._store_arena = None
+        self._flushed = True
         if self._pending_commits:
             keys = list(self._pending_commits)
 

@@ -228,3 +228,21 @@ def test_batched_load_matches_single_batch(gpu, tmp_path):
         assert torch.equal(a, b)
     assert torch.equal(outs[0][0][:, 0], caches[0][:, 7])
     w.shutdown()
+
+
+def test_save_without_layer_hooks_and_repeated_wait(gpu, tmp_path):
+    """Under full graph replay no save_kv_layer runs: wait_for_save gathers
+    every layer itself; a second wait_for_save in the step is a no-op."""
+    print("case: connector save without hooks", flush=True)
+    w, ipc = _worker(tmp_path)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=36)
+    w.register_kv_caches(_named(caches))
+    w.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_store=_store_reqs()))
+    w.wait_for_save()
+    w.wait_for_save()
+    host = [to_bits_np(c, "bf16") for c in caches]
+    ref = np.zeros(3 * SHAPE.slot_bytes, dtype=np.uint8)
+    oracle.gather(host, [5, 9, 2], np.arange(3) * SHAPE.slot_bytes, ref, SHAPE.layer_bytes)
+    assert np.array_equal(_file_records(tmp_path / "daser.store", 3, 3), ref)
+    assert sorted(ipc.committed) == ["ka", "kb"]  # committed once
+    w.shutdown()
