@@ -37,7 +37,7 @@ import logging
 import math
 import threading
 from dataclasses import dataclass, field
-from typing import Any, Optional, Sequence
+from typing import Any, Optional
 
 import numpy as np
 import torch

@@ -227,7 +227,7 @@ def gather(
     ``layers=(first, count)`` restricts the launch to a layer range; the
     record index of table layer ``first + i`` is ``layer0 + first + i``.
     """
-    args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers,
+    args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers,
                             records_written=True)
     rc = _lib.lib().dsr_gather(*args, _stream_handle(table.layout.device))
     _lib.check("dsr_gather", rc)
@@ -244,7 +244,7 @@ def scatter(
 ) -> None:
     """Unpacks slot records into pages (reference load loop, :536-551)."""
     page_ids, slot_offsets, _ = dest_order(page_ids, slot_offsets)
-    args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
+    args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
     rc = _lib.lib().dsr_scatter(*args, _stream_handle(table.layout.device))
     _lib.check("dsr_scatter", rc)
 
@@ -284,9 +284,9 @@ def scatter_rerotate(
     if ridx is not None and ridx.size and (ridx.max() >= cos_sin.shape[0] or ridx.min() < -1):
         raise IndexError("rope_idx outside [-1, n_tables)")
     page_ids, slot_offsets, rope_idx = dest_order(page_ids, slot_offsets, rope_idx)
-    args, keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
+    args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
     ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")
-    if ridx_d.numel() != keep[0].numel():
+    if ridx_d.numel() != _tables[0].numel():
         raise ValueError("rope_idx and page_ids differ in length")
     ks_ptr = None
     if lay.dtype == torch.float8_e4m3fn:
@@ -358,7 +358,7 @@ def gather_slots(table: LayerTable, slot_mapping, row_offsets, staging: torch.Te
     """Token-granular gather driven by vLLM's slot_mapping (-1 = padding):
     each valid token's K and V rows of every layer go to its record rows at
     ``row_offsets[t]`` (see :func:`token_row_offsets`)."""
-    args, keep = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, True)
+    args, _tables = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, True)
     rc = _lib.lib().dsr_gather_slots(*args, _stream_handle(table.layout.device))
     _lib.check("dsr_gather_slots", rc)
 
@@ -372,7 +372,7 @@ def scatter_slots(table: LayerTable, slot_mapping, row_offsets, staging: torch.T
     if sm is not None and ro is not None and sm.size:
         order = np.argsort(sm, kind="stable")
         slot_mapping, row_offsets = sm[order], ro[order]
-    args, keep = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, False)
+    args, _tables = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, False)
     rc = _lib.lib().dsr_scatter_slots(*args, _stream_handle(table.layout.device))
     _lib.check("dsr_scatter_slots", rc)
 

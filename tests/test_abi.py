@@ -3,7 +3,6 @@ declares, and rejects bad arguments before touching the device."""
 
 from __future__ import annotations
 
-import ctypes
 import os
 import re
 
