@@ -8,13 +8,14 @@ launch covering every page of every request over all 32 layers.
 
 value = algorithmic bytes of the step (gather reads P, writes P; scatter the
 same: 4P) / step time, inputs resident in HBM. The fused re-rotate+scatter of
-config 3 (RAG reuse) is reported beside it in tokens/s.
+configs 3 (RAG reuse), 4 (e4m3) and 5 (70B share) are reported beside it.
 
 Per-kernel durations come from HIP events recorded on the launch stream
 around every timed launch. cpu_baseline times the C oracle (one thread) on a
 bounded sample of the same shape on the host.
 
 Usage: python bench.py [--steps K] [--warmup W] [--configs 2,3,4,5] [--no-cpu]
+                       [--no-ref-loop] [--io] [--calibrate]
 """
 
 from __future__ import annotations
@@ -409,7 +410,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="2,3")
+    ap.add_argument("--configs", default="2,3,4,5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ref-loop", action="store_true",
                     help="skip timing the reference's per-page torch copy loop on the GPU")
