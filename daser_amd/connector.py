@@ -21,6 +21,7 @@ assembled into one request, each with its own positions).
 
 Extra ``kv_connector_extra_config`` keys: ``rope_theta`` (default 10000),
 ``rope_style`` ("neox" | "gptj"), ``rotary_dim`` (default head_dim),
+``rope_scaling`` (the model's HF ``rope_scaling`` dict: linear, llama3, yarn),
 ``save_mode`` ("per_layer" | "deferred": one all-layer gather in
 wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry),
 ``io_backend`` ("native": the C++ io_uring ring of libdaser_kv, default;
@@ -204,7 +205,8 @@ class KVDataPlane:
 
     def __init__(self, store_path: str, *, rope_theta: float = 10000.0,
                  rope_style: str = "neox", rotary_dim: Optional[int] = None,
-                 inv_freq: Optional[np.ndarray] = None, save_mode: str = "per_layer",
+                 inv_freq: Optional[np.ndarray] = None, rope_scaling: Optional[dict] = None,
+                 save_mode: str = "per_layer",
                  io_slot_bytes: int = 64 << 20, io_slots: int = 4,
                  io_backend: str = "native", save_stream: str = "side",
                  k_scales: Optional[torch.Tensor] = None) -> None:
@@ -222,6 +224,15 @@ class KVDataPlane:
         self.rope_style = rope_style
         self.rotary_dim = rotary_dim
         self.inv_freq = inv_freq
+        self.rope_scaling = rope_scaling
+        if rope_scaling and inv_freq is None:
+            from daser_amd.position import inv_freq_for
+
+            # Unsupported scalings fail here, not at the first load.
+            probe_dim = int(rotary_dim) if rotary_dim else 2
+            scaled = inv_freq_for(rope_scaling, probe_dim, rope_theta)
+            if rotary_dim:
+                self.inv_freq = scaled
         self.save_mode = save_mode
         self._io_slot_bytes = io_slot_bytes
         self._io_slots = io_slots
@@ -247,6 +258,10 @@ class KVDataPlane:
         self.slot_bytes = derived
         if self.rotary_dim is None:
             self.rotary_dim = lay.head_dim
+        if self.inv_freq is None and self.rope_scaling:
+            from daser_amd.position import inv_freq_for
+
+            self.inv_freq = inv_freq_for(self.rope_scaling, self.rotary_dim, self.rope_theta)
         preallocate_store(self.store_path, max(self.slot_bytes * 1024, 64 << 20))
         if self.save_stream == "side" and lay.device.type == "cuda" and self._side is None:
             self._side = torch.cuda.Stream(lay.device)  # default priority
@@ -425,6 +440,7 @@ class DaserConnector(KVConnectorBase_V1):
                 rope_theta=float(extra.get("rope_theta", 10000.0)),
                 rope_style=extra.get("rope_style", "neox"),
                 rotary_dim=extra.get("rotary_dim"),
+                rope_scaling=extra.get("rope_scaling"),
                 save_mode=extra.get("save_mode", "per_layer"),
                 io_slot_bytes=int(float(extra.get("io_slot_mb", 64)) * (1 << 20)),
                 io_slots=int(extra.get("io_slots", 4)),

@@ -78,6 +78,62 @@ def llama3_inv_freq(
     return np.where(mid, (1 - smooth) * inv / factor + smooth * inv, scaled)
 
 
+def yarn_inv_freq(rot_dim: int, theta: float, factor: float, original_max_position: int,
+                  beta_fast: float = 32.0, beta_slow: float = 1.0,
+                  truncate: bool = True) -> np.ndarray:
+    """YaRN frequencies (Peng et al. 2023, "YaRN: Efficient Context Window
+    Extension"): dimensions rotating faster than beta_fast turns over the
+    original context keep their frequency, slower than beta_slow are
+    interpolated by 1/factor, a linear ramp in between. The attention
+    magnitude factor of YaRN scales cos/sin at prefill; a delta rotation is
+    pure, so that factor is not part of the re-rotation table."""
+    import math
+
+    inv = rope_inv_freq(rot_dim, theta)
+
+    def corr_dim(n_rot: float) -> float:
+        return (rot_dim * math.log(original_max_position / (n_rot * 2 * math.pi))) / (
+            2 * math.log(theta))
+
+    low, high = corr_dim(beta_fast), corr_dim(beta_slow)
+    if truncate:
+        low, high = math.floor(low), math.ceil(high)
+    low, high = max(low, 0), min(high, rot_dim - 1)
+    if low == high:
+        high += 0.001
+    ramp = np.clip((np.arange(rot_dim // 2, dtype=np.float64) - low) / (high - low), 0.0, 1.0)
+    extrapolation = 1.0 - ramp
+    return (inv / factor) * (1.0 - extrapolation) + inv * extrapolation
+
+
+def inv_freq_for(rope_scaling: Optional[dict], rot_dim: int, theta: float) -> np.ndarray:
+    """inv_freq of a model's RoPE from its HF-style ``rope_scaling`` entry
+    (None / "default", "linear", "llama3", "yarn"). Scalings whose
+    frequencies depend on the sequence length at prefill ("dynamic",
+    "longrope") leave no single rotation between two positions and are
+    rejected."""
+    if not rope_scaling:
+        return rope_inv_freq(rot_dim, theta)
+    kind = rope_scaling.get("rope_type", rope_scaling.get("type", "default"))
+    if kind == "default":
+        return rope_inv_freq(rot_dim, theta)
+    if kind == "linear":
+        return rope_inv_freq(rot_dim, theta) / float(rope_scaling["factor"])
+    if kind == "llama3":
+        return llama3_inv_freq(rot_dim, theta, float(rope_scaling["factor"]),
+                               float(rope_scaling["low_freq_factor"]),
+                               float(rope_scaling["high_freq_factor"]),
+                               int(rope_scaling["original_max_position_embeddings"]))
+    if kind == "yarn":
+        return yarn_inv_freq(rot_dim, theta, float(rope_scaling["factor"]),
+                             int(rope_scaling["original_max_position_embeddings"]),
+                             float(rope_scaling.get("beta_fast", 32.0)),
+                             float(rope_scaling.get("beta_slow", 1.0)),
+                             bool(rope_scaling.get("truncate", True)))
+    raise ValueError(f"RoPE scaling {kind!r} depends on the sequence length; a stored chunk "
+                     "cannot be re-rotated by a position delta")
+
+
 def delta_tables(
     deltas: Sequence[int],
     rot_dim: int,

@@ -113,9 +113,21 @@ def test_load_round_trip_into_other_blocks(gpu, tmp_path):
     r.shutdown()
 
 
-def test_load_with_new_position_rerotates_k(gpu, tmp_path):
-    print("case: connector load rerotate", flush=True)
-    w, _ = _worker(tmp_path, rope_theta=500000.0)
+LLAMA31_SCALING = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+                   "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
+
+
+@pytest.mark.parametrize("scaling", [None, LLAMA31_SCALING], ids=["plain", "llama3"])
+def test_load_with_new_position_rerotates_k(gpu, tmp_path, scaling):
+    """The rotation uses the model's frequencies; the scaled ones are pinned
+    against transformers' own in the CPU tests of position.inv_freq_for."""
+    print(f"case: connector load rerotate scaling={scaling}", flush=True)
+    from daser_amd.position import inv_freq_for
+
+    extra = {"rope_theta": 500000.0}
+    if scaling:
+        extra["rope_scaling"] = scaling
+    w, _ = _worker(tmp_path, **extra)
     caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=33)
     named = _named(caches)
     w.register_kv_caches(named)
@@ -124,7 +136,7 @@ def test_load_with_new_position_rerotates_k(gpu, tmp_path):
     recs = _file_records(tmp_path / "daser.store", 3, 3).copy()
 
     fresh = [torch.zeros_like(c) for c in caches]
-    w2, _ = _worker(tmp_path, rope_theta=500000.0)
+    w2, _ = _worker(tmp_path, **extra)
     w2.register_kv_caches(_named(fresh))
     # stored at 100, placed at 4196: delta 4096; second request as stored
     meta = C.DaserConnectorMeta(reqs_to_load={
@@ -138,7 +150,8 @@ def test_load_with_new_position_rerotates_k(gpu, tmp_path):
     oracle.scatter_rerotate(ref, [1, 12, 4], np.arange(3) * slot, recs, SHAPE.layer_bytes,
                             dtype=oracle.BF16, rot_dim=64, style=oracle.NEOX,
                             stored_pos=np.full(3, 100), new_pos=np.full(3, 4196),
-                            rotate=np.ones(3), theta=500000.0)
+                            rotate=np.ones(3), theta=500000.0,
+                            inv_freq=inv_freq_for(scaling, 64, 500000.0))
     for l, f in enumerate(fresh):
         got = to_bits_np(f, "bf16")
         assert np.array_equal(got[1][[1, 12, 4]], ref[l][1][[1, 12, 4]])
