@@ -8,13 +8,14 @@ launch covering every page of every request over all 32 layers.
 
 value = algorithmic bytes of the step (gather reads P, writes P; scatter the
 same: 4P) / step time, inputs resident in HBM. The fused re-rotate+scatter of
-configs 3 (RAG reuse), 4 (e4m3) and 5 (70B share) are reported beside it.
+configs 3 (RAG reuse), 4 (e4m3), 5 (70B share) and 6 (one TP8 rank of 70B:
+one KV head, 4 KiB pages) are reported beside it.
 
 Per-kernel durations come from HIP events recorded on the launch stream
 around every timed launch. cpu_baseline times the C oracle (one thread) on a
 bounded sample of the same shape on the host.
 
-Usage: python bench.py [--steps K] [--warmup W] [--configs 2,3,4,5] [--no-cpu]
+Usage: python bench.py [--steps K] [--warmup W] [--configs 2,3,4,5,6] [--no-cpu]
                        [--no-ref-loop] [--io] [--calibrate]
 """
 
@@ -238,9 +239,25 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
     torch.cuda.synchronize()
     copy_ms = tc.mean_ms()
     P = wl.n_pages * shape.slot_bytes
+    extra = {}
+    if P < torch.cuda.mem_get_info(dev)[0] // 2:
+        # the save direction over the same pages into one record per page
+        del src
+        recs = torch.empty(P, dtype=torch.uint8, device=dev)
+        roffs = torch.arange(wl.n_pages, dtype=torch.int64, device=dev) * shape.slot_bytes
+        tg = Timer(torch)
+        for _ in range(warmup):
+            ops.gather(table, ids, roffs, recs)
+        for _ in range(steps):
+            with tg:
+                ops.gather(table, ids, roffs, recs)
+        torch.cuda.synchronize()
+        extra = {"gather_ms": tg.mean_ms(),
+                 "gather_GBps": 2 * P / (tg.mean_ms() * 1e-3) / 1e9}
+        src = recs
     del full, caches, table, src
     torch.cuda.empty_cache()
-    return {
+    return {**extra,
         "payload_bytes": P,
         "pages": wl.n_pages,
         "tokens": wl.tokens,
@@ -360,6 +377,11 @@ def reference_loop(torch, dev, budget_s: float = 6.0) -> dict:
             "sample": f"{wl.n_pages} pages x 32 layers, {n} save+load rounds in {el:.1f} s"}
 
 
+# the re-rotation kernel each configuration's launch selects (by page size)
+ROT_KERNEL = {3: "kv_scatter_rerotate_contig_kernel", 5: "kv_scatter_rerotate_contig_kernel",
+              6: "kv_scatter_rerotate_grouped_kernel"}
+
+
 def pmc_traffic(kernel: str, config: int, pages: int):
     """HBM bytes per launch recorded from rocprofv3 PMC runs of this same
     workload (profiles/pmc_traffic.txt), or None if not recorded."""
@@ -410,7 +432,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="2,3,4,5")
+    ap.add_argument("--configs", default="2,3,4,5,6")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-ref-loop", action="store_true",
                     help="skip timing the reference's per-page torch copy loop on the GPU")
@@ -492,7 +514,7 @@ def main() -> int:
             "ms": round(r["slots_scatter_ms"], 4), "GBps": round(r["slots_scatter_GBps"], 1),
             "frac": round(r["slots_scatter_GBps"] / HBM_PEAK_GBS, 4)}
         out["check"] = {"round_trip_probe": r["probe_ok"]}
-    for c in (3, 5):
+    for c in (3, 5, 6):
         if c in res:
             r = res[c]
             out[f"rerotate_cfg{c}"] = {
@@ -501,7 +523,10 @@ def main() -> int:
                 "GBps": round(r["GBps"], 1), "frac": round(r["frac_hbm_peak"], 4),
                 "kernel_ms": round(r["kernel_ms"], 4), "tokens": r["tokens"],
                 "same_pages_plain_scatter_GBps": round(r["plain_scatter_GBps"], 1),
-                "traffic": pmc_traffic("kv_scatter_rerotate_contig_kernel", c, r["pages"]),
+                **({"same_pages_gather_GBps": round(r["gather_GBps"], 1)}
+                   if "gather_GBps" in r else {}),
+                "kernel": ROT_KERNEL[c],
+                "traffic": pmc_traffic(ROT_KERNEL[c], c, r["pages"]),
                 "algorithmic_bytes": 2 * r["payload_bytes"]}
     if 4 in res:
         r = res[4]

@@ -43,6 +43,7 @@ QWEN2_05B = KVShape(24, 2, 64, 16, 2)
 LLAMA3_8B = KVShape(32, 8, 128, 16, 2)
 LLAMA3_8B_FP8 = KVShape(32, 8, 128, 16, 1)
 LLAMA3_70B = KVShape(80, 8, 128, 16, 2)
+LLAMA3_70B_TP8 = KVShape(80, 1, 128, 16, 2)  # one rank's heads under 8-way tensor parallelism
 
 
 @dataclass
@@ -162,6 +163,8 @@ def config(n: int, seed: int = 0) -> PagedWorkload:
         return ragged(LLAMA3_8B_FP8, 128, 256, 16384, seed, pool_slack=1.05)
     if n == 5:  # Llama-3-70B single-GPU share
         return rag_reuse(LLAMA3_70B, 16, 64, 512, 64, 32768, seed)
+    if n == 6:  # the same workload as config 5, one TP8 rank's share (H = 1, 4 KiB pages)
+        return rag_reuse(LLAMA3_70B_TP8, 16, 64, 512, 64, 32768, seed)
     raise ValueError(f"unknown config {n}")
 
 
@@ -171,4 +174,5 @@ CONFIG_NAMES = {
     3: "llama-3-8b RAG reuse re-rotate+scatter (32 req x 10 x 512-token chunks, offset U[0,32768), theta 5e5)",
     4: "llama-3-8b fp8 e4m3 paged gather->scatter (128 req U[256,16384], per-layer scales)",
     5: "llama-3-70b single-GPU share re-rotate+scatter (L80, 16 x 32768 tokens from 64 reused 512-token chunks)",
+    6: "llama-3-70b TP8 rank share re-rotate+scatter (L80 H1 D128, 4 KiB pages, config 5's requests)",
 }

@@ -69,9 +69,10 @@ def test_round_trip_full_size(gpu, cfg, dtype):
     torch.cuda.synchronize()
 
 
-def test_rerotate_full_size_properties(gpu):
-    print("case: full-size rerotate cfg3", flush=True)
-    wl = workloads.config(3)
+@pytest.mark.parametrize("cfg", [3, 6])  # 6: one KV head, 4 KiB pages (grouped kernels)
+def test_rerotate_full_size_properties(gpu, cfg):
+    print(f"case: full-size rerotate cfg{cfg}", flush=True)
+    wl = workloads.config(cfg)
     shape = wl.shape
     src_full, src_caches, _ = bench.fill_caches(torch, shape, wl.num_blocks, "bf16", gpu, seed=61)
     # records of every destination page, from the source caches
@@ -79,8 +80,9 @@ def test_rerotate_full_size_properties(gpu):
     offs = wl.slot_offsets
     ops.gather(ops.LayerTable(src_caches), wl.page_ids, offs, st)
     ridx, uniq = position.page_rope_index(wl.chunk_pages, wl.chunk_delta)
-    fwd = position.delta_tables(uniq, 128, 500000.0, device=gpu)
-    bwd = position.delta_tables([-d for d in uniq], 128, 500000.0, device=gpu)
+    D = shape.head_dim
+    fwd = position.delta_tables(uniq, D, 500000.0, device=gpu)
+    bwd = position.delta_tables([-d for d in uniq], D, 500000.0, device=gpu)
     ids = torch.from_numpy(wl.page_ids.astype(np.int64)).to(gpu)
 
     # zero delta everywhere: a bit-exact copy
@@ -107,9 +109,9 @@ def test_rerotate_full_size_properties(gpu):
         z = back[l][:, ids]
         assert torch.equal(y[1], x[1]) and torch.equal(z[1], x[1]), f"layer {l}: V changed"
         xf, yf, zf = x[0].float(), y[0].float(), z[0].float()
-        # pair norms preserved (neox pairs j, j + 64) within bf16 rounding
-        nx = torch.hypot(xf[..., :64], xf[..., 64:])
-        ny = torch.hypot(yf[..., :64], yf[..., 64:])
+        # pair norms preserved (neox pairs j, j + D/2) within bf16 rounding
+        nx = torch.hypot(xf[..., :D // 2], xf[..., D // 2:])
+        ny = torch.hypot(yf[..., :D // 2], yf[..., D // 2:])
         assert ((ny - nx).abs() <= 2 ** -7 * nx + 1e-6).all(), f"layer {l}: norm"
         # round trip: two bf16 roundings, relative to the row's magnitude
         rowmax = xf.abs().amax(dim=-1, keepdim=True)

@@ -230,6 +230,21 @@ def test_rerotate_matches_oracle(gpu, dt, style, head_dim, rot_dim):
             assert (a - b).abs().max().item() <= 1e-2 * max(1.0, b.abs().max().item())
 
 
+@pytest.mark.parametrize("dt", ["bf16", "e4m3"])
+def test_rerotate_single_kv_head(gpu, dt):
+    """One KV head per page (a TP8 rank of a 70B model: 4 KiB bf16 pages,
+    2 KiB e4m3): rows of 256 / 128 bytes."""
+    print(f"case: rerotate single head {dt}", flush=True)
+    shape, dst, dst_ref, page_ids, page_delta = _rerotate_case(
+        gpu, dt, "neox", 128, 128, heads=1, layers=5, seed=9,
+        scale=40.0 if dt == "e4m3" else 1.0)
+    for l in range(shape.num_layers):
+        got = to_bits_np(dst[l], dt)
+        assert np.array_equal(got[1], dst_ref[l][1])
+        ok, msg = rotation_within_tolerance(got[0], dst_ref[l][0], dt)
+        assert ok, f"layer {l}: {msg}"
+
+
 def test_rerotate_inverse_is_identity(gpu):
     """Rotating by +d then -d returns the input within 2 bf16 ulps."""
     print("case: rerotate inverse", flush=True)
@@ -396,3 +411,112 @@ def test_large_page_geometry(gpu):
         assert np.array_equal(got[1], r[1])
         ok, msg = oracle.rotation_within_tolerance(got[0], r[0], oracle.BF16)
         assert ok, msg
+
+
+# ---------------------------------------------------------------------------
+# pages of whole 4 KiB slices: several units per workgroup
+
+
+@pytest.mark.parametrize("layers,heads,head_dim,dt", [
+    (7, 1, 128, "bf16"),   # 4 KiB pages: one slice per unit
+    (5, 2, 128, "bf16"),   # 8 KiB: two slices per unit
+    (6, 2, 64, "bf16"),    # Qwen2-0.5B geometry
+    (5, 2, 128, "e4m3"),   # 4 KiB e4m3
+    (5, 1, 128, "e4m3"),   # 2 KiB: two units per workgroup slice
+    (4, 1, 64, "bf16"),    # 2 KiB
+    (3, 1, 64, "e4m3"),    # 1 KiB: one unit per wave
+])
+@pytest.mark.parametrize("group_cap", ["1", "2", "3", ""])
+def test_grouped_units_match_oracle(gpu, monkeypatch, layers, heads, head_dim, dt, group_cap):
+    """Groups span layer boundaries (3 pages, fewer than a group) and end
+    part-way; every grouping (1 = the one-unit kernels) gives the oracle's
+    bytes for gather, scatter and re-rotation."""
+    print(f"case: grouped L{layers} H{heads} D{head_dim} {dt} cap={group_cap!r}", flush=True)
+    if group_cap:
+        monkeypatch.setenv("DSR_UNITS_PER_GROUP", group_cap)
+    else:
+        monkeypatch.delenv("DSR_UNITS_PER_GROUP", raising=False)
+    shape = KVShape(layers, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    nb = 9
+    src = rand_caches(shape, nb, dt, gpu, seed=60, scale=40.0 if dt == "e4m3" else 1.0)
+    ids = np.array([5, 0, 7], dtype=np.int32)
+    offs = np.array([2, 0, 1], dtype=np.int64) * shape.slot_bytes
+    staging = torch.zeros(3 * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(src), ids, offs, staging)
+    ref = np.zeros(3 * shape.slot_bytes, dtype=np.uint8)
+    src_np = _np_layers(src, dt)
+    oracle.gather(src_np, ids, offs, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    assert np.array_equal(staging.cpu().numpy(), ref)
+
+    dst_ids = np.array([4, 8, 1], dtype=np.int32)
+    dst = [torch.zeros_like(c) for c in src]
+    ops.scatter(ops.LayerTable(dst), dst_ids, offs, staging)
+    dref = [np.zeros_like(a) for a in src_np]
+    oracle.scatter(dref, dst_ids, offs, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    for l in range(layers):
+        assert np.array_equal(to_bits_np(dst[l], dt), dref[l])
+
+    deltas = [0, 517, 32767]
+    ridx, uniq = position.page_rope_index([1, 1, 1], deltas)
+    tabs = position.delta_tables(uniq, head_dim, 500000.0, device=gpu)
+    ks_np = None
+    k_scale = None
+    if dt == "e4m3":
+        ks_np = np.linspace(0.05, 0.5, layers).astype(np.float32)
+        k_scale = torch.from_numpy(ks_np).to(gpu)
+    rot = [torch.zeros_like(c) for c in src]
+    ops.scatter_rerotate(ops.LayerTable(rot), dst_ids, offs, staging, tabs, ridx,
+                         k_scale=k_scale)
+    rref = [np.zeros_like(a) for a in src_np]
+    d = np.asarray(deltas, np.int64)
+    oracle.scatter_rerotate(rref, dst_ids, offs, ref, shape.layer_bytes, dtype=ORC_DT[dt],
+                            rot_dim=head_dim, style=0, stored_pos=np.zeros(3, np.int64),
+                            new_pos=d, rotate=d != 0, theta=500000.0, k_scale=ks_np)
+    torch.cuda.synchronize()
+    for l in range(layers):
+        got = to_bits_np(rot[l], dt)
+        assert np.array_equal(got[1], rref[l][1])
+        assert np.array_equal(got[0][4], rref[l][0][4])  # delta 0: copy
+        ok, msg = rotation_within_tolerance(got[0], rref[l][0], dt)
+        assert ok, f"layer {l}: {msg}"
+
+
+@pytest.mark.parametrize("group_cap", ["1", ""])
+def test_grouped_units_skip_out_of_range(gpu, monkeypatch, group_cap):
+    """Device tables with an out-of-range block inside a group: that unit is
+    skipped in every layer, its neighbours in the group still move."""
+    print(f"case: grouped skip cap={group_cap!r}", flush=True)
+    if group_cap:
+        monkeypatch.setenv("DSR_UNITS_PER_GROUP", group_cap)
+    else:
+        monkeypatch.delenv("DSR_UNITS_PER_GROUP", raising=False)
+    shape = KVShape(5, 1, 128, 16, 2)
+    src = rand_caches(shape, 8, "bf16", gpu, seed=61)
+    staging = torch.zeros(3 * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ids = torch.tensor([3, 1000, 6], dtype=torch.int32, device=gpu)
+    offs = torch.tensor([0, 1, 2], dtype=torch.int64, device=gpu) * shape.slot_bytes
+    ops.gather(ops.LayerTable(src), ids, offs, staging)
+    torch.cuda.synchronize()
+    for i, b in ((0, 3), (2, 6)):
+        exp = torch.cat([c[:, b].reshape(-1).view(torch.uint8) for c in src])
+        assert torch.equal(staging[i * shape.slot_bytes:(i + 1) * shape.slot_bytes], exp)
+    assert not staging[shape.slot_bytes:2 * shape.slot_bytes].any()
+    dst = [torch.zeros_like(c) for c in src]
+    dids = torch.tensor([1, -1, 4], dtype=torch.int32, device=gpu)
+    ops.scatter(ops.LayerTable(dst), dids, offs, staging)
+    tabs = position.delta_tables([300], 128, 500000.0, device=gpu)
+    rot = [torch.zeros_like(c) for c in src]
+    ridx = torch.tensor([0, 0, -1], dtype=torch.int32, device=gpu)
+    ops.scatter_rerotate(ops.LayerTable(rot), dids, offs, staging, tabs, ridx)
+    torch.cuda.synchronize()
+    for l in range(shape.num_layers):
+        assert torch.equal(dst[l][:, 1], src[l][:, 3])
+        assert torch.equal(dst[l][:, 4], src[l][:, 6])
+        assert torch.equal(rot[l][:, 4], src[l][:, 6])       # no table: copy
+        assert torch.equal(rot[l][1, 1], src[l][1, 3])       # V copied
+        assert not torch.equal(rot[l][0, 1], src[l][0, 3])   # K rotated
+        others = [b for b in range(8) if b not in (1, 4)]
+        assert not dst[l][:, others].view(torch.int16).any()
+        assert not rot[l][:, others].view(torch.int16).any()
