@@ -333,18 +333,27 @@ def test_rerotate_special_values(gpu, dt):
         assert ok, msg
 
 
-def test_slots_gather_scatter_match_oracle(gpu):
-    """slot_mapping-driven token gather/scatter at the Qwen2-0.5B shape with
-    ragged requests, partial last pages and padding tokens."""
-    print("case: slots gather/scatter", flush=True)
-    wl = workloads.config(1)
+@pytest.mark.parametrize("shape", [
+    None,                          # config 1, Qwen2-0.5B: 256-byte rows (16 vectors)
+    KVShape(6, 1, 64, 16, 2),      # 128-byte rows
+    KVShape(5, 2, 128, 16, 2),     # 512-byte rows (32 vectors)
+    KVShape(4, 4, 128, 16, 2),     # 1 KiB rows: the large-row kernel
+    KVShape(5, 1, 128, 16, 1),     # e4m3, 128-byte rows
+], ids=["cfg1", "row128", "row512", "row1k", "e4m3_row128"])
+def test_slots_gather_scatter_match_oracle(gpu, shape):
+    """slot_mapping-driven token gather/scatter with ragged requests, partial
+    last pages and padding tokens, at each row-size class of the kernels."""
+    print(f"case: slots gather/scatter {shape}", flush=True)
+    wl = workloads.config(1) if shape is None else workloads.ragged(
+        shape, 8, 100, 2000, seed=3, num_blocks=1024)
     shape = wl.shape
-    caches = rand_caches(shape, wl.num_blocks, "bf16", gpu, seed=50)
+    dt = "e4m3" if shape.elem_bytes == 1 else "bf16"
+    caches = rand_caches(shape, wl.num_blocks, dt, gpu, seed=50)
     tables, k = [], 0
     for n in wl.req_pages:
         tables.append(wl.page_ids[k:k + n].tolist())
         k += n
-    row = shape.num_heads * shape.head_dim * 2
+    row = shape.num_heads * shape.head_dim * shape.elem_bytes
     sm = ops.slot_mapping_for(tables, wl.req_tokens, shape.block_size)
     ro = ops.token_row_offsets(wl.req_tokens, shape.slot_bytes, shape.block_size, row)
     pad = np.arange(0, sm.size, 97)
@@ -352,7 +361,7 @@ def test_slots_gather_scatter_match_oracle(gpu):
     st = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
     ops.gather_slots(ops.LayerTable(caches), sm, ro, st)
     ref = np.zeros(wl.staging_bytes, dtype=np.uint8)
-    host = [to_bits_np(c, "bf16") for c in caches]
+    host = [to_bits_np(c, dt) for c in caches]
     oracle.gather_slots(host, sm, ro, ref, shape.layer_bytes)
     torch.cuda.synchronize()
     assert np.array_equal(st.cpu().numpy(), ref)
@@ -362,7 +371,7 @@ def test_slots_gather_scatter_match_oracle(gpu):
     oracle.scatter_slots(dref, sm, ro, ref, shape.layer_bytes)
     torch.cuda.synchronize()
     for d, r in zip(dst, dref):
-        assert np.array_equal(to_bits_np(d, "bf16"), r)
+        assert np.array_equal(to_bits_np(d, dt), r)
 
 
 def test_slots_gather_equals_page_gather_for_full_pages(gpu):
