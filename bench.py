@@ -289,7 +289,7 @@ def bench_io(torch, dev, budget_bytes: int = 2 << 30, reps: int = 3) -> dict:
     named = {f"layer.{i}": c for i, c in enumerate(caches)}
     d = tempfile.mkdtemp(prefix="daser_bench_")
     try:
-        plane = KVDataPlane(os.path.join(d, "daser.store"), io_slot_bytes=64 << 20, io_slots=4)
+        plane = KVDataPlane(os.path.join(d, "daser.store"))  # default ring: 8 x 4 MiB
         plane.register(named)
         rng = np.random.default_rng(3)
         blocks = rng.permutation(nb)[:n_pages].tolist()

@@ -207,7 +207,7 @@ class KVDataPlane:
                  rope_style: str = "neox", rotary_dim: Optional[int] = None,
                  inv_freq: Optional[np.ndarray] = None, rope_scaling: Optional[dict] = None,
                  save_mode: str = "per_layer",
-                 io_slot_bytes: int = 64 << 20, io_slots: int = 4,
+                 io_slot_bytes: int = 4 << 20, io_slots: int = 8,
                  io_backend: str = "native", save_stream: str = "side",
                  k_scales: Optional[torch.Tensor] = None) -> None:
         if save_mode not in ("per_layer", "deferred"):
@@ -442,8 +442,8 @@ class DaserConnector(KVConnectorBase_V1):
                 rotary_dim=extra.get("rotary_dim"),
                 rope_scaling=extra.get("rope_scaling"),
                 save_mode=extra.get("save_mode", "per_layer"),
-                io_slot_bytes=int(float(extra.get("io_slot_mb", 64)) * (1 << 20)),
-                io_slots=int(extra.get("io_slots", 4)),
+                io_slot_bytes=int(float(extra.get("io_slot_mb", 4)) * (1 << 20)),
+                io_slots=int(extra.get("io_slots", 8)),
                 io_backend=extra.get("io_backend", "native"),
                 save_stream=extra.get("save_stream", "side"),
             )

@@ -288,7 +288,7 @@ class NativeRingIO:
     """
 
     def __init__(self, path: str, device: torch.device | str = "cuda",
-                 slot_bytes: int = 64 << 20, n_slots: int = 4, use_io_uring: bool = True,
+                 slot_bytes: int = 4 << 20, n_slots: int = 8, use_io_uring: bool = True,
                  direct: bool = False) -> None:
         import ctypes
 

@@ -259,3 +259,27 @@ def test_save_without_layer_hooks_and_repeated_wait(gpu, tmp_path):
     assert np.array_equal(_file_records(tmp_path / "daser.store", 3, 3), ref)
     assert sorted(ipc.committed) == ["ka", "kb"]  # committed once
     w.shutdown()
+
+
+def test_unknown_layer_warns_and_others_still_save(gpu, tmp_path, caplog):
+    """An unknown layer name in save_kv_layer is a warning and a skip, as in
+    the reference (daser_connector.py:602-606); the known layers' records
+    are still written and committed."""
+    print("case: connector unknown layer", flush=True)
+    w, ipc = _worker(tmp_path)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=37)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    w.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_store=_store_reqs()))
+    with caplog.at_level("WARNING"):
+        w.save_kv_layer("model.layers.99.self_attn.attn", caches[0], None)
+    assert any("unknown layer" in r.message for r in caplog.records)
+    for name, t in named.items():
+        w.save_kv_layer(name, t, None)
+    w.wait_for_save()
+    host = [to_bits_np(c, "bf16") for c in caches]
+    ref = np.zeros(3 * SHAPE.slot_bytes, dtype=np.uint8)
+    oracle.gather(host, [5, 9, 2], np.arange(3) * SHAPE.slot_bytes, ref, SHAPE.layer_bytes)
+    assert np.array_equal(_file_records(tmp_path / "daser.store", 3, 3), ref)
+    assert sorted(ipc.committed) == ["ka", "kb"]
+    w.shutdown()

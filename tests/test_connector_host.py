@@ -234,3 +234,37 @@ def test_ring_concurrent_callers_serialise(store):
         io.read_into_device(out, 40_000)
     assert not errs
     assert (out[:30_000] == 1).all() and (out[40_000:70_000] == 2).all()
+
+
+def test_worker_hooks_without_metadata_are_noops(tmp_path):
+    """Reference behaviour of the worker hooks with no bound metadata or
+    with nothing to load or store: return silently, launch nothing
+    (daser_connector.py:455-472, 574-580, 634-640)."""
+    from types import SimpleNamespace
+
+    import torch
+
+    from daser_amd import connector as C
+
+    class IPC:
+        async def commit_chunk(self, key):
+            raise AssertionError("nothing may be committed")
+
+    cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(kv_connector_extra_config=dict(
+        store_path=str(tmp_path / "s"), io_slot_mb=0.03125, io_slots=3, io_backend="python")))
+    w = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=IPC())
+    caches = {f"model.layers.{i}.self_attn.attn": torch.zeros(2, 16, 16, 2, 64, dtype=torch.bfloat16)
+              for i in range(3)}
+    w.register_kv_caches(caches)
+    layer = caches["model.layers.0.self_attn.attn"]
+    for meta in (None, C.DaserConnectorMeta()):
+        if meta is not None:
+            w.bind_connector_metadata(meta)
+        w.start_load_kv(None)
+        w.wait_for_layer_load("model.layers.0.self_attn.attn")
+        w.save_kv_layer("model.layers.0.self_attn.attn", layer, None)
+        w.save_kv_layer("not.a.layer", layer, None)
+        w.wait_for_save()
+        w.clear_connector_metadata()
+    assert (tmp_path / "s").stat().st_size > 0  # store pre-allocated at registration
+    w.shutdown()
