@@ -1024,6 +1024,50 @@ UnitArgs make_unit(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   return a;
 }
 
+// Largest workgroup count of one launch: HIP caps gridDim.x * blockDim.x at
+// 2^32 - 1 threads (16.7 M workgroups of 256). Env DSR_MAX_WG_PER_LAUNCH
+// lowers it, so that tests can exercise the split.
+int64_t max_wg_per_launch() {
+  int64_t m = 0xffffffffLL / kThreads / kXcds * kXcds;
+  if (const char* e = getenv("DSR_MAX_WG_PER_LAUNCH")) {
+    const int64_t v = atoll(e) / kXcds * kXcds;
+    if (v >= 2 * kXcds && v < m) m = v;
+  }
+  return m;
+}
+
+// Items (pages or tokens) per launch such that ceil(items * n_layers /
+// per_wg), rounded up to the XCD count, stays within max_wg_per_launch();
+// per_wg = items' units per workgroup (G pages or a block of tokens).
+int64_t items_per_launch(int n_layers, int64_t per_wg) {
+  const int64_t wg = max_wg_per_launch() - kXcds;
+  const int64_t per = wg * per_wg / n_layers;
+  return per > 0 ? per : 0;
+}
+
+// Launches over consecutive page ranges of `a` (one launch unless the pages
+// exceed max_wg_per_launch()), each range's tables offset to its first
+// page; launch(b, grid) enqueues one kernel. Grids are a whole multiple of
+// the XCD count so that the XCD remap covers every unit. Returns the first
+// launch error.
+template <class F>
+int launch_page_ranges(const UnitArgs& a, int n_pages, int G, F launch) {
+  const int64_t per = items_per_launch(a.n_layers, G);
+  if (per <= 0) return DSR_ERR_ARG;
+  for (int64_t p0 = 0; p0 < n_pages; p0 += per) {
+    const int64_t n = n_pages - p0 < per ? n_pages - p0 : per;
+    UnitArgs b = a;
+    b.page_ids += p0;
+    b.slot_offsets += p0;
+    b.n_units = n * a.n_layers;
+    const unsigned grid = (unsigned)(((b.n_units + G - 1) / G + kXcds - 1) / kXcds * kXcds);
+    launch(b, grid);
+    const int rc = (int)hipGetLastError();
+    if (rc != 0) return rc;
+  }
+  return DSR_OK;
+}
+
 // Dynamic LDS that limits the re-rotation kernel to kRotWgPerCu workgroups
 // per CU on the current device (0 if the capacity cannot be read).
 size_t rot_occupancy_lds(int wg_per_cu) {
@@ -1037,7 +1081,7 @@ size_t rot_occupancy_lds(int wg_per_cu) {
 }
 
 template <int DT>
-int launch_rerotate(const RotArgs& ra, int style, hipStream_t s) {
+int launch_rerotate(const RotArgs& ra, int n_pages, int style, hipStream_t s) {
   const int h = ra.half_vecs;
   int wg = rot_wg_per_cu<DT>();
   if (const char* e = getenv("DSR_ROT_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
@@ -1046,28 +1090,29 @@ int launch_rerotate(const RotArgs& ra, int style, hipStream_t s) {
   const int G = contig ? units_per_group(ra.u.page_bytes, rot_contig_unroll<DT>(),
                                          kMaxRotHalf / ra.rot_half)
                        : 1;
-  const unsigned grid =
-      (unsigned)(((ra.u.n_units + G - 1) / G + kXcds - 1) / kXcds * kXcds);
   if (G > 1) {
     wg = rot_grouped_wg_per_cu<DT>();
     if (const char* e = getenv("DSR_ROT_GROUPED_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
-    const size_t dyn = rot_occupancy_lds(wg);
-    if (style == DSR_ROPE_NEOX)
-      kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(ra, G);
-    else
-      kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(ra, G);
-    return (int)hipGetLastError();
   }
   const size_t dyn = rot_occupancy_lds(wg);
-  if (contig) {
-    if (style == DSR_ROPE_NEOX)
-      kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(ra);
-    else
-      kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(ra);
-  } else {
-    kv_scatter_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(ra);
-  }
-  return (int)hipGetLastError();
+  return launch_page_ranges(ra.u, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
+    RotArgs rb = ra;
+    rb.u = b;
+    rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
+    if (G > 1) {
+      if (style == DSR_ROPE_NEOX)
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb, G);
+      else
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(rb, G);
+    } else if (contig) {
+      if (style == DSR_ROPE_NEOX)
+        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb);
+      else
+        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(rb);
+    } else {
+      kv_scatter_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb);
+    }
+  });
 }
 
 }  // namespace
@@ -1110,13 +1155,12 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   // Grouped only below one workgroup's 4 KiB: from 4 KiB up the one-unit
   // kernel measured faster (6.14 vs 5.57 TB/s at 4 KiB pages).
   const int G = page_bytes < kThreads * 16 ? units_per_group(page_bytes, kGatherUnroll, kMaxGroup) : 1;
-  // whole multiple of the XCD count so that the remap covers every unit
-  const unsigned grid = (unsigned)(((a.n_units + G - 1) / G + kXcds - 1) / kXcds * kXcds);
-  if (G > 1)
-    kv_copy_grouped_kernel<true, kGatherUnroll><<<grid, kThreads, 0, (hipStream_t)stream>>>(a, G);
-  else
-    kv_gather_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(a);
-  return (int)hipGetLastError();
+  return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
+    if (G > 1)
+      kv_copy_grouped_kernel<true, kGatherUnroll><<<grid, kThreads, 0, (hipStream_t)stream>>>(b, G);
+    else
+      kv_gather_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(b);
+  });
 }
 
 int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
@@ -1134,12 +1178,12 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   // Grouped up to 4 KiB pages (6.47 vs 5.04 TB/s at 4 KiB); at 8-32 KiB the
   // one-unit kernel measured equal or faster.
   const int G = page_bytes <= kThreads * 16 ? units_per_group(page_bytes, kScatterUnroll, kMaxGroup) : 1;
-  const unsigned grid = (unsigned)(((a.n_units + G - 1) / G + kXcds - 1) / kXcds * kXcds);
-  if (G > 1)
-    kv_copy_grouped_kernel<false, kScatterUnroll><<<grid, kThreads, 0, (hipStream_t)stream>>>(a, G);
-  else
-    kv_scatter_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(a);
-  return (int)hipGetLastError();
+  return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
+    if (G > 1)
+      kv_copy_grouped_kernel<false, kScatterUnroll><<<grid, kThreads, 0, (hipStream_t)stream>>>(b, G);
+    else
+      kv_scatter_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(b);
+  });
 }
 
 int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
@@ -1208,11 +1252,11 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case DSR_DTYPE_BF16:
-      return launch_rerotate<DSR_DTYPE_BF16>(ra, rope_style, s);
+      return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, s);
     case DSR_DTYPE_FP16:
-      return launch_rerotate<DSR_DTYPE_FP16>(ra, rope_style, s);
+      return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, s);
     default:
-      return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, rope_style, s);
+      return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, s);
   }
 }
 
@@ -1261,30 +1305,41 @@ int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t 
   a.layer0 = layer0;
   a.block_size = block_size;
   a.block_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
-  const int64_t units = blocks * n_layers;
-  const unsigned grid = (unsigned)(gather ? units : (units + kXcds - 1) / kXcds * kXcds);
   hipStream_t s = (hipStream_t)stream;
-  if (tpw == 16) {
-    if (gather)
-      kv_slots_small_kernel<true, 16><<<grid, kThreads, 0, s>>>(a);
-    else
-      kv_slots_small_kernel<false, 16><<<grid, kThreads, 0, s>>>(a);
-  } else if (tpw == 8) {
-    if (gather)
-      kv_slots_small_kernel<true, 8><<<grid, kThreads, 0, s>>>(a);
-    else
-      kv_slots_small_kernel<false, 8><<<grid, kThreads, 0, s>>>(a);
-  } else if (tpw == 4) {
-    if (gather)
-      kv_slots_small_kernel<true, 4><<<grid, kThreads, 0, s>>>(a);
-    else
-      kv_slots_small_kernel<false, 4><<<grid, kThreads, 0, s>>>(a);
-  } else if (gather) {
-    kv_slots_kernel<true><<<grid, kThreads, 0, s>>>(a);
-  } else {
-    kv_slots_kernel<false><<<grid, kThreads, 0, s>>>(a);
+  // token ranges whose launches stay within max_wg_per_launch()
+  const int64_t per = items_per_launch(n_layers, tok_wg) / tok_wg * tok_wg;
+  if (per <= 0) return DSR_ERR_ARG;
+  for (int64_t t0 = 0; t0 < n_tokens; t0 += per) {
+    SlotArgs b = a;
+    b.slot_mapping += t0;
+    b.row_offsets += t0;
+    b.n_tokens = (int32_t)(n_tokens - t0 < per ? n_tokens - t0 : per);
+    const int64_t units = ((int64_t)b.n_tokens + tok_wg - 1) / tok_wg * n_layers;
+    const unsigned grid = (unsigned)(gather ? units : (units + kXcds - 1) / kXcds * kXcds);
+    if (tpw == 16) {
+      if (gather)
+        kv_slots_small_kernel<true, 16><<<grid, kThreads, 0, s>>>(b);
+      else
+        kv_slots_small_kernel<false, 16><<<grid, kThreads, 0, s>>>(b);
+    } else if (tpw == 8) {
+      if (gather)
+        kv_slots_small_kernel<true, 8><<<grid, kThreads, 0, s>>>(b);
+      else
+        kv_slots_small_kernel<false, 8><<<grid, kThreads, 0, s>>>(b);
+    } else if (tpw == 4) {
+      if (gather)
+        kv_slots_small_kernel<true, 4><<<grid, kThreads, 0, s>>>(b);
+      else
+        kv_slots_small_kernel<false, 4><<<grid, kThreads, 0, s>>>(b);
+    } else if (gather) {
+      kv_slots_kernel<true><<<grid, kThreads, 0, s>>>(b);
+    } else {
+      kv_slots_kernel<false><<<grid, kThreads, 0, s>>>(b);
+    }
+    const int rc = (int)hipGetLastError();
+    if (rc != 0) return rc;
   }
-  return (int)hipGetLastError();
+  return DSR_OK;
 }
 
 }  // namespace

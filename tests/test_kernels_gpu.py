@@ -529,3 +529,57 @@ def test_grouped_units_skip_out_of_range(gpu, monkeypatch, group_cap):
         others = [b for b in range(8) if b not in (1, 4)]
         assert not dst[l][:, others].view(torch.int16).any()
         assert not rot[l][:, others].view(torch.int16).any()
+
+
+@pytest.mark.parametrize("layers,heads,head_dim,dt", [
+    (4, 8, 128, "bf16"),    # one-unit kernels
+    (7, 1, 128, "bf16"),    # grouped (4 KiB pages)
+    (5, 1, 128, "e4m3"),    # grouped (2 KiB pages)
+])
+def test_launch_split_matches_single_launch(gpu, monkeypatch, layers, heads, head_dim, dt):
+    """Calls whose workgroups exceed one launch's limit run as several
+    launches over page (token) ranges; forced here with a limit of 16
+    workgroups, every entry point writes the same bytes as one launch."""
+    print(f"case: launch split L{layers} H{heads} {dt}", flush=True)
+    shape = KVShape(layers, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    wl = workloads.ragged(shape, 6, 40, 700, seed=12, num_blocks=256)
+    src = rand_caches(shape, wl.num_blocks, dt, gpu, seed=70, scale=40.0 if dt == "e4m3" else 1.0)
+    ridx = np.arange(wl.n_pages, dtype=np.int32) % 3 - 1  # -1 (copy), 0, 1
+    tabs = position.delta_tables([517, 32767], head_dim, 500000.0, device=gpu)
+    ks = torch.linspace(0.05, 0.5, layers, device=gpu) if dt == "e4m3" else None
+    tables, k = [], 0
+    for n in wl.req_pages:
+        tables.append(wl.page_ids[k:k + n].tolist())
+        k += n
+    row = heads * head_dim * shape.elem_bytes
+    sm = ops.slot_mapping_for(tables, wl.req_tokens, 16)
+    ro = ops.token_row_offsets(wl.req_tokens, shape.slot_bytes, 16, row)
+
+    def run():
+        table = ops.LayerTable(src)
+        st = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+        ops.gather(table, wl.page_ids, wl.slot_offsets, st)
+        st2 = torch.zeros_like(st)
+        ops.gather_slots(table, sm, ro, st2)
+        outs = [st, st2]
+        perm = np.random.default_rng(1).permutation(wl.num_blocks)[:wl.n_pages].astype(np.int32)
+        for kind in ("scatter", "rerotate", "slots"):
+            dst = [torch.zeros_like(c) for c in src]
+            t = ops.LayerTable(dst)
+            if kind == "scatter":
+                ops.scatter(t, perm, wl.slot_offsets, st)
+            elif kind == "rerotate":
+                ops.scatter_rerotate(t, perm, wl.slot_offsets, st, tabs, ridx, k_scale=ks)
+            else:
+                ops.scatter_slots(t, sm, ro, st2)
+            outs += [d.view(torch.uint8).clone() for d in dst]
+        torch.cuda.synchronize()
+        return outs
+
+    monkeypatch.delenv("DSR_MAX_WG_PER_LAUNCH", raising=False)
+    one = run()
+    monkeypatch.setenv("DSR_MAX_WG_PER_LAUNCH", "16")
+    split = run()
+    for i, (a, b) in enumerate(zip(one, split)):
+        assert torch.equal(a, b), f"output {i}"
+    assert one[0].any() and one[2].any()
