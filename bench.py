@@ -378,7 +378,7 @@ def reference_loop(torch, dev, budget_s: float = 6.0) -> dict:
 
 
 # the re-rotation kernel each configuration's launch selects (by page size)
-ROT_KERNEL = {3: "kv_scatter_rerotate_contig_kernel", 5: "kv_scatter_rerotate_contig_kernel",
+ROT_KERNEL = {3: "kv_scatter_rerotate_grouped_kernel", 5: "kv_scatter_rerotate_grouped_kernel",
               6: "kv_scatter_rerotate_grouped_kernel"}
 
 

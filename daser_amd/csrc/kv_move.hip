@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "daser_kv.h"
 
@@ -58,6 +59,14 @@ template <int DT>
 constexpr int rot_grouped_wg_per_cu() {
   return DT == DSR_DTYPE_FP8_E4M3 ? 8 : 4;
 }
+// The grouped kernel with one unit per workgroup (16-bit pages of exactly
+// U * 4 KiB, the Llama-3-8B/70B shapes): 3 per CU. Measured in-process:
+// config 3 7.05 ms at 2-3 per CU, 7.36 at 4-5 (the contig kernel 7.68);
+// config 5 55.1 ms at 2-3, 50.4 at 4-6 (contig 55.4), where the shared
+// source chunks' reads hit the memory-side cache. 3 is taken for the
+// HBM-bound case. e4m3 keeps the contig kernel (24.05 vs 24.22 ms at
+// config 4).
+constexpr int kRotSingleWgPerCu = 3;
 constexpr int kMaxRotHalf = 512;   // LDS table capacity: rot_dim <= 1024
 constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
 
@@ -1090,8 +1099,19 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, hipStream_t s) {
   const int G = contig ? units_per_group(ra.u.page_bytes, rot_contig_unroll<DT>(),
                                          kMaxRotHalf / ra.rot_half)
                        : 1;
-  if (G > 1) {
-    wg = rot_grouped_wg_per_cu<DT>();
+  // The grouped kernel also serves pages of exactly U vectors per lane
+  // (G = 1), for 16-bit K. Env DSR_ROT_KERNEL=contig|grouped overrides the
+  // choice where both apply, for in-process comparisons.
+  const int64_t nvec = ra.u.page_bytes >> 4;
+  const bool single = contig && nvec % kThreads == 0 &&
+                      nvec == (int64_t)rot_contig_unroll<DT>() * kThreads;
+  bool grouped = G > 1 || (single && DT != DSR_DTYPE_FP8_E4M3);
+  if (const char* e = getenv("DSR_ROT_KERNEL")) {
+    if (!strcmp(e, "contig") && contig) grouped = false;
+    if (!strcmp(e, "grouped") && (G > 1 || single)) grouped = true;
+  }
+  if (grouped) {
+    wg = G > 1 ? rot_grouped_wg_per_cu<DT>() : kRotSingleWgPerCu;
     if (const char* e = getenv("DSR_ROT_GROUPED_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
   }
   const size_t dyn = rot_occupancy_lds(wg);
@@ -1099,7 +1119,7 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, hipStream_t s) {
     RotArgs rb = ra;
     rb.u = b;
     rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
-    if (G > 1) {
+    if (grouped) {
       if (style == DSR_ROPE_NEOX)
         kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb, G);
       else
