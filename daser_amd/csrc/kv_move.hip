@@ -620,6 +620,83 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
   }
 }
 
+// neox rows whose partner distance is not a power of two (head_dim 80, 96,
+// 192, ...): each wave takes rpw = 64 / row_vecs whole rows (lanes past
+// rpw * row_vecs idle), so a vector's partner half a rotation away lies in
+// the same wave and comes from lane +- half_vecs by an arbitrary-lane
+// shuffle. Idle lanes and rows past the page get an offset beyond the
+// descriptor: their loads read 0 and their stores are dropped. One unit per
+// workgroup, layer-major; V is copied in flat rounds alongside. Replaced the
+// pair-task kernel for these shapes (3.5-4.2 TB/s, 35-45% behind a plain
+// scatter of the same pages).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_rows_kernel(RotArgs ra) {
+  constexpr int U = rot_contig_unroll<DT>();
+  __shared__ float2 tab[kMaxRotHalf];
+  uint8_t *cache, *rec;
+  int l;
+  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
+  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  const int64_t p = u / ra.u.n_layers;
+  const int ti = ra.rope_idx[p];
+  const int64_t pb = ra.u.page_bytes;
+  if (ti < 0 || ti >= ra.n_tables) {
+    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    return;
+  }
+  const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
+  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const int nvec = (int)(pb >> 4);
+  const int rv = ra.row_vecs;
+  const int rpw = kWave / rv;
+  const int rows = nvec / rv;
+  const int slots = (rows + rpw - 1) / rpw;  // wave-sized groups of rows
+  const int lane = (int)threadIdx.x % kWave;
+  const int wave = (int)threadIdx.x / kWave;
+  const int r_in = lane / rv;
+  const int c = lane - r_in * rv;
+  const int h = ra.half_vecs;
+  const int partner = c < h ? lane + h : c < 2 * h ? lane - h : lane;
+  const int waves = kThreads / kWave;
+  const int rounds_k = (slots + waves * U - 1) / (waves * U);
+  const int rounds_v = (nvec + kThreads * U - 1) / (kThreads * U);
+  const int rounds = rounds_k > rounds_v ? rounds_k : rounds_v;
+  auto k_off = [&](int r, int k) {
+    const int row = ((r * U + k) * waves + wave) * rpw + r_in;
+    return r_in < rpw && row < rows ? (row * rv + c) << 4 : (int)pb;
+  };
+  VRound<U> v;
+  u32x4 x[U];
+  v.load(vs, threadIdx.x, nvec);
+#pragma unroll
+  for (int k = 0; k < U; ++k) x[k] = bload(ks, k_off(0, k));
+  const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
+  for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
+  float scale = 1.0f, inv_scale = 1.0f;
+  if (DT == DSR_DTYPE_FP8_E4M3) {
+    scale = ra.k_scale[ra.u.layer0 + l];
+    inv_scale = 1.0f / scale;
+  }
+  __syncthreads();
+  for (int r = 0; r < rounds; ++r) {  // uniform trip count: shuffles stay converged
+    const int base = r * kThreads * U + threadIdx.x;
+    if (r > 0) {
+      v.load(vs, base, nvec);
+#pragma unroll
+      for (int k = 0; k < U; ++k) x[k] = bload(ks, k_off(r, k));
+    }
+    v.store(vd, base, nvec);
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      u32x4 q;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) q[w] = (unsigned)__shfl((int)x[k][w], partner);
+      bstore(kd, k_off(r, k),
+             rotate_vec<DT, DSR_ROPE_NEOX>(ra, x[k], q, c, tab, scale, inv_scale));
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Small pages: several units per workgroup.
 //
@@ -1099,6 +1176,12 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, hipStream_t s) {
   const int G = contig ? units_per_group(ra.u.page_bytes, rot_contig_unroll<DT>(),
                                          kMaxRotHalf / ra.rot_half)
                        : 1;
+  // neox rows of <= 64 vectors whatever the partner distance: the row-aligned
+  // kernel (env DSR_ROT_KERNEL=pairs keeps the pair-task kernel).
+  bool rows_ok = !contig && style == DSR_ROPE_NEOX && ra.row_vecs <= kWave && h > 0 &&
+                 2 * h <= ra.row_vecs;
+  if (const char* e = getenv("DSR_ROT_KERNEL"))
+    if (!strcmp(e, "pairs")) rows_ok = false;
   // The grouped kernel also serves pages of exactly U vectors per lane
   // (G = 1), for 16-bit K. Env DSR_ROT_KERNEL=contig|grouped overrides the
   // choice where both apply, for in-process comparisons.
@@ -1129,6 +1212,8 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, hipStream_t s) {
         kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb);
       else
         kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(rb);
+    } else if (rows_ok) {
+      kv_scatter_rerotate_rows_kernel<DT><<<grid, kThreads, dyn, s>>>(rb);
     } else {
       kv_scatter_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb);
     }

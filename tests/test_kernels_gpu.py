@@ -203,7 +203,7 @@ def _rerotate_case(gpu, dt, style, head_dim, rot_dim, heads=4, layers=3, seed=0,
         ("fp16", "gptj", 256, 128),
         ("e4m3", "neox", 128, 128),
         ("e4m3", "gptj", 128, 96),
-        # partner distance not a power of two: the pair-task kernel
+        # partner distance not a power of two: the row-aligned kernel
         ("bf16", "neox", 80, 80),
         ("fp16", "neox", 96, 96),
         ("e4m3", "neox", 192, 192),
@@ -228,6 +228,21 @@ def test_rerotate_matches_oracle(gpu, dt, style, head_dim, rot_dim):
             a = torch.from_numpy(got[0].view(np.int16)).view(torch.bfloat16).float()
             b = torch.from_numpy(ref[0].view(np.int16)).view(torch.bfloat16).float()
             assert (a - b).abs().max().item() <= 1e-2 * max(1.0, b.abs().max().item())
+
+
+@pytest.mark.parametrize("dt,head_dim", [("bf16", 80), ("fp16", 96), ("e4m3", 192)])
+def test_rerotate_pair_task_kernel_matches_oracle(gpu, monkeypatch, dt, head_dim):
+    """The pair-task kernel (kept for rows of more than 64 vectors), forced
+    on the shapes the row-aligned kernel serves by default."""
+    print(f"case: rerotate pair-task {dt} D{head_dim}", flush=True)
+    monkeypatch.setenv("DSR_ROT_KERNEL", "pairs")
+    shape, dst, dst_ref, page_ids, page_delta = _rerotate_case(
+        gpu, dt, "neox", head_dim, head_dim, scale=40.0 if dt == "e4m3" else 1.0)
+    for l in range(shape.num_layers):
+        got = to_bits_np(dst[l], dt)
+        assert np.array_equal(got[1], dst_ref[l][1])
+        ok, msg = rotation_within_tolerance(got[0], dst_ref[l][0], dt)
+        assert ok, f"layer {l}: {msg}"
 
 
 @pytest.mark.parametrize("dt", ["bf16", "e4m3"])
