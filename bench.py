@@ -427,6 +427,46 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
     }
 
 
+def cpu_rerotate(torch, budget_s: float = 8.0) -> dict:
+    """fp32 torch rotate-half re-rotation on the host, vectorised: one reused
+    512-token chunk of config 3's shape (32 pages x 32 layers) loaded from
+    its records into a host cache, V copied and K rotated by one delta
+    (neox, theta 5e5), on all host threads; repeated to ~budget_s."""
+    from daser_amd import position, workloads
+
+    shape = workloads.LLAMA3_8B
+    L, bs, H, D = shape.num_layers, shape.block_size, shape.num_heads, shape.head_dim
+    n_pages, nb = 32, 256
+    g = torch.Generator().manual_seed(5)
+    recs = torch.randn(n_pages, L, 2, bs, H, D, generator=g).to(torch.bfloat16)
+    caches = [torch.zeros(2, nb, bs, H, D, dtype=torch.bfloat16) for _ in range(L)]
+    dst = torch.randperm(nb, generator=g)[:n_pages]
+    cs = position.delta_tables([12345], D, THETA)[0]  # [D/2, 2] float32
+    cos = torch.cat([cs[:, 0], cs[:, 0]])
+    sin = torch.cat([cs[:, 1], cs[:, 1]])
+
+    def once():
+        for l in range(L):
+            k = recs[:, l, 0].float()
+            rot = torch.cat([-k[..., D // 2:], k[..., :D // 2]], dim=-1)
+            caches[l][0, dst] = (k * cos + rot * sin).to(torch.bfloat16)
+            caches[l][1, dst] = recs[:, l, 1]
+
+    once()
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        once()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": n_pages * bs * n / el, "unit": "tokens/s",
+            "cores": torch.get_num_threads(), "kind": "torch fp32 rotate-half",
+            "sample": f"one 512-token chunk (32 pages x 32 layers, Llama-3-8B shape) x {n} "
+                      f"in {el:.1f} s"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -562,6 +602,8 @@ def main() -> int:
         r = reference_loop(torch, torch.device("cpu"), budget_s=10.0)
         r["threads"] = ncpu
         out["cpu_reference_loop"] = r
+        log(f"[bench] fp32 torch re-rotation on the CPU ({ncpu} threads)")
+        out["cpu_rerotate"] = cpu_rerotate(torch)
     print(json.dumps(out), flush=True)
     return 0
 
