@@ -15,8 +15,21 @@
 // buffer_store_dwordx4 through a descriptor bounded to the run), issuing
 // every load of a round before any store so each lane keeps up to 2*U
 // 16-byte requests in flight. No LDS is needed for the copy: both sides are
-// contiguous within a unit. The re-rotation kernel keeps the unit's
+// contiguous within a unit. The re-rotation kernels keep the unit's
 // (cos, sin) table in LDS.
+//
+// Kernel choice, by page and row geometry (all inside the entry points):
+//   gather / scatter: one unit per workgroup; pages of at most 4 KiB
+//     (scatter) or under 4 KiB (gather) take several units per workgroup
+//     (kv_copy_grouped_kernel).
+//   re-rotation: kv_scatter_rerotate_grouped_kernel for pages below U * 4
+//     KiB and 16-bit pages of exactly U * 4 KiB; kv_scatter_rerotate_contig_
+//     kernel for larger pages with a power-of-two partner distance;
+//     kv_scatter_rerotate_rows_kernel for other neox rows of <= 64 vectors;
+//     the pair-task kv_scatter_rerotate_kernel otherwise.
+//   token form (dsr_gather_slots / dsr_scatter_slots): kv_slots_small_kernel
+//     for rows of <= 32 vectors, kv_slots_kernel above.
+// Calls too large for one launch run as several over page (token) ranges.
 //
 // Reference being replaced: the Python per-(request, block, layer) torch
 // copy_ loops of daser/connector/daser_connector.py:536-551 (load) and
