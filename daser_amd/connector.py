@@ -146,17 +146,18 @@ class LoadPlan:
 def plan_store(reqs: dict[str, ReqStoreSpec], slot_bytes: int) -> StorePlan:
     """Record of request r's slot i at arena_r + i * SLOT, written to the file
     at start_slot * SLOT (reference :616-632, :652)."""
-    ids, offs, transfers = [], [], []
+    ids, transfers = [], []
     base = 0
     for spec in reqs.values():
         n = len(spec.block_ids)
         if n == 0:
             continue
         ids.extend(spec.block_ids)
-        offs.extend(base + i * slot_bytes for i in range(n))
         transfers.append((spec.chunk_key, base, n * slot_bytes, spec.start_slot * slot_bytes))
         base += n * slot_bytes
-    return StorePlan(np.asarray(ids, np.int32), np.asarray(offs, np.int64), transfers, base)
+    # records are packed back to back: page k of the step at k * SLOT
+    offs = np.arange(len(ids), dtype=np.int64) * slot_bytes
+    return StorePlan(np.asarray(ids, np.int32), offs, transfers, base)
 
 
 def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
@@ -164,7 +165,8 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
     segment scatters record j into block_ids[block_offset + j]. A segment
     whose new position differs from its stored one gets a rotation table for
     delta = new_pos - pos_offset (reference :498-551 for the unrotated part)."""
-    ids, offs, ridx, reads, page_read = [], [], [], [], []
+    ids: list[int] = []
+    seg_pages, seg_table, reads = [], [], []
     table: dict[int, int] = {}
     base = 0
     for spec in reqs.values():
@@ -179,16 +181,16 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
                 raise ValueError(f"segment of {spec.chunk_key[:8]} exceeds its block list")
             reads.append((base, n * slot_bytes, seg.start_slot * slot_bytes))
             delta = 0 if seg.new_pos is None else int(seg.new_pos) - int(seg.pos_offset)
-            t = -1 if delta == 0 else table.setdefault(delta, len(table))
-            for j in range(n):
-                ids.append(blocks[seg.block_offset + j])
-                offs.append(base + j * slot_bytes)
-                ridx.append(t)
-                page_read.append(len(reads) - 1)
+            seg_table.append(-1 if delta == 0 else table.setdefault(delta, len(table)))
+            seg_pages.append(n)
+            ids.extend(blocks[seg.block_offset:seg.block_offset + n])
             base += n * slot_bytes
-    return LoadPlan(np.asarray(ids, np.int32), np.asarray(offs, np.int64),
-                    np.asarray(ridx, np.int32), list(table.keys()), reads, base,
-                    np.asarray(page_read, np.int64))
+    # segments' records are packed back to back: page k at k * SLOT
+    counts = np.asarray(seg_pages, np.int64)
+    return LoadPlan(np.asarray(ids, np.int32),
+                    np.arange(len(ids), dtype=np.int64) * slot_bytes,
+                    np.repeat(np.asarray(seg_table, np.int32), counts), list(table.keys()),
+                    reads, base, np.repeat(np.arange(len(reads), dtype=np.int64), counts))
 
 
 # ---------------------------------------------------------------------------
