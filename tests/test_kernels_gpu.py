@@ -91,6 +91,40 @@ def test_per_layer_launches_match_all_layer_launch(gpu):
     assert torch.equal(full, per)
 
 
+@pytest.mark.parametrize("heads,head_dim,dt", [
+    (8, 128, "bf16"),   # 32 KiB pages: grouped kernel, one unit per workgroup
+    (1, 128, "bf16"),   # 4 KiB: grouped, 8 units per workgroup
+    (8, 128, "e4m3"),   # 16 KiB e4m3: contig kernel
+    (1, 128, "e4m3"),   # 2 KiB e4m3: grouped
+    (4, 96, "e4m3"),    # row-aligned kernel
+])
+def test_per_layer_rerotate_matches_all_layer_launch(gpu, heads, head_dim, dt):
+    """Re-rotation launched per layer range (layers=(l, 1)) writes the same
+    bytes as one launch over all layers: every kernel reads layer l's K scale
+    at k_scale[layer0 + l]."""
+    print(f"case: per-layer rerotate H{heads} D{head_dim} {dt}", flush=True)
+    shape = KVShape(6, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    wl = workloads.ragged(shape, 4, 40, 400, seed=13, num_blocks=128)
+    src = rand_caches(shape, wl.num_blocks, dt, gpu, seed=80, scale=40.0 if dt == "e4m3" else 1.0)
+    st = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(src), wl.page_ids, wl.slot_offsets, st)
+    ridx = (np.arange(wl.n_pages) % 3 - 1).astype(np.int32)
+    tabs = position.delta_tables([517, 32767], head_dim, 500000.0, device=gpu)
+    ks = torch.linspace(0.05, 0.6, shape.num_layers, device=gpu) if dt == "e4m3" else None
+    dst = np.random.default_rng(2).permutation(wl.num_blocks)[:wl.n_pages].astype(np.int32)
+    one = [torch.zeros_like(c) for c in src]
+    ops.scatter_rerotate(ops.LayerTable(one), dst, wl.slot_offsets, st, tabs, ridx, k_scale=ks)
+    per = [torch.zeros_like(c) for c in src]
+    t = ops.LayerTable(per)
+    for l in range(shape.num_layers):
+        ops.scatter_rerotate(t, dst, wl.slot_offsets, st, tabs, ridx, k_scale=ks,
+                             layers=(l, 1))
+    torch.cuda.synchronize()
+    for l in range(shape.num_layers):
+        assert torch.equal(one[l].view(torch.uint8), per[l].view(torch.uint8)), f"layer {l}"
+    assert not torch.equal(one[0].view(torch.uint8), torch.zeros_like(one[0]).view(torch.uint8))
+
+
 def test_strided_layout_block_major(gpu):
     """A cache allocated block-major (NB, 2, bs, H, D) and viewed as
     (2, NB, ...) has kv_stride = page, page_stride = 2 pages."""
