@@ -50,6 +50,35 @@ class FixedOffsetEncoder(PositionEncoder):
         return int(meta.pos_offset)
 
 
+class PrefillOffsetEncoder(PositionEncoder):
+    """Stores each chunk at the position it was actually prefilled at.
+
+    The reference's interface anticipates encoders beyond the fixed offset
+    (daser/position/base.py:10-20). A chunk cached out of the middle of a
+    prompt (a retrieved passage at token 3000) holds K rotated for positions
+    3000.., so its stored offset must be 3000 for a later load at another
+    position to re-rotate by the right delta. Whoever splits the prompt
+    calls :meth:`note_position` before the chunk is allocated;
+    :meth:`assign_offset` then returns that position once (and ``default``
+    for chunks never noted, e.g. prompt prefixes at 0).
+    """
+
+    def __init__(self, default: int = 0) -> None:
+        self._default = int(default)
+        self._pending: dict[str, int] = {}
+
+    def note_position(self, chunk_key: str, first_position: int) -> None:
+        if first_position < 0:
+            raise ValueError("positions are non-negative")
+        self._pending[chunk_key] = int(first_position)
+
+    def assign_offset(self, chunk_key: str, token_count: int) -> int:
+        return self._pending.pop(chunk_key, self._default)
+
+    def get_offset(self, meta) -> int:
+        return int(meta.pos_offset)
+
+
 def rope_inv_freq(rot_dim: int, theta: float) -> np.ndarray:
     """inv_freq_j = theta^(-2j/rot_dim), j < rot_dim/2, in float64
     (RoFormer, Su et al. 2021; the Llama / GPT-NeoX convention)."""
