@@ -1271,7 +1271,8 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
                          num_blocks, page_ids, slot_offsets, n_pages, staging,
                          staging_bytes, layer_bytes, layer0);
   // Grouped only below one workgroup's 4 KiB: from 4 KiB up the one-unit
-  // kernel measured faster (6.14 vs 5.57 TB/s at 4 KiB pages).
+  // kernel measured faster (6.14 vs 5.57 TB/s at 4 KiB pages; 3-8% at 8, 16
+  // and 32 KiB).
   const int G = page_bytes < kThreads * 16 ? units_per_group(page_bytes, kGatherUnroll, kMaxGroup) : 1;
   return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
     if (G > 1)
