@@ -2,9 +2,14 @@
 // hipMalloc, gathers a permuted page list into slot records with dsr_gather,
 // checks the records against a host memcpy of the same layout, scatters them
 // into a second cache with dsr_scatter and checks the pages, then re-rotates
-// with a zero table (rope_idx -1) and checks a bit-exact copy. Exit code 0 on
-// success; prints the failing check otherwise.
+// with a zero table (rope_idx -1) and checks a bit-exact copy; gathers the
+// same records token by token with dsr_gather_slots; writes them to a store
+// file through the staging ring and reads them back. Exit code 0 on success;
+// prints the failing check otherwise.
+#include <fcntl.h>
 #include <hip/hip_runtime_api.h>
+#include <stdlib.h>
+#include <unistd.h>
 
 #include <cstdint>
 #include <cstdio>
@@ -101,6 +106,53 @@ int main() {
   REQUIRE(dsr_gather(bases, L, 4100, page, page, NB, d_ids, d_offs, n, stg, n * slot,
                      layer_bytes, 0, nullptr) == DSR_ERR_ALIGN,
           "misaligned stride rejected");
+
+  // token form: slot_mapping of the same pages, full pages -> the same records
+  const int64_t row = (int64_t)H * D * 2;
+  std::vector<int64_t> sm(n * bs), ro(n * bs);
+  for (int p = 0; p < n; ++p)
+    for (int t = 0; t < bs; ++t) {
+      sm[p * bs + t] = (int64_t)ids[p] * bs + t;
+      ro[p * bs + t] = offs[p] + t * row;
+    }
+  int64_t *d_sm, *d_ro;
+  uint8_t* stg2;
+  REQUIRE(hipMalloc(&d_sm, sm.size() * 8) == hipSuccess, "hipMalloc");
+  REQUIRE(hipMalloc(&d_ro, ro.size() * 8) == hipSuccess, "hipMalloc");
+  REQUIRE(hipMalloc(&stg2, n * slot) == hipSuccess, "hipMalloc");
+  hipMemcpy(d_sm, sm.data(), sm.size() * 8, hipMemcpyHostToDevice);
+  hipMemcpy(d_ro, ro.data(), ro.size() * 8, hipMemcpyHostToDevice);
+  hipMemset(stg2, 0, n * slot);
+  rc = dsr_gather_slots(bases, L, NB * page, page, page, NB, bs, row, d_sm, d_ro, n * bs, stg2,
+                        n * slot, layer_bytes, 0, nullptr);
+  REQUIRE(rc == 0, dsr_error_string(rc));
+  std::vector<uint8_t> got2(n * slot);
+  hipMemcpy(got2.data(), stg2, got2.size(), hipMemcpyDeviceToHost);
+  REQUIRE(got2 == want, "slot_mapping gather equals page gather");
+
+  // staging ring: records -> store file at a slot offset -> back to the device
+  char path[] = "/tmp/dsr_abi_XXXXXX";
+  const int fd = mkstemp(path);
+  REQUIRE(fd >= 0, "mkstemp");
+  REQUIRE(ftruncate(fd, 8 * slot) == 0, "ftruncate");
+  close(fd);
+  dsr_ring* ring = nullptr;
+  REQUIRE(dsr_ring_open("/tmp/dsr_abi_missing_file", page, 2, 0, &ring) == DSR_ERR_NOFILE,
+          "missing store file rejected");
+  rc = dsr_ring_open(path, page, 2, 0, &ring);  // pieces smaller than the transfer
+  REQUIRE(rc == 0 && ring, dsr_error_string(rc));
+  rc = dsr_ring_write(ring, stg, n * slot, 3 * slot, nullptr);
+  REQUIRE(rc == 0, dsr_error_string(rc));
+  hipMemset(stg2, 0, n * slot);
+  rc = dsr_ring_read(ring, stg2, n * slot, 3 * slot, nullptr);
+  REQUIRE(rc == 0, dsr_error_string(rc));
+  REQUIRE(hipDeviceSynchronize() == hipSuccess, "device sync");
+  hipMemcpy(got2.data(), stg2, got2.size(), hipMemcpyDeviceToHost);
+  REQUIRE(got2 == want, "ring write/read round trip");
+  REQUIRE(dsr_ring_read(ring, stg2, n * slot, 6 * slot, nullptr) == DSR_ERR_IO,
+          "read past the end of the file");
+  REQUIRE(dsr_ring_close(ring) == 0, "ring close");
+  unlink(path);
   REQUIRE(hipDeviceSynchronize() == hipSuccess, "device sync");
   printf("abi_roundtrip ok\n");
   return 0;
