@@ -25,6 +25,7 @@ Extra ``kv_connector_extra_config`` keys: ``rope_theta`` (default 10000),
 ``save_mode`` ("per_layer" | "deferred": one all-layer gather in
 wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry),
 ``io_backend`` ("native": the C++ io_uring ring of libdaser_kv, default;
+"direct": the same ring with the store file opened O_DIRECT;
 "python": the threaded ring of store_io.PinnedRingIO), ``save_stream``
 ("side": per-layer gathers on a side stream after the layer's KV writes,
 overlapping later layers, default; "current": on the model's stream).
@@ -214,8 +215,8 @@ class KVDataPlane:
                  k_scales: Optional[torch.Tensor] = None) -> None:
         if save_mode not in ("per_layer", "deferred"):
             raise ValueError("save_mode must be 'per_layer' or 'deferred'")
-        if io_backend not in ("native", "python"):
-            raise ValueError("io_backend must be 'native' or 'python'")
+        if io_backend not in ("native", "direct", "python"):
+            raise ValueError("io_backend must be 'native', 'direct' or 'python'")
         if save_stream not in ("side", "current"):
             raise ValueError("save_stream must be 'side' or 'current'")
         self.io_backend = io_backend
@@ -268,9 +269,17 @@ class KVDataPlane:
         if self.save_stream == "side" and lay.device.type == "cuda" and self._side is None:
             self._side = torch.cuda.Stream(lay.device)  # default priority
         if self.io is None:
-            ring = NativeRingIO if self.io_backend == "native" else PinnedRingIO
-            self.io = ring(self.store_path, lay.device, slot_bytes=self._io_slot_bytes,
-                           n_slots=self._io_slots)
+            if self.io_backend == "python":
+                self.io = PinnedRingIO(self.store_path, lay.device,
+                                       slot_bytes=self._io_slot_bytes, n_slots=self._io_slots)
+            else:
+                direct = self.io_backend == "direct"
+                if direct and self.slot_bytes % 4096:
+                    raise ValueError("io_backend='direct' needs a slot record size that is a "
+                                     "multiple of 4096 bytes")
+                self.io = NativeRingIO(self.store_path, lay.device,
+                                       slot_bytes=self._io_slot_bytes, n_slots=self._io_slots,
+                                       direct=direct)
         return self.slot_bytes
 
     @property

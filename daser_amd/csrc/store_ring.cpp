@@ -139,6 +139,7 @@ struct dsr_ring {
   int64_t slot_bytes = 0;
   int n_slots = 0;
   bool host = false;
+  bool direct = false;  // O_DIRECT: offsets and lengths in kDirectAlign units
   bool use_uring = false;
   Uring uring;
   std::vector<uint8_t*> slots;
@@ -151,6 +152,14 @@ struct dsr_ring {
 };
 
 namespace {
+
+// O_DIRECT transfers need file offsets, lengths and buffers aligned to the
+// device's logical block; 4 KiB covers NVMe and the usual file systems.
+constexpr int64_t kDirectAlign = 4096;
+
+bool direct_misaligned(const dsr_ring* r, int64_t nbytes, int64_t file_offset) {
+  return r->direct && (nbytes % kDirectAlign || file_offset % kDirectAlign);
+}
 
 // Completes a transfer's piece synchronously (fallback path, or the rest of
 // a short io_uring transfer). Returns 0 or -errno; 0 bytes read is -EIO.
@@ -265,6 +274,11 @@ int dsr_ring_open(const char* path, int64_t slot_bytes, int n_slots, int flags,
   r->slot_bytes = slot_bytes;
   r->n_slots = n_slots;
   r->host = (flags & DSR_RING_HOST) != 0;
+  r->direct = (flags & DSR_RING_DIRECT) != 0;
+  if (r->direct && slot_bytes % kDirectAlign) {
+    delete r;
+    return DSR_ERR_ALIGN;
+  }
   r->fd = open(path, O_RDWR | O_CLOEXEC | ((flags & DSR_RING_DIRECT) ? O_DIRECT : 0));
   if (r->fd < 0) {
     r->last_errno = errno;
@@ -276,7 +290,10 @@ int dsr_ring_open(const char* path, int64_t slot_bytes, int n_slots, int flags,
   r->state.assign((size_t)n_slots, kFree);
   int rc = 0;
   for (int i = 0; i < n_slots && rc == 0; ++i) {
-    if (r->host) {
+    // Pinned memory from hipHostMalloc is a driver mapping that O_DIRECT
+    // cannot pin (the file operations fail with EFAULT), so direct mode
+    // stages through aligned pageable slots and HIP's pageable copy path.
+    if (r->host || r->direct) {
       if (posix_memalign((void**)&r->slots[i], 4096, (size_t)slot_bytes)) rc = DSR_ERR_ARG;
     } else {
       rc = hip_rc(hipHostMalloc((void**)&r->slots[i], (size_t)slot_bytes, hipHostMallocDefault));
@@ -306,6 +323,7 @@ int dsr_ring_write(dsr_ring* r, const void* src, int64_t nbytes, int64_t file_of
                    dsr_stream_t producer) {
   if (!r || (!src && nbytes) || nbytes < 0 || file_offset < 0) return DSR_ERR_ARG;
   if (nbytes == 0) return DSR_OK;
+  if (direct_misaligned(r, nbytes, file_offset)) return DSR_ERR_ALIGN;
   pthread_mutex_lock(&r->mu);
   const std::vector<Piece> pieces = split(nbytes, r->slot_bytes, file_offset);
   const int64_t np = (int64_t)pieces.size(), S = r->n_slots;
@@ -374,6 +392,7 @@ int dsr_ring_read(dsr_ring* r, void* dst, int64_t nbytes, int64_t file_offset,
                   dsr_stream_t consumer) {
   if (!r || (!dst && nbytes) || nbytes < 0 || file_offset < 0) return DSR_ERR_ARG;
   if (nbytes == 0) return DSR_OK;
+  if (direct_misaligned(r, nbytes, file_offset)) return DSR_ERR_ALIGN;
   pthread_mutex_lock(&r->mu);
   const std::vector<Piece> pieces = split(nbytes, r->slot_bytes, file_offset);
   const int64_t np = (int64_t)pieces.size(), S = r->n_slots;
@@ -457,7 +476,7 @@ int dsr_ring_close(dsr_ring* r) {
   r->uring.close_all();
   for (uint8_t* p : r->slots) {
     if (!p) continue;
-    if (r->host)
+    if (r->host || r->direct)
       free(p);
     else
       hipHostFree(p);

@@ -207,7 +207,9 @@ int dsr_scatter_slots(const uint64_t* layer_base, int n_layers, int64_t kv_strid
 typedef struct dsr_ring dsr_ring;
 
 #define DSR_RING_HOST 1     /* src/dst are host memory: memcpy, no HIP calls */
-#define DSR_RING_DIRECT 2   /* open the file with O_DIRECT                   */
+#define DSR_RING_DIRECT 2   /* open the file with O_DIRECT: slot_bytes, file
+                               offsets and transfer sizes must be multiples of
+                               4096 (DSR_ERR_ALIGN otherwise)               */
 #define DSR_RING_NO_URING 4 /* use pread/pwrite even if io_uring works       */
 
 /* Opens `path` (must exist: DSR_ERR_NOFILE otherwise) and allocates the

@@ -67,7 +67,7 @@ def _file_records(path, start_slot, n):
 @pytest.mark.parametrize("mode,backend,stream", [
     ("per_layer", "native", "side"), ("deferred", "native", "side"),
     ("per_layer", "python", "side"), ("per_layer", "native", "current"),
-    ("deferred", "python", "current")])
+    ("deferred", "python", "current"), ("per_layer", "direct", "side")])
 def test_save_writes_reference_layout(gpu, tmp_path, mode, backend, stream):
     print(f"case: connector save {mode} {backend} {stream}", flush=True)
     w, ipc = _worker(tmp_path, save_mode=mode, io_backend=backend, save_stream=stream)
@@ -176,13 +176,15 @@ def test_pinned_ring_device_round_trip(gpu, tmp_path):
     assert torch.equal(src, dst)
 
 
-@pytest.mark.parametrize("uring", [True, False])
-def test_native_ring_device_round_trip(gpu, tmp_path, uring):
-    print(f"case: native ring uring={uring}", flush=True)
+@pytest.mark.parametrize("uring,direct", [(True, False), (False, False), (True, True)])
+def test_native_ring_device_round_trip(gpu, tmp_path, uring, direct):
+    print(f"case: native ring uring={uring} direct={direct}", flush=True)
     path = str(tmp_path / "n.store")
     preallocate_store(path, 16 << 20)
-    src = torch.randint(0, 256, (5_000_001,), dtype=torch.uint8, device=gpu)
-    with NativeRingIO(path, gpu, slot_bytes=1 << 20, n_slots=3, use_io_uring=uring) as io:
+    n = 5_000_001 if not direct else 5 << 20  # O_DIRECT: whole 4 KiB blocks
+    src = torch.randint(0, 256, (n,), dtype=torch.uint8, device=gpu)
+    with NativeRingIO(path, gpu, slot_bytes=1 << 20, n_slots=3, use_io_uring=uring,
+                      direct=direct) as io:
         src.add_(1)  # producer-stream work the ring must wait for
         io.write_from_device(src, 65536)
         dst = torch.zeros_like(src)

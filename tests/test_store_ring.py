@@ -76,3 +76,39 @@ def test_closed_ring_refuses(store):
     io.close()
     with pytest.raises(StoreIOError):
         io.write_from_device(torch.ones(4, dtype=torch.uint8), 0)
+
+
+def _direct_ring(store, **kw):
+    from daser_amd._lib import DSR_ERR_IO, DaserKVError
+
+    try:
+        return NativeRingIO(store, "cpu", direct=True, **kw)
+    except DaserKVError as e:
+        if e.code == DSR_ERR_IO:
+            pytest.skip("file system without O_DIRECT")
+        raise
+
+
+@pytest.mark.parametrize("uring", [True, False])
+def test_direct_io_round_trip_and_alignment(store, uring):
+    """O_DIRECT mode: 4 KiB-aligned transfers round-trip through the file;
+    unaligned offsets, sizes or slot sizes are DSR_ERR_ALIGN before any I/O."""
+    from daser_amd._lib import DSR_ERR_ALIGN, DaserKVError
+
+    src = torch.from_numpy(np.random.default_rng(4).integers(0, 256, 1 << 20, dtype=np.uint8))
+    with _direct_ring(store, slot_bytes=65536, n_slots=3, use_io_uring=uring) as io:
+        io.write_from_device(src, 8192)
+        dst = torch.zeros_like(src)
+        io.read_into_device(dst, 8192)
+        assert torch.equal(src, dst)
+        for n, off in ((4096, 100), (1000, 4096)):
+            with pytest.raises(DaserKVError) as e:
+                io.write_from_device(src[:n], off)
+            assert e.value.code == DSR_ERR_ALIGN
+        io.read_into_device(dst[:4096], 8192)  # still usable
+    with open(store, "rb") as f:
+        f.seek(8192)
+        assert f.read(src.numel()) == src.numpy().tobytes()
+    with pytest.raises(DaserKVError) as e:
+        NativeRingIO(store, "cpu", slot_bytes=5000, direct=True)
+    assert e.value.code == DSR_ERR_ALIGN
