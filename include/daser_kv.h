@@ -209,7 +209,9 @@ typedef struct dsr_ring dsr_ring;
 #define DSR_RING_HOST 1     /* src/dst are host memory: memcpy, no HIP calls */
 #define DSR_RING_DIRECT 2   /* open the file with O_DIRECT: slot_bytes, file
                                offsets and transfer sizes must be multiples of
-                               4096 (DSR_ERR_ALIGN otherwise)               */
+                               4096 (DSR_ERR_ALIGN otherwise). The slots are
+                               then 4 KiB-aligned pageable memory (O_DIRECT
+                               cannot use hipHostMalloc'd pages)            */
 #define DSR_RING_NO_URING 4 /* use pread/pwrite even if io_uring works       */
 
 /* Opens `path` (must exist: DSR_ERR_NOFILE otherwise) and allocates the
