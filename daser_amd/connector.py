@@ -26,7 +26,9 @@ Extra ``kv_connector_extra_config`` keys: ``rope_theta`` (default 10000),
 wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry),
 ``io_backend`` ("native": the C++ io_uring ring of libdaser_kv, default;
 "direct": the same ring with the store file opened O_DIRECT;
-"python": the threaded ring of store_io.PinnedRingIO), ``save_stream``
+"python": the threaded ring of store_io.PinnedRingIO), ``k_scale`` (one K
+scale for every layer of an fp8 cache, when the attention modules' own
+``_k_scale`` are not reachable), ``save_stream``
 ("side": per-layer gathers on a side stream after the layer's KV writes,
 overlapping later layers, default; "current": on the model's stream).
 """
@@ -458,6 +460,7 @@ class DaserConnector(KVConnectorBase_V1):
                 io_backend=extra.get("io_backend", "native"),
                 save_stream=extra.get("save_stream", "side"),
             )
+            self._k_scale_cfg = extra.get("k_scale")  # uniform fp8 K scale, optional
             self._meta: Optional[DaserConnectorMeta] = None
             self._store_plan: Optional[StorePlan] = None
             self._store_arena: Optional[torch.Tensor] = None
@@ -566,7 +569,33 @@ class DaserConnector(KVConnectorBase_V1):
         if self._meta is None or not self._meta.reqs_to_load or self._plane.table is None:
             return
         plan = plan_load(self._meta.reqs_to_load, self._slot_size)
+        if plan.deltas and self._plane.table.layout.dtype == torch.float8_e4m3fn:
+            self._plane.k_scales = self._fp8_k_scales(forward_context)
         self._plane.load(plan)
+
+    def _fp8_k_scales(self, forward_context: Any) -> torch.Tensor:
+        """Per-layer K scales of an e4m3 cache, in registration order: the
+        attention modules' ``_k_scale`` (vLLM keeps them there; the forward
+        context maps layer names to the modules in ``no_compile_layers``), or
+        ``kv_connector_extra_config["k_scale"]`` for one scale everywhere.
+        Read at every load, since vLLM may recompute them after its first
+        pass. Rotating e4m3 codes needs them; without them this raises."""
+        dev = self._plane.device
+        names = self._plane.layer_names
+        layers = getattr(forward_context, "no_compile_layers", None) or {}
+        found = [getattr(layers.get(n), "_k_scale", None) for n in names]
+        if all(t is not None for t in found):
+            return torch.stack([torch.as_tensor(t, dtype=torch.float32, device=dev).reshape(())
+                                for t in found])
+        if self._k_scale_cfg is not None:
+            return torch.full((len(names),), float(self._k_scale_cfg), dtype=torch.float32,
+                              device=dev)
+        missing = [n for n, t in zip(names, found) if t is None]
+        raise ValueError(
+            "re-rotating an fp8 KV cache needs each layer's K scale: none found for "
+            f"{missing[:3]}{'...' if len(missing) > 3 else ''} in "
+            "forward_context.no_compile_layers[layer]._k_scale, and no "
+            "kv_connector_extra_config['k_scale']")
 
     def wait_for_layer_load(self, layer_name: str) -> None:
         return

@@ -285,3 +285,48 @@ def test_unknown_layer_warns_and_others_still_save(gpu, tmp_path, caplog):
     assert np.array_equal(_file_records(tmp_path / "daser.store", 3, 3), ref)
     assert sorted(ipc.committed) == ["ka", "kb"]
     w.shutdown()
+
+
+def test_fp8_load_rerotates_with_module_scales(gpu, tmp_path):
+    """An e4m3 cache saved and reloaded at a new position through the
+    connector: K is re-rotated with each layer's scale taken from the
+    attention modules of the forward context, V and the unmoved request
+    are bit-exact."""
+    print("case: connector fp8 rerotate", flush=True)
+    shape = KVShape(3, 2, 64, 16, 1)
+    slot = shape.slot_bytes
+    w, _ = _worker(tmp_path, rope_theta=500000.0)
+    caches = rand_caches(shape, 16, "e4m3", gpu, seed=38, scale=40.0)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    _save(w, named, {"a": C.ReqStoreSpec("ka", 3, 3, [5, 9, 2], 3 * slot, 40),
+                     "b": C.ReqStoreSpec("kb", 10, 1, [7], 10 * slot, 16)})
+    recs = np.fromfile(tmp_path / "daser.store", dtype=np.uint8, count=3 * slot,
+                       offset=3 * slot)
+    scales = np.array([0.02, 0.05, 0.11], np.float32)
+    fc = SimpleNamespace(no_compile_layers={
+        n: SimpleNamespace(_k_scale=torch.tensor(float(v), device=gpu))
+        for n, v in zip(named, scales)})
+    fresh = [torch.zeros_like(c) for c in caches]
+    w2, _ = _worker(tmp_path, rope_theta=500000.0)
+    w2.register_kv_caches(_named(fresh))
+    w2.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_load={
+        "x": C.ReqLoadSpec("ka", 3, 3, [1, 12, 4], 3 * slot, 40, pos_offset=100, new_pos=2148),
+        "y": C.ReqLoadSpec("kb", 10, 1, [0], 10 * slot, 16, pos_offset=5, new_pos=5),
+    }))
+    w2.start_load_kv(fc)
+    torch.cuda.synchronize()
+    ref = [np.zeros_like(to_bits_np(c, "e4m3")) for c in caches]
+    oracle.scatter_rerotate(ref, [1, 12, 4], np.arange(3) * slot, recs, shape.layer_bytes,
+                            dtype=oracle.E4M3, rot_dim=64, style=oracle.NEOX,
+                            stored_pos=np.full(3, 100), new_pos=np.full(3, 2148),
+                            rotate=np.ones(3), theta=500000.0, k_scale=scales)
+    for l, f in enumerate(fresh):
+        got = to_bits_np(f, "e4m3")
+        assert np.array_equal(got[1][[1, 12, 4]], ref[l][1][[1, 12, 4]])
+        ok, msg = oracle.rotation_within_tolerance(got[0][[1, 12, 4]], ref[l][0][[1, 12, 4]],
+                                                   oracle.E4M3)
+        assert ok, f"layer {l}: {msg}"
+        assert torch.equal(f[:, 0].view(torch.uint8), caches[l][:, 7].view(torch.uint8))
+    w.shutdown()
+    w2.shutdown()

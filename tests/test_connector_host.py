@@ -268,3 +268,39 @@ def test_worker_hooks_without_metadata_are_noops(tmp_path):
         w.clear_connector_metadata()
     assert (tmp_path / "s").stat().st_size > 0  # store pre-allocated at registration
     w.shutdown()
+
+
+def test_fp8_rotated_load_needs_k_scales(tmp_path):
+    """Re-rotating e4m3 codes needs each layer's K scale: taken from the
+    attention modules in forward_context.no_compile_layers, or from the
+    extra config; with neither the load raises before any I/O."""
+    from types import SimpleNamespace
+
+    import torch
+
+    from daser_amd import connector as C
+
+    def worker(**extra):
+        cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(kv_connector_extra_config=dict(
+            store_path=str(tmp_path / "s"), io_backend="python", io_slot_mb=0.03125,
+            io_slots=2, **extra)))
+        w = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=object())
+        names = [f"model.layers.{i}.self_attn.attn" for i in range(3)]
+        w.register_kv_caches({n: torch.zeros(2, 8, 16, 1, 64, dtype=torch.float8_e4m3fn)
+                              for n in names})
+        return w, names
+
+    w, names = worker()
+    slot = w._slot_size
+    w.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_load={
+        "r": C.ReqLoadSpec("k", 0, 1, [2], 0, 16, pos_offset=0, new_pos=100)}))
+    with pytest.raises(ValueError, match="K scale"):
+        w.start_load_kv(SimpleNamespace(no_compile_layers={}))
+    fc = SimpleNamespace(no_compile_layers={
+        n: SimpleNamespace(_k_scale=torch.tensor([0.5 + i])) for i, n in enumerate(names)})
+    assert torch.equal(w._fp8_k_scales(fc), torch.tensor([0.5, 1.5, 2.5]))
+    w.shutdown()
+    w2, _ = worker(k_scale=0.25)
+    assert torch.equal(w2._fp8_k_scales(None), torch.full((3,), 0.25))
+    assert slot == 3 * 2 * 16 * 64
+    w2.shutdown()
