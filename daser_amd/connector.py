@@ -461,6 +461,8 @@ class DaserConnector(KVConnectorBase_V1):
                 save_stream=extra.get("save_stream", "side"),
             )
             self._k_scale_cfg = extra.get("k_scale")  # uniform fp8 K scale, optional
+            cache_cfg = getattr(vllm_config, "cache_config", None)
+            self._cache_dtype = str(getattr(cache_cfg, "cache_dtype", "auto"))
             self._meta: Optional[DaserConnectorMeta] = None
             self._store_plan: Optional[StorePlan] = None
             self._store_arena: Optional[torch.Tensor] = None
@@ -545,6 +547,11 @@ class DaserConnector(KVConnectorBase_V1):
 
     # --------------------------------------------------------------- worker
     def register_kv_caches(self, kv_caches: dict[str, torch.Tensor]) -> None:
+        if self._cache_dtype in ("fp8", "fp8_e4m3"):
+            # vLLM may hold an fp8 cache as raw uint8; the re-rotation needs the
+            # element format (OCP e4m3fn on gfx950). A view, no copy.
+            kv_caches = {n: t.view(torch.float8_e4m3fn) if t.dtype == torch.uint8 else t
+                         for n, t in kv_caches.items()}
         self._slot_size = self._plane.register(kv_caches, self._slot_size)
         logger.info("[CONNECTOR] %d layers, slot_size=%d", len(kv_caches), self._slot_size)
 

@@ -304,3 +304,27 @@ def test_fp8_rotated_load_needs_k_scales(tmp_path):
     assert torch.equal(w2._fp8_k_scales(None), torch.full((3,), 0.25))
     assert slot == 3 * 2 * 16 * 64
     w2.shutdown()
+
+
+@pytest.mark.parametrize("cache_dtype,expect", [("fp8", "float8_e4m3fn"),
+                                                 ("fp8_e4m3", "float8_e4m3fn"),
+                                                 ("auto", "uint8")])
+def test_uint8_fp8_cache_viewed_as_e4m3(tmp_path, cache_dtype, expect):
+    """vLLM may allocate an fp8 cache as uint8; with cache_config.cache_dtype
+    fp8 the connector registers an e4m3fn view (no copy)."""
+    from types import SimpleNamespace
+
+    import torch
+
+    from daser_amd import connector as C
+
+    cfg = SimpleNamespace(
+        cache_config=SimpleNamespace(cache_dtype=cache_dtype),
+        kv_transfer_config=SimpleNamespace(kv_connector_extra_config=dict(
+            store_path=str(tmp_path / "s"), io_backend="python", io_slot_mb=0.03125,
+            io_slots=2)))
+    w = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=object())
+    t = torch.zeros(2, 8, 16, 1, 64, dtype=torch.uint8)
+    w.register_kv_caches({"model.layers.0.self_attn.attn": t})
+    assert str(w._plane.table.layout.dtype) == f"torch.{expect}"
+    w.shutdown()
