@@ -28,7 +28,10 @@ wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry),
 "direct": the same ring with the store file opened O_DIRECT;
 "python": the threaded ring of store_io.PinnedRingIO), ``k_scale`` (one K
 scale for every layer of an fp8 cache, when the attention modules' own
-``_k_scale`` are not reachable), ``save_stream``
+``_k_scale`` are not reachable), ``async_save`` (wait_for_save returns once
+the gathers are enqueued and ordered before the next step's KV writes; file
+writes and commits finish on a background writer; default False, the
+reference's blocking behaviour), ``save_stream``
 ("side": per-layer gathers on a side stream after the layer's KV writes,
 overlapping later layers, default; "current": on the model's stream).
 """
@@ -242,6 +245,9 @@ class KVDataPlane:
         self._io_slot_bytes = io_slot_bytes
         self._io_slots = io_slots
         self.k_scales = k_scales
+        self._writer = None  # background writer of flush_async
+        self._idle_stream: Optional[torch.cuda.Stream] = None
+        self._pending_writes: list = []
         self.table = None
         self.layer_names: list[str] = []
         self.layer_idx: dict[str, int] = {}
@@ -337,6 +343,46 @@ class KVDataPlane:
         with self._on_save_stream(arena):
             ops.gather(self.table, ids, offs, arena)
 
+    def flush_async(self, plan: StorePlan, arena: torch.Tensor, done) -> None:
+        """Like flush, but the file writes run on a background writer thread
+        (one, so steps are written in order) and this returns at once. The
+        current stream is first ordered after the step's gathers, so vLLM may
+        reuse the cache blocks as soon as the gathers have run; the arena
+        keeps the records until they are written. ``done(keys, error)`` is
+        called on the writer thread with the chunk keys fully written (all
+        of them unless ``error``)."""
+        from concurrent.futures import ThreadPoolExecutor
+
+        cur = torch.cuda.current_stream(self.device)
+        ev = torch.cuda.Event()
+        ev.record(self._side if self._side is not None else cur)
+        if self._side is not None:
+            cur.wait_event(ev)
+        if self._writer is None:
+            self._writer = ThreadPoolExecutor(max_workers=1, thread_name_prefix="daser-save")
+            self._idle_stream = torch.cuda.Stream(self.device)  # never given work
+
+        def job() -> None:
+            keys: list[str] = []
+            err: Optional[BaseException] = None
+            try:
+                ev.synchronize()  # the gathers into this arena have run
+                for key, off, nbytes, file_off in plan.transfers:
+                    self.io.write_from_device(arena[off:off + nbytes], file_off,
+                                              self._idle_stream)
+                    keys.append(key)
+            except BaseException as e:  # reported, never lost on the thread
+                err = e
+            done(keys, err)
+
+        self._pending_writes.append(self._writer.submit(job))
+
+    def drain(self, timeout: Optional[float] = None) -> None:
+        """Waits for every write started by flush_async."""
+        pending, self._pending_writes = self._pending_writes, []
+        for f in pending:
+            f.result(timeout=timeout)
+
     def flush(self, plan: StorePlan, arena: torch.Tensor) -> list[str]:
         """Writes each request's records at its file offset; returns the
         chunk keys written (to commit)."""
@@ -382,6 +428,10 @@ class KVDataPlane:
                                      style=self.rope_style, k_scale=self.k_scales)
 
     def close(self) -> None:
+        self.drain()
+        if self._writer is not None:
+            self._writer.shutdown(wait=True)
+            self._writer = None
         if self.io is not None:
             self.io.close()
             self.io = None
@@ -461,6 +511,8 @@ class DaserConnector(KVConnectorBase_V1):
                 save_stream=extra.get("save_stream", "side"),
             )
             self._k_scale_cfg = extra.get("k_scale")  # uniform fp8 K scale, optional
+            self._async_save = bool(extra.get("async_save", False))
+            self._commit_futs: list = []
             cache_cfg = getattr(vllm_config, "cache_config", None)
             self._cache_dtype = str(getattr(cache_cfg, "cache_dtype", "auto"))
             self._meta: Optional[DaserConnectorMeta] = None
@@ -645,21 +697,40 @@ class DaserConnector(KVConnectorBase_V1):
             for name, idx in self._plane.layer_idx.items():
                 if idx not in self._saved_layers:
                     self._plane.save_layer(name, self._store_plan, self._store_arena)
-        self._plane.flush(self._store_plan, self._store_arena)
+        if self._async_save:
+            self._plane.flush_async(self._store_plan, self._store_arena, self._commit_written)
+        else:
+            self._plane.flush(self._store_plan, self._store_arena)
         self._store_plan = None
         self._store_arena = None
         self._flushed = True
-        if self._pending_commits:
+        if self._pending_commits and not self._async_save:
             keys = list(self._pending_commits)
-
-            async def _commit_all() -> None:
-                await asyncio.gather(*(self._ipc_async.commit_chunk(k) for k in keys))
-
-            self._bg.run(_commit_all(), timeout=120.0)
+            self._bg.run(self._commit_keys(keys), timeout=120.0)
         self._pending_commits.clear()
+
+    async def _commit_keys(self, keys: list[str]) -> None:
+        await asyncio.gather(*(self._ipc_async.commit_chunk(k) for k in keys))
+
+    def _commit_written(self, keys: list[str], err: Optional[BaseException]) -> None:
+        """async_save: runs on the writer thread once a step's records are in
+        the file; commits the chunks written (a failed write is logged and
+        its chunk stays uncommitted, so lookups keep missing it)."""
+        if err is not None:
+            logger.error("[CONNECTOR] async save failed after %d chunk(s): %s", len(keys), err)
+        if keys:
+            self._commit_futs.append(
+                asyncio.run_coroutine_threadsafe(self._commit_keys(keys), self._bg.loop))
 
     def shutdown(self) -> None:
         if self._role_kind != KVConnectorRole.WORKER:
             return
+        self._plane.drain(timeout=120.0)  # async_save: the last steps' writes
+        for f in self._commit_futs:
+            try:
+                f.result(timeout=120.0)
+            except Exception as exc:  # noqa: BLE001 - reported, shutdown continues
+                logger.error("[CONNECTOR] commit failed: %s", exc)
+        self._commit_futs = []
         self._plane.close()
         self._bg.stop()

@@ -330,3 +330,31 @@ def test_fp8_load_rerotates_with_module_scales(gpu, tmp_path):
         assert torch.equal(f[:, 0].view(torch.uint8), caches[l][:, 7].view(torch.uint8))
     w.shutdown()
     w2.shutdown()
+
+
+@pytest.mark.parametrize("backend", ["native", "python"])
+def test_async_save_survives_immediate_block_reuse(gpu, tmp_path, backend):
+    """async_save: wait_for_save returns before the file writes; the next
+    step's KV writes to the same blocks (enqueued at once on the current
+    stream) must not reach the records, and the chunks are committed once
+    written (shutdown drains)."""
+    print(f"case: connector async save {backend}", flush=True)
+    w, ipc = _worker(tmp_path, async_save=True, io_backend=backend)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=39)
+    host = [to_bits_np(c, "bf16") for c in caches]
+    named = _named(caches)
+    w.register_kv_caches(named)
+    _save(w, named, _store_reqs())
+    for c in caches:  # the blocks are reused right away
+        c.fill_(3.0)
+    second = {"c": C.ReqStoreSpec("kc", 20, 2, [5, 7], 20 * SHAPE.slot_bytes, 32)}
+    _save(w, named, second)  # a second step queued behind the first
+    w.shutdown()
+    ref = np.zeros(3 * SHAPE.slot_bytes, dtype=np.uint8)
+    oracle.gather(host, [5, 9, 2], np.arange(3) * SHAPE.slot_bytes, ref, SHAPE.layer_bytes)
+    assert np.array_equal(_file_records(tmp_path / "daser.store", 3, 3), ref)
+    filled = [to_bits_np(c, "bf16") for c in caches]
+    ref2 = np.zeros(2 * SHAPE.slot_bytes, dtype=np.uint8)
+    oracle.gather(filled, [5, 7], np.arange(2) * SHAPE.slot_bytes, ref2, SHAPE.layer_bytes)
+    assert np.array_equal(_file_records(tmp_path / "daser.store", 20, 2), ref2)
+    assert sorted(ipc.committed) == ["ka", "kb", "kc"]
