@@ -245,7 +245,8 @@ class KVDataPlane:
         self._io_slot_bytes = io_slot_bytes
         self._io_slots = io_slots
         self.k_scales = k_scales
-        self._writer = None  # background writer of flush_async
+        self._writer = None  # background writer of flush_async, with its own ring
+        self._wio = None
         self._idle_stream: Optional[torch.cuda.Stream] = None
         self._pending_writes: list = []
         self.table = None
@@ -257,7 +258,7 @@ class KVDataPlane:
     # -- registration (reference register_kv_caches :383-429)
     def register(self, kv_caches: dict[str, torch.Tensor], slot_size: int = 0) -> int:
         from daser_amd import ops
-        from daser_amd.store_io import NativeRingIO, PinnedRingIO, preallocate_store
+        from daser_amd.store_io import preallocate_store
 
         self.layer_names = list(kv_caches.keys())
         self.layer_idx = {n: i for i, n in enumerate(self.layer_names)}
@@ -276,19 +277,21 @@ class KVDataPlane:
         preallocate_store(self.store_path, max(self.slot_bytes * 1024, 64 << 20))
         if self.save_stream == "side" and lay.device.type == "cuda" and self._side is None:
             self._side = torch.cuda.Stream(lay.device)  # default priority
+        if self.io_backend == "direct" and self.slot_bytes % 4096:
+            raise ValueError("io_backend='direct' needs a slot record size that is a "
+                             "multiple of 4096 bytes")
         if self.io is None:
-            if self.io_backend == "python":
-                self.io = PinnedRingIO(self.store_path, lay.device,
-                                       slot_bytes=self._io_slot_bytes, n_slots=self._io_slots)
-            else:
-                direct = self.io_backend == "direct"
-                if direct and self.slot_bytes % 4096:
-                    raise ValueError("io_backend='direct' needs a slot record size that is a "
-                                     "multiple of 4096 bytes")
-                self.io = NativeRingIO(self.store_path, lay.device,
-                                       slot_bytes=self._io_slot_bytes, n_slots=self._io_slots,
-                                       direct=direct)
+            self.io = self._open_ring(lay.device)
         return self.slot_bytes
+
+    def _open_ring(self, device: torch.device):
+        from daser_amd.store_io import NativeRingIO, PinnedRingIO
+
+        if self.io_backend == "python":
+            return PinnedRingIO(self.store_path, device, slot_bytes=self._io_slot_bytes,
+                                n_slots=self._io_slots)
+        return NativeRingIO(self.store_path, device, slot_bytes=self._io_slot_bytes,
+                            n_slots=self._io_slots, direct=self.io_backend == "direct")
 
     @property
     def device(self) -> torch.device:
@@ -361,6 +364,8 @@ class KVDataPlane:
         if self._writer is None:
             self._writer = ThreadPoolExecutor(max_workers=1, thread_name_prefix="daser-save")
             self._idle_stream = torch.cuda.Stream(self.device)  # never given work
+            # its own ring: a load (start_load_kv) never waits behind a write
+            self._wio = self._open_ring(self.table.layout.device)
 
         def job() -> None:
             keys: list[str] = []
@@ -368,8 +373,8 @@ class KVDataPlane:
             try:
                 ev.synchronize()  # the gathers into this arena have run
                 for key, off, nbytes, file_off in plan.transfers:
-                    self.io.write_from_device(arena[off:off + nbytes], file_off,
-                                              self._idle_stream)
+                    self._wio.write_from_device(arena[off:off + nbytes], file_off,
+                                                self._idle_stream)
                     keys.append(key)
             except BaseException as e:  # reported, never lost on the thread
                 err = e
@@ -432,6 +437,9 @@ class KVDataPlane:
         if self._writer is not None:
             self._writer.shutdown(wait=True)
             self._writer = None
+        if self._wio is not None:
+            self._wio.close()
+            self._wio = None
         if self.io is not None:
             self.io.close()
             self.io = None
