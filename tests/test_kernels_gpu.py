@@ -686,3 +686,71 @@ def test_hip_graph_capture_and_replay(gpu):
         for i, (a, b) in enumerate(zip(got, want)):
             assert torch.equal(a, b), f"replay {rep}, output {i}"
     assert want[0].any()
+
+
+def _random_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        dt = ["bf16", "fp16", "e4m3"][rng.integers(3)]
+        e = 1 if dt == "e4m3" else 2
+        ve = 16 if e == 1 else 8
+        D = int(rng.choice([64, 80, 96, 128, 192, 256]))
+        H = int(rng.choice([1, 2, 3, 4, 8]))
+        bs = int(rng.choice([1, 4, 8, 16, 32]))
+        style = "gptj" if rng.random() < 0.25 else "neox"
+        R = D if rng.random() < 0.75 else D // 2
+        if (R // 2) % ve or (R % ve if style == "gptj" else 0) or ((D - R) * e) % 16:
+            continue
+        if (bs * H * D * e) % 16:
+            continue
+        cases.append((dt, D, H, bs, style, R, int(rng.integers(1, 6)), int(rng.integers(1 << 30))))
+    return cases
+
+
+@pytest.mark.parametrize("dt,D,H,bs,style,R,L,seed", _random_cases(40, 2024))
+def test_random_geometry_parity(gpu, dt, D, H, bs, style, R, L, seed):
+    """Seeded random geometries (page and row sizes of every kernel class,
+    partial rotary, gptj) through gather, scatter and re-rotation, against
+    the oracle."""
+    print(f"case: random {dt} D{D} H{H} bs{bs} {style} R{R} L{L} seed{seed}", flush=True)
+    shape = KVShape(L, H, D, bs, 1 if dt == "e4m3" else 2)
+    rng = np.random.default_rng(seed)
+    nb = int(rng.integers(8, 40))
+    n = int(rng.integers(1, nb))
+    src = rand_caches(shape, nb, dt, gpu, seed=seed % 1000, scale=40.0 if dt == "e4m3" else 1.0)
+    ids = rng.permutation(nb)[:n].astype(np.int32)
+    offs = rng.permutation(n).astype(np.int64) * shape.slot_bytes
+    st = torch.zeros(n * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(src), ids, offs, st)
+    host = _np_layers(src, dt)
+    ref = np.zeros(n * shape.slot_bytes, dtype=np.uint8)
+    oracle.gather(host, ids, offs, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    assert np.array_equal(st.cpu().numpy(), ref)
+    dst_ids = rng.permutation(nb)[:n].astype(np.int32)
+    deltas = rng.integers(-4000, 32768, size=n) * (rng.random(n) < 0.8)
+    ridx, uniq = position.page_rope_index([1] * n, deltas)
+    tabs = position.delta_tables(uniq or [0], R, 500000.0, device=gpu)
+    ks_np = (rng.random(L).astype(np.float32) * 0.5 + 0.01) if dt == "e4m3" else None
+    ks = torch.from_numpy(ks_np).to(gpu) if ks_np is not None else None
+    dst = [torch.zeros_like(c) for c in src]
+    ops.scatter(ops.LayerTable(dst), dst_ids, offs, st)
+    rot = [torch.zeros_like(c) for c in src]
+    ops.scatter_rerotate(ops.LayerTable(rot), dst_ids, offs, st, tabs, ridx, rot_dim=R,
+                         style=style, k_scale=ks)
+    dref = [np.zeros_like(h) for h in host]
+    oracle.scatter(dref, dst_ids, offs, ref, shape.layer_bytes)
+    rref = [np.zeros_like(h) for h in host]
+    d = np.asarray(deltas, np.int64)
+    oracle.scatter_rerotate(rref, dst_ids, offs, ref, shape.layer_bytes, dtype=ORC_DT[dt],
+                            rot_dim=R, style=0 if style == "neox" else 1,
+                            stored_pos=np.zeros(n, np.int64), new_pos=d, rotate=d != 0,
+                            theta=500000.0, k_scale=ks_np)
+    torch.cuda.synchronize()
+    for l in range(L):
+        assert np.array_equal(to_bits_np(dst[l], dt), dref[l]), f"scatter layer {l}"
+        got = to_bits_np(rot[l], dt)
+        assert np.array_equal(got[1], rref[l][1]), f"V layer {l}"
+        ok, msg = rotation_within_tolerance(got[0], rref[l][0], dt)
+        assert ok, f"K layer {l}: {msg}"
