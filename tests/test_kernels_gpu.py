@@ -754,3 +754,40 @@ def test_random_geometry_parity(gpu, dt, D, H, bs, style, R, L, seed):
         assert np.array_equal(got[1], rref[l][1]), f"V layer {l}"
         ok, msg = rotation_within_tolerance(got[0], rref[l][0], dt)
         assert ok, f"K layer {l}: {msg}"
+
+
+@pytest.mark.parametrize("dt,D,H,bs,style,R,L,seed", _random_cases(20, 77))
+def test_random_geometry_slots_parity(gpu, dt, D, H, bs, style, R, L, seed):
+    """Token-granular gather / scatter on random geometries and random
+    slot mappings (ragged requests, partial pages, padding) vs the oracle."""
+    print(f"case: random slots {dt} D{D} H{H} bs{bs} L{L} seed{seed}", flush=True)
+    shape = KVShape(L, H, D, bs, 1 if dt == "e4m3" else 2)
+    rng = np.random.default_rng(seed)
+    nb = int(rng.integers(16, 64))
+    toks = [int(x) for x in rng.integers(1, 6 * bs, size=int(rng.integers(1, 5)))]
+    pages = [(t + bs - 1) // bs for t in toks]
+    if sum(pages) > nb:
+        pytest.skip("pool too small for this draw")
+    perm = rng.permutation(nb).astype(np.int64)
+    tables, k = [], 0
+    for p in pages:
+        tables.append(perm[k:k + p].tolist())
+        k += p
+    row = H * D * shape.elem_bytes
+    sm = ops.slot_mapping_for(tables, toks, bs)
+    ro = ops.token_row_offsets(toks, shape.slot_bytes, bs, row)
+    sm[rng.random(sm.size) < 0.1] = -1  # padding
+    src = rand_caches(shape, nb, dt, gpu, seed=seed % 997)
+    st = torch.zeros(sum(pages) * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather_slots(ops.LayerTable(src), sm, ro, st)
+    host = _np_layers(src, dt)
+    ref = np.zeros(st.numel(), dtype=np.uint8)
+    oracle.gather_slots(host, sm, ro, ref, shape.layer_bytes)
+    dst = [torch.zeros_like(c) for c in src]
+    ops.scatter_slots(ops.LayerTable(dst), sm, ro, st)
+    dref = [np.zeros_like(h) for h in host]
+    oracle.scatter_slots(dref, sm, ro, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    assert np.array_equal(st.cpu().numpy(), ref)
+    for l in range(L):
+        assert np.array_equal(to_bits_np(dst[l], dt), dref[l]), f"layer {l}"
