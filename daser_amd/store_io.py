@@ -102,6 +102,12 @@ class PinnedRingIO:
     def slot_bytes(self) -> int:
         return self._slot_bytes
 
+    @property
+    def backend(self) -> str:
+        """Threads doing pread/pwrite through pinned slots (counterpart of
+        GDSTransferLayer.backend, gds_transfer.py:37-60)."""
+        return "threads"
+
     def _take_slot(self) -> _Slot:
         """Next ring slot, after its previous host I/O (and so its copy) ended."""
         s = self._slots[self._next]
@@ -312,6 +318,7 @@ class NativeRingIO:
         _lib.check("dsr_ring_open", rc)
         self._h = h
         self._slot_bytes = int(slot_bytes)
+        self._direct = bool(direct)
 
     @property
     def slot_bytes(self) -> int:
@@ -320,6 +327,13 @@ class NativeRingIO:
     @property
     def uses_io_uring(self) -> bool:
         return bool(self._lib.lib().dsr_ring_uses_io_uring(self._handle()))
+
+    @property
+    def backend(self) -> str:
+        """How file I/O is done ("io_uring" or "posix", "+O_DIRECT"); the
+        counterpart of GDSTransferLayer.backend (gds_transfer.py:37-60)."""
+        return ("io_uring" if self.uses_io_uring else "posix") + ("+O_DIRECT" if self._direct
+                                                                  else "")
 
     def _handle(self):
         if self._h is None:
