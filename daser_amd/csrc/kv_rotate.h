@@ -1,0 +1,562 @@
+// kv_rotate.h -- element codecs and the re-rotation kernels (contiguous,
+// row-aligned, pair-task and grouped).
+// Part of libdaser_kv: included by kv_move.hip, one translation unit.
+
+#pragma once
+
+#include "kv_page_kernels.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Element codecs for the rotation. Each 16-byte vector holds VE elements.
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+// Round-to-nearest-even fp32 -> bf16; NaN -> 0x7FC0 with its sign dropped.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float fp16_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+// fp32 -> fp16 by the hardware conversion (round-to-nearest-even);
+// NaN -> 0x7E00.
+__device__ __forceinline__ uint32_t f32_to_fp16(float f) {
+  if (__builtin_isnan(f)) return 0x7e00u;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// OCP e4m3fn (bias 7, no infinities, S.1111.111 = NaN) through the gfx950
+// conversion instructions, which use the OCP formats: v_cvt_pk_f32_fp8
+// decodes two codes, v_cvt_pk_fp8_f32 encodes two floats with
+// round-to-nearest-even (both checked exhaustively against the bit-level
+// definition on MI355X: all 256 codes, 200k values incl. every midpoint).
+// Encoding saturates by clamping to +-448 first (compare-select keeps NaN);
+// the instruction turns NaN into 0xFF, which the clamp range never produces,
+// so 0xFF bytes are rewritten to the canonical 0x7F.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float clamp448(float f) {
+  f = f > 448.0f ? 448.0f : f;
+  return f < -448.0f ? -448.0f : f;
+}
+// 0x80 in every byte of w that equals 0xFF.
+__device__ __forceinline__ uint32_t ff_bytes(uint32_t w) {
+  const uint32_t t = ~w;
+  return ~(((t & 0x7f7f7f7fu) + 0x7f7f7f7fu) | t) & 0x80808080u;
+}
+__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* x) {
+  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  x[0] = lo.x;
+  x[1] = lo.y;
+  x[2] = hi.x;
+  x[3] = hi.y;
+}
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(const float* y) {
+  int e = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(y[0]), clamp448(y[1]), 0, false);
+  e = __builtin_amdgcn_cvt_pk_fp8_f32(clamp448(y[2]), clamp448(y[3]), e, true);
+  const uint32_t w = (uint32_t)e;
+  return w ^ ff_bytes(w);
+}
+
+template <int DT>
+struct Codec;
+
+template <>
+struct Codec<DSR_DTYPE_BF16> {
+  static constexpr int VE = 8;
+  __device__ static void decode(u32x4 v, float* x) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = bf16_to_f32(v[k] & 0xffffu);
+      x[2 * k + 1] = bf16_to_f32(v[k] >> 16);
+    }
+  }
+  __device__ static u32x4 encode(const float* y) {
+    u32x4 v;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      v[k] = f32_to_bf16(y[2 * k]) | (f32_to_bf16(y[2 * k + 1]) << 16);
+    return v;
+  }
+};
+
+template <>
+struct Codec<DSR_DTYPE_FP16> {
+  static constexpr int VE = 8;
+  __device__ static void decode(u32x4 v, float* x) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = fp16_to_f32(v[k] & 0xffffu);
+      x[2 * k + 1] = fp16_to_f32(v[k] >> 16);
+    }
+  }
+  __device__ static u32x4 encode(const float* y) {
+    u32x4 v;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      v[k] = f32_to_fp16(y[2 * k]) | (f32_to_fp16(y[2 * k + 1]) << 16);
+    return v;
+  }
+};
+
+template <>
+struct Codec<DSR_DTYPE_FP8_E4M3> {
+  static constexpr int VE = 16;
+  __device__ static void decode(u32x4 v, float* x) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) e4m3x4_to_f32(v[k], x + 4 * k);
+  }
+  __device__ static u32x4 encode(const float* y) {
+    u32x4 v;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = f32x4_to_e4m3(y + 4 * k);
+    return v;
+  }
+};
+
+struct RotArgs {
+  UnitArgs u;
+  const float2* cos_sin;
+  const int32_t* rope_idx;
+  int32_t n_tables;
+  int32_t row_vecs;    // 16-byte vectors per K row (head_dim * e / 16)
+  int32_t rot_half;    // rot_dim / 2 (pairs per row)
+  int32_t task_vecs;   // rotation tasks per row
+  int32_t tail_vec0;   // first un-rotated vector of a row
+  int32_t tasks_per_row;
+  int32_t rot_vecs;   // 16-byte vectors of a row inside the rotated region
+  int32_t half_vecs;  // neox: vectors from a first-half vector to its partner
+  const float* k_scale;
+};
+
+// Rotates the K page (rows of head_dim elements) from src into dst.
+// neox task c: vector c of the first half and its partner at +rot_half;
+// gptj task c: vector c, whose VE/2 adjacent pairs rotate in place;
+// tail task: one un-rotated 16-byte vector, copied.
+// K-page rotation in rounds of kRotUnroll tasks per lane. Task t covers row
+// t / tasks_per_row, column c = t % tasks_per_row:
+//   neox, c < task_vecs: vector c of the rotated first half and its partner
+//                        at +rot_half elements;
+//   gptj, c < task_vecs: vector c, whose VE/2 adjacent pairs rotate in place;
+//   c >= task_vecs:      one un-rotated 16-byte tail vector, copied.
+template <int DT, int STYLE>
+struct KRound {
+  static constexpr int VE = Codec<DT>::VE;
+  u32x4 a[kRotUnroll], b[kRotUnroll];
+  int off[kRotUnroll];
+  int kind[kRotUnroll];  // 0 = rotate, 1 = copy, -1 = none
+  int c_of[kRotUnroll];
+
+  __device__ __forceinline__ void load(const RotArgs& ra, rsrc_t rs, int base, int ntask,
+                                       int row_bytes, int half_off) {
+#pragma unroll
+    for (int k = 0; k < kRotUnroll; ++k) {
+      const int t = base + k * kThreads;
+      kind[k] = -1;
+      off[k] = 0;
+      c_of[k] = 0;
+      a[k] = u32x4{0u, 0u, 0u, 0u};
+      b[k] = a[k];
+      if (t < ntask) {
+        const int row = t / ra.tasks_per_row;
+        const int c = t - row * ra.tasks_per_row;
+        c_of[k] = c;
+        if (c < ra.task_vecs) {
+          kind[k] = 0;
+          off[k] = row * row_bytes + (c << 4);
+          a[k] = bload(rs, off[k]);
+          if (STYLE == DSR_ROPE_NEOX) b[k] = bload(rs, off[k] + half_off);
+        } else {
+          kind[k] = 1;
+          off[k] = row * row_bytes + ((ra.tail_vec0 + c - ra.task_vecs) << 4);
+          a[k] = bload(rs, off[k]);
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(rsrc_t rd, const float2* tab, int half_off,
+                                        float scale, float inv_scale) {
+    using C = Codec<DT>;
+    constexpr bool kScaled = DT == DSR_DTYPE_FP8_E4M3;
+#pragma unroll
+    for (int k = 0; k < kRotUnroll; ++k) {
+      if (kind[k] == 1) {
+        bstore(rd, off[k], a[k]);
+      } else if (kind[k] == 0) {
+        float x[VE];
+        C::decode(a[k], x);
+        if (STYLE == DSR_ROPE_NEOX) {
+          float z[VE];
+          C::decode(b[k], z);
+          const int j0 = c_of[k] * VE;
+#pragma unroll
+          for (int e = 0; e < VE; ++e) {
+            const float2 cs = tab[j0 + e];
+            const float x1 = kScaled ? x[e] * scale : x[e];
+            const float x2 = kScaled ? z[e] * scale : z[e];
+            const float y1 = x1 * cs.x - x2 * cs.y;
+            const float y2 = x2 * cs.x + x1 * cs.y;
+            x[e] = kScaled ? y1 * inv_scale : y1;
+            z[e] = kScaled ? y2 * inv_scale : y2;
+          }
+          bstore(rd, off[k], C::encode(x));
+          bstore(rd, off[k] + half_off, C::encode(z));
+        } else {
+          const int j0 = c_of[k] * (VE / 2);
+#pragma unroll
+          for (int e = 0; e < VE / 2; ++e) {
+            const float2 cs = tab[j0 + e];
+            const float x1 = kScaled ? x[2 * e] * scale : x[2 * e];
+            const float x2 = kScaled ? x[2 * e + 1] * scale : x[2 * e + 1];
+            const float y1 = x1 * cs.x - x2 * cs.y;
+            const float y2 = x2 * cs.x + x1 * cs.y;
+            x[2 * e] = kScaled ? y1 * inv_scale : y1;
+            x[2 * e + 1] = kScaled ? y2 * inv_scale : y2;
+          }
+          bstore(rd, off[k], C::encode(x));
+        }
+      }
+    }
+  }
+};
+
+// One page_bytes run copied in rounds of U vectors per lane.
+template <int U>
+struct VRound {
+  u32x4 r[U];
+  __device__ __forceinline__ void load(rsrc_t rs, int base, int nvec) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * kThreads;
+      r[k] = i < nvec ? bload(rs, i << 4) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __device__ __forceinline__ void store(rsrc_t rd, int base, int nvec) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * kThreads;
+      if (i < nvec) bstore(rd, i << 4, r[k]);
+    }
+  }
+};
+
+// One workgroup per (page, layer) unit in page-list order. V, and K of pages
+// without a table (rope_idx < 0), are copied bit-exactly; K of the others is
+// re-rotated row by row with the page's (cos, sin) table staged in LDS. The
+// first round of V and K loads is issued before the table is fetched and the
+// workgroup synchronises, so the table latency overlaps the page reads.
+template <int DT, int STYLE>
+__global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs ra) {
+  __shared__ float2 tab[kMaxRotHalf];
+  uint8_t *cache, *rec;
+  int l;
+  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
+  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  const int64_t p = u / ra.u.n_layers;
+  const int ti = ra.rope_idx[p];
+  const int64_t pb = ra.u.page_bytes;
+  if (ti < 0 || ti >= ra.n_tables) {
+    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    return;
+  }
+  const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
+  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const int nvec = (int)(pb >> 4);
+  const int row_bytes = ra.row_vecs << 4;
+  const int ntask = (int)(pb / row_bytes) * ra.tasks_per_row;
+  const int half_off = ra.rot_half * 16 / Codec<DT>::VE;
+
+  VRound<kScatterUnroll> v;
+  KRound<DT, STYLE> k;
+  v.load(vs, threadIdx.x, nvec);
+  k.load(ra, ks, threadIdx.x, ntask, row_bytes, half_off);
+
+  const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
+  for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
+  float scale = 1.0f, inv_scale = 1.0f;
+  if (DT == DSR_DTYPE_FP8_E4M3) {
+    scale = ra.k_scale[ra.u.layer0 + l];
+    inv_scale = 1.0f / scale;
+  }
+  __syncthreads();
+
+  v.store(vd, threadIdx.x, nvec);
+  k.store(kd, tab, half_off, scale, inv_scale);
+  for (int base = threadIdx.x + kThreads * kScatterUnroll; base < nvec;
+       base += kThreads * kScatterUnroll) {
+    v.load(vs, base, nvec);
+    v.store(vd, base, nvec);
+  }
+  for (int base = threadIdx.x + kThreads * kRotUnroll; base < ntask;
+       base += kThreads * kRotUnroll) {
+    k.load(ra, ks, base, ntask, row_bytes, half_off);
+    k.store(kd, tab, half_off, scale, inv_scale);
+  }
+}
+
+// One K vector after rotation: c is its vector column in the row, own its
+// bytes, partner (neox) the bytes of the vector half a rotation away.
+// Vectors past the rotated region are returned unchanged.
+template <int DT, int STYLE>
+__device__ __forceinline__ u32x4 rotate_vec(const RotArgs& ra, u32x4 own, u32x4 partner, int c,
+                                            const float2* tab, float scale, float inv_scale) {
+  using C = Codec<DT>;
+  constexpr int VE = C::VE;
+  constexpr bool kScaled = DT == DSR_DTYPE_FP8_E4M3;
+  if (c >= ra.rot_vecs) return own;
+  float x[VE];
+  C::decode(own, x);
+  if (STYLE == DSR_ROPE_NEOX) {
+    float z[VE];
+    C::decode(partner, z);
+    const bool first = c < ra.half_vecs;
+    const int j0 = (first ? c : c - ra.half_vecs) * VE;
+    const float sg = first ? -1.0f : 1.0f;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+      const float2 cs = tab[j0 + e];
+      const float xo = kScaled ? x[e] * scale : x[e];
+      const float xp = kScaled ? z[e] * scale : z[e];
+      // first half: x c - p s; second half: x c + p s
+      const float y = xo * cs.x + sg * (xp * cs.y);
+      x[e] = kScaled ? y * inv_scale : y;
+    }
+  } else {
+    const int j0 = c * (VE / 2);
+#pragma unroll
+    for (int e = 0; e < VE / 2; ++e) {
+      const float2 cs = tab[j0 + e];
+      const float x1 = kScaled ? x[2 * e] * scale : x[2 * e];
+      const float x2 = kScaled ? x[2 * e + 1] * scale : x[2 * e + 1];
+      const float y1 = x1 * cs.x - x2 * cs.y;
+      const float y2 = x2 * cs.x + x1 * cs.y;
+      x[2 * e] = kScaled ? y1 * inv_scale : y1;
+      x[2 * e + 1] = kScaled ? y2 * inv_scale : y2;
+    }
+  }
+  return C::encode(x);
+}
+
+// Contiguous variant: lane-consecutive 16-byte vectors over the whole K page
+// (every load instruction of a wave covers 1 KiB of contiguous page), with
+// the neox partner vector fetched from lane ^ half_vecs by a cross-lane
+// shuffle. Valid when half_vecs is a power of two <= 32 dividing the row
+// evenly (rows then start on 2*half_vecs lane boundaries), and always for
+// gptj, whose pairs sit inside one vector.
+template <int DT, int STYLE, int U>
+__device__ __forceinline__ void rotate_contig_round(const RotArgs& ra, VRound<U>& kk,
+                                                    int base, int nvec, rsrc_t kd,
+                                                    const float2* tab, float scale,
+                                                    float inv_scale) {
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const int i = base + k * kThreads;
+    u32x4 q = kk.r[k];
+    if (STYLE == DSR_ROPE_NEOX) {  // whole wave takes part in the shuffle
+#pragma unroll
+      for (int w = 0; w < 4; ++w) q[w] = (unsigned)__shfl_xor((int)kk.r[k][w], ra.half_vecs);
+    }
+    if (i >= nvec) continue;
+    bstore(kd, i << 4, rotate_vec<DT, STYLE>(ra, kk.r[k], q, i % ra.row_vecs, tab, scale,
+                                             inv_scale));
+  }
+}
+
+// K and V vectors per lane per round: one round covers a 32 KiB bf16 or a
+// 16 KiB e4m3 Llama page.
+template <int DT>
+constexpr int rot_contig_unroll() {
+  return DT == DSR_DTYPE_FP8_E4M3 ? 4 : 8;
+}
+
+template <int DT, int STYLE>
+__global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(RotArgs ra) {
+  __shared__ float2 tab[kMaxRotHalf];
+  uint8_t *cache, *rec;
+  int l;
+  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
+  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  const int64_t p = u / ra.u.n_layers;
+  const int ti = ra.rope_idx[p];
+  const int64_t pb = ra.u.page_bytes;
+  if (ti < 0 || ti >= ra.n_tables) {
+    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    return;
+  }
+  constexpr int U = rot_contig_unroll<DT>();
+  const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
+  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const int nvec = (int)(pb >> 4);
+  VRound<U> v, kk;
+  v.load(vs, threadIdx.x, nvec);
+  kk.load(ks, threadIdx.x, nvec);
+  const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
+  for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
+  float scale = 1.0f, inv_scale = 1.0f;
+  if (DT == DSR_DTYPE_FP8_E4M3) {
+    scale = ra.k_scale[ra.u.layer0 + l];
+    inv_scale = 1.0f / scale;
+  }
+  __syncthreads();
+  const int rounds = (nvec + kThreads * U - 1) / (kThreads * U);
+  for (int r = 0; r < rounds; ++r) {  // uniform trip count: shuffles stay converged
+    const int base = r * kThreads * U + threadIdx.x;
+    if (r > 0) {
+      v.load(vs, base, nvec);
+      kk.load(ks, base, nvec);
+    }
+    v.store(vd, base, nvec);
+    rotate_contig_round<DT, STYLE, U>(ra, kk, base, nvec, kd, tab, scale, inv_scale);
+  }
+}
+
+// neox rows whose partner distance is not a power of two (head_dim 80, 96,
+// 192, ...): each wave takes rpw = 64 / row_vecs whole rows (lanes past
+// rpw * row_vecs idle), so a vector's partner half a rotation away lies in
+// the same wave and comes from lane +- half_vecs by an arbitrary-lane
+// shuffle. Idle lanes and rows past the page get an offset beyond the
+// descriptor: their loads read 0 and their stores are dropped. One unit per
+// workgroup, layer-major; V is copied in flat rounds alongside. Replaced the
+// pair-task kernel for these shapes (3.5-4.2 TB/s, 35-45% behind a plain
+// scatter of the same pages).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_rows_kernel(RotArgs ra) {
+  constexpr int U = rot_contig_unroll<DT>();
+  __shared__ float2 tab[kMaxRotHalf];
+  uint8_t *cache, *rec;
+  int l;
+  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
+  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  const int64_t p = u / ra.u.n_layers;
+  const int ti = ra.rope_idx[p];
+  const int64_t pb = ra.u.page_bytes;
+  if (ti < 0 || ti >= ra.n_tables) {
+    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    return;
+  }
+  const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
+  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const int nvec = (int)(pb >> 4);
+  const int rv = ra.row_vecs;
+  const int rpw = kWave / rv;
+  const int rows = nvec / rv;
+  const int slots = (rows + rpw - 1) / rpw;  // wave-sized groups of rows
+  const int lane = (int)threadIdx.x % kWave;
+  const int wave = (int)threadIdx.x / kWave;
+  const int r_in = lane / rv;
+  const int c = lane - r_in * rv;
+  const int h = ra.half_vecs;
+  const int partner = c < h ? lane + h : c < 2 * h ? lane - h : lane;
+  const int waves = kThreads / kWave;
+  const int rounds_k = (slots + waves * U - 1) / (waves * U);
+  const int rounds_v = (nvec + kThreads * U - 1) / (kThreads * U);
+  const int rounds = rounds_k > rounds_v ? rounds_k : rounds_v;
+  auto k_off = [&](int r, int k) {
+    const int row = ((r * U + k) * waves + wave) * rpw + r_in;
+    return r_in < rpw && row < rows ? (row * rv + c) << 4 : (int)pb;
+  };
+  VRound<U> v;
+  u32x4 x[U];
+  v.load(vs, threadIdx.x, nvec);
+#pragma unroll
+  for (int k = 0; k < U; ++k) x[k] = bload(ks, k_off(0, k));
+  const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
+  for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
+  float scale = 1.0f, inv_scale = 1.0f;
+  if (DT == DSR_DTYPE_FP8_E4M3) {
+    scale = ra.k_scale[ra.u.layer0 + l];
+    inv_scale = 1.0f / scale;
+  }
+  __syncthreads();
+  for (int r = 0; r < rounds; ++r) {  // uniform trip count: shuffles stay converged
+    const int base = r * kThreads * U + threadIdx.x;
+    if (r > 0) {
+      v.load(vs, base, nvec);
+#pragma unroll
+      for (int k = 0; k < U; ++k) x[k] = bload(ks, k_off(r, k));
+    }
+    v.store(vd, base, nvec);
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      u32x4 q;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) q[w] = (unsigned)__shfl((int)x[k][w], partner);
+      bstore(kd, k_off(r, k),
+             rotate_vec<DT, DSR_ROPE_NEOX>(ra, x[k], q, c, tab, scale, inv_scale));
+    }
+  }
+}
+
+// Re-rotation over G units per workgroup (layer-major order, as the one-unit
+// kernel). The group's (cos, sin) tables are staged in LDS, one rot_half
+// stretch per unit; G * rot_half <= kMaxRotHalf. K of an un-rotated unit is
+// stored as loaded.
+template <int DT, int STYLE>
+__global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(RotArgs ra,
+                                                                               int G) {
+  constexpr int U = rot_contig_unroll<DT>();
+  __shared__ float2 tab[kMaxRotHalf];
+  const UnitArgs& a = ra.u;
+  const int64_t g = xcd_unit((a.n_units + G - 1) / G);
+  if (g < 0) return;
+  const int64_t n_pages = a.n_units / a.n_layers;
+  const int nvec = (int)(a.page_bytes >> 4);
+  int64_t p0;
+  int l0;
+  const int64_t n_here = group_start<false>(a, g, G, n_pages, &p0, &l0);
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const int lane = (int)threadIdx.x % kWave;
+  rsrc_t kd[U], vd[U];
+  u32x4 rk[U], rv[U];
+  int tj[U];    // LDS table slot of the vector's unit (-1: copy)
+  float sc[U];  // its layer's K scale (e4m3)
+  int off[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const int fw = k * kThreads + wave * kWave;
+    const int j = fw / nvec;
+    off[k] = (fw - j * nvec + lane) << 4;
+    const UnitRsrc u = unit_rsrc<false>(a, n_pages, p0, l0, j, n_here);
+    rk[k] = bload(make_rsrc(u.rec, u.n), off[k]);
+    rv[k] = bload(make_rsrc(u.rec + a.page_bytes, u.n), off[k]);
+    kd[k] = make_rsrc(u.cache, u.n);
+    vd[k] = make_rsrc(u.cache + a.kv_stride, u.n);
+    const int ti = u.n ? ra.rope_idx[u.p] : -1;
+    tj[k] = ti >= 0 && ti < ra.n_tables ? j : -1;
+    sc[k] = DT == DSR_DTYPE_FP8_E4M3 && u.n ? ra.k_scale[a.layer0 + u.l] : 1.0f;
+  }
+  // tables of the group's units, fetched while the page loads are in flight
+  for (int e = threadIdx.x; e < (int)n_here * ra.rot_half; e += kThreads) {
+    const int jj = e / ra.rot_half;
+    const int64_t p = (p0 + jj) % n_pages;
+    const int ti = ra.rope_idx[p];
+    if (ti >= 0 && ti < ra.n_tables)
+      tab[e] = ra.cos_sin[(int64_t)ti * ra.rot_half + (e - jj * ra.rot_half)];
+  }
+#pragma unroll
+  for (int k = 0; k < U; ++k) bstore(vd[k], off[k], rv[k]);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    u32x4 q = rk[k];
+    if (STYLE == DSR_ROPE_NEOX) {
+#pragma unroll
+      for (int x = 0; x < 4; ++x) q[x] = (unsigned)__shfl_xor((int)rk[k][x], ra.half_vecs);
+    }
+    const int t = tj[k] < 0 ? 0 : tj[k];
+    const u32x4 r = rotate_vec<DT, STYLE>(ra, rk[k], q, (off[k] >> 4) % ra.row_vecs,
+                                          tab + t * ra.rot_half, sc[k], 1.0f / sc[k]);
+    bstore(kd[k], off[k], tj[k] < 0 ? rk[k] : r);
+  }
+}
+
+}  // namespace
