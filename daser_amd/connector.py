@@ -23,7 +23,8 @@ Extra ``kv_connector_extra_config`` keys: ``rope_theta`` (default 10000),
 ``rope_style`` ("neox" | "gptj"), ``rotary_dim`` (default head_dim),
 ``rope_scaling`` (the model's HF ``rope_scaling`` dict: linear, llama3, yarn),
 ``save_mode`` ("per_layer" | "deferred": one all-layer gather in
-wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry),
+wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry), ``io_readers``
+(rings reading a load in parallel, default 4),
 ``io_backend`` ("native": the C++ io_uring ring of libdaser_kv, default;
 "direct": the same ring with the store file opened O_DIRECT;
 "python": the threaded ring of store_io.PinnedRingIO), ``k_scale`` (one K
@@ -217,7 +218,7 @@ class KVDataPlane:
                  save_mode: str = "per_layer",
                  io_slot_bytes: int = 4 << 20, io_slots: int = 8,
                  io_backend: str = "native", save_stream: str = "side",
-                 k_scales: Optional[torch.Tensor] = None) -> None:
+                 k_scales: Optional[torch.Tensor] = None, io_readers: int = 4) -> None:
         if save_mode not in ("per_layer", "deferred"):
             raise ValueError("save_mode must be 'per_layer' or 'deferred'")
         if io_backend not in ("native", "direct", "python"):
@@ -247,6 +248,9 @@ class KVDataPlane:
         self.k_scales = k_scales
         self._writer = None  # background writer of flush_async, with its own ring
         self._wio = None
+        self._io_readers = max(1, int(io_readers))  # parallel rings of load()
+        self._reader_pool = None
+        self._readers: list = []
         self._idle_stream: Optional[torch.cuda.Stream] = None
         self._pending_writes: list = []
         self.table = None
@@ -402,8 +406,8 @@ class KVDataPlane:
     def load(self, plan: LoadPlan, batch_bytes: int = 256 << 20) -> None:
         """Reads the plan's records and scatters them. Reads are grouped into
         batches of about ``batch_bytes``; each batch is scattered as soon as
-        it has landed, so the GPU scatters batch i while the ring reads
-        batch i+1."""
+        it has landed, so the GPU scatters batch i while the reader rings
+        read batch i+1."""
         from daser_amd import ops, position
 
         if plan.page_ids.size == 0:
@@ -416,11 +420,14 @@ class KVDataPlane:
         page_read = plan.page_read if plan.page_read.size else np.zeros(plan.page_ids.size,
                                                                          np.int64)
         first, acc = 0, 0
+        batch: list[tuple[int, int, int]] = []
         for r, (off, nbytes, file_off) in enumerate(plan.reads):
-            self.io.read_into_device(arena[off:off + nbytes], file_off)
+            batch.append((off, nbytes, file_off))
             acc += nbytes
             if acc < batch_bytes and r + 1 < len(plan.reads):
                 continue
+            self._read_batch(arena, batch)
+            batch = []
             sel = np.nonzero((page_read >= first) & (page_read <= r))[0]
             first, acc = r + 1, 0
             if sel.size == 0:
@@ -432,8 +439,43 @@ class KVDataPlane:
                                      arena, tabs, plan.rope_idx[sel], rot_dim=self.rotary_dim,
                                      style=self.rope_style, k_scale=self.k_scales)
 
+    def _read_batch(self, arena: torch.Tensor, reads: list[tuple[int, int, int]]) -> None:
+        """Reads (arena_off, nbytes, file_off) ranges into the arena with the
+        reader rings in parallel (page-cache reads measured 15-18 GB/s on
+        one ring, 32-37 GB/s on four), in pieces of at most 16 MiB. On
+        return the current stream is ordered after every copy."""
+        piece = 16 << 20  # a multiple of 4 KiB: O_DIRECT reads stay aligned
+        parts = [(o + k, min(piece, n - k), f + k) for o, n, f in reads
+                 for k in range(0, n, piece)]
+        consumer = torch.cuda.current_stream(self.device) if self.device.type == "cuda" else None
+        if self._io_readers <= 1 or len(parts) == 1:
+            for o, n, f in parts:
+                self.io.read_into_device(arena[o:o + n], f, consumer)
+            return
+        if self._reader_pool is None:
+            from concurrent.futures import ThreadPoolExecutor
+
+            self._readers = [self.io] + [self._open_ring(self.device)
+                                         for _ in range(self._io_readers - 1)]
+            self._reader_pool = ThreadPoolExecutor(max_workers=self._io_readers,
+                                                   thread_name_prefix="daser-load")
+
+        def run(i: int) -> None:
+            ring = self._readers[i]
+            for o, n, f in parts[i::len(self._readers)]:
+                ring.read_into_device(arena[o:o + n], f, consumer)
+
+        for fut in [self._reader_pool.submit(run, i) for i in range(len(self._readers))]:
+            fut.result()
+
     def close(self) -> None:
         self.drain()
+        if self._reader_pool is not None:
+            self._reader_pool.shutdown(wait=True)
+            self._reader_pool = None
+            for ring in self._readers[1:]:
+                ring.close()
+            self._readers = []
         if self._writer is not None:
             self._writer.shutdown(wait=True)
             self._writer = None
@@ -515,6 +557,7 @@ class DaserConnector(KVConnectorBase_V1):
                 save_mode=extra.get("save_mode", "per_layer"),
                 io_slot_bytes=int(float(extra.get("io_slot_mb", 4)) * (1 << 20)),
                 io_slots=int(extra.get("io_slots", 8)),
+                io_readers=int(extra.get("io_readers", 4)),
                 io_backend=extra.get("io_backend", "native"),
                 save_stream=extra.get("save_stream", "side"),
             )

@@ -217,8 +217,9 @@ def test_missing_layer_saves_are_completed(gpu, tmp_path):
 
 
 def test_batched_load_matches_single_batch(gpu, tmp_path):
-    """Scattering per batch while later batches are read gives the same
-    caches as one scatter after all reads."""
+    """Scattering per batch while later batches are read, with one reader
+    ring or several in parallel, gives the same caches as one scatter after
+    all reads."""
     print("case: batched load", flush=True)
     w, _ = _worker(tmp_path, rope_theta=500000.0)
     caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=35)
@@ -231,16 +232,18 @@ def test_batched_load_matches_single_batch(gpu, tmp_path):
         "y": C.ReqLoadSpec("kb", 10, 1, [0], 10 * slot, 16),
     }
     outs = []
-    for batch in (1, 1 << 30):
+    for batch, readers in ((1, 1), (1 << 30, 1), (1, 4), (1 << 30, 3)):
         fresh = [torch.zeros_like(c) for c in caches]
-        p = C.KVDataPlane(str(tmp_path / "daser.store"), rope_theta=500000.0)
+        p = C.KVDataPlane(str(tmp_path / "daser.store"), rope_theta=500000.0,
+                          io_readers=readers, io_slot_bytes=4096, io_slots=2)
         p.register(_named(fresh))
         p.load(C.plan_load(reqs, slot), batch_bytes=batch)
         torch.cuda.synchronize()
         outs.append(fresh)
         p.close()
-    for a, b in zip(*outs):
-        assert torch.equal(a, b)
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            assert torch.equal(a, b)
     assert torch.equal(outs[0][0][:, 0], caches[0][:, 7])
     w.shutdown()
 
