@@ -46,6 +46,18 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 
 #define DSR_ABI_VERSION 1
 
+/*
+ * Kernel choice and launch shape follow from the geometry; these environment
+ * variables, read at every call, override them for measurements and tests
+ * only (results are the same bytes; leave them unset in production):
+ *   DSR_UNITS_PER_GROUP=n        cap the (page, layer) units per workgroup
+ *                                of the small-page kernels (1: off)
+ *   DSR_MAX_WG_PER_LAUNCH=n      split calls into launches of <= n workgroups
+ *   DSR_ROT_KERNEL=contig|grouped|pairs   re-rotation kernel where several apply
+ *   DSR_ROT_WG_PER_CU=n, DSR_ROT_GROUPED_WG_PER_CU=n   re-rotation occupancy
+ *   DSR_SLOTS_TPW=4|8|16         tokens per wave of the small-row token kernels
+ */
+
 #define DSR_OK 0
 #define DSR_ERR_ARG (-1)   /* null pointer, negative count, bad enum     */
 #define DSR_ERR_ALIGN (-2) /* a pointer/stride/size is not 16-byte aligned */
