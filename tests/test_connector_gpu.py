@@ -361,3 +361,122 @@ def test_async_save_survives_immediate_block_reuse(gpu, tmp_path, backend):
     oracle.gather(filled, [5, 7], np.arange(2) * SHAPE.slot_bytes, ref2, SHAPE.layer_bytes)
     assert np.array_equal(_file_records(tmp_path / "daser.store", 20, 2), ref2)
     assert sorted(ipc.committed) == ["ka", "kb", "kc"]
+
+
+class _FakeServer:
+    """In-process stand-in of the DaseR server's chunk index: match_and_alloc
+    (scheduler, sync) and commit_chunk (worker, async) over shared state, with
+    the reply shapes the reference's IPC server uses."""
+
+    def __init__(self, slot_bytes, block_tokens=16, new_pos=None):
+        self.slot, self.bs, self.new_pos = slot_bytes, block_tokens, new_pos
+        self.next_slot, self.pending, self.committed = 1, {}, {}
+
+    def match_and_alloc(self, prefix, store_key, model_id):
+        if store_key in self.committed:
+            meta = dict(self.committed[store_key])
+            if self.new_pos is not None:
+                meta["new_pos"] = self.new_pos
+            return {"chunks": [meta], "alloc": None}
+        n = len(prefix) // self.bs
+        meta = {"chunk_key": store_key, "start_slot": self.next_slot, "num_slots": n,
+                "file_offset": self.next_slot * self.slot, "token_count": n * self.bs,
+                "pos_offset": 0}
+        self.next_slot += n
+        self.pending[store_key] = meta
+        return {"chunks": [], "alloc": meta}
+
+    async def commit_chunk(self, key):
+        self.committed[key] = self.pending.pop(key)
+        return {"ok": True}
+
+
+def test_cold_then_warm_request_end_to_end(gpu, tmp_path):
+    """The reference's integration check (tests/integration/test_vllm_e2e.py:
+    177-181, cold == warm) at the connector level: a cold request is missed,
+    allocated and saved by the worker; the same prompt later hits and its
+    KV is loaded into other blocks bit-exactly; placed at a new position it
+    is re-rotated."""
+    print("case: connector cold/warm end to end", flush=True)
+    server = _FakeServer(SHAPE.slot_bytes)
+    extra = dict(store_path=str(tmp_path / "daser.store"), io_slot_mb=0.03125, io_slots=3,
+                 rope_theta=500000.0, block_tokens=16)
+    cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(kv_connector_extra_config=extra))
+    sched = C.DaserConnector(cfg, C.KVConnectorRole.SCHEDULER, ipc_client=server)
+    worker = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=server)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=41)
+    named = _named(caches)
+    worker.register_kv_caches(named)
+    prompt = SimpleNamespace(request_id="cold", prompt_token_ids=list(range(1000, 1050)))
+
+    def step(conn, req, blocks, hit, fc=None, save_named=None):
+        conn_blocks = SimpleNamespace(blocks=[[SimpleNamespace(block_id=b) for b in blocks]])
+        sched.update_state_after_alloc(req, conn_blocks, hit)
+        meta = sched.build_connector_meta(
+            SimpleNamespace(num_scheduled_tokens={req.request_id: len(req.prompt_token_ids)}))
+        conn.bind_connector_metadata(meta)
+        conn.start_load_kv(fc)
+        for name, t in (save_named or {}).items():
+            conn.save_kv_layer(name, t, None)
+        conn.wait_for_save()
+        conn.clear_connector_metadata()
+        return meta
+
+    assert sched.get_num_new_matched_tokens(prompt, 0) == (0, False)  # cold: miss
+    meta = step(worker, prompt, [5, 9, 2, 11], 0, save_named=named)
+    assert list(meta.reqs_to_store) == ["cold"] and not meta.reqs_to_load
+    assert len(server.committed) == 1
+
+    warm = SimpleNamespace(request_id="warm", prompt_token_ids=list(prompt.prompt_token_ids))
+    assert sched.get_num_new_matched_tokens(warm, 0) == (48, False)  # 3 whole blocks
+    fresh = [torch.zeros_like(c) for c in caches]
+    w2 = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=server)
+    w2.register_kv_caches(_named(fresh))
+    meta = step(w2, warm, [1, 12, 4, 7], 48)
+    assert list(meta.reqs_to_load) == ["warm"]
+    torch.cuda.synchronize()
+    for l in range(SHAPE.num_layers):
+        assert torch.equal(fresh[l][:, [1, 12, 4]], caches[l][:, [5, 9, 2]]), f"layer {l}"
+        assert not fresh[l][:, 7].view(torch.int16).any()  # the uncached tail block
+
+    # the same chunk placed at position 700: K re-rotated by +700, V as stored
+    server.new_pos = 700
+    moved = SimpleNamespace(request_id="moved", prompt_token_ids=list(prompt.prompt_token_ids))
+    assert sched.get_num_new_matched_tokens(moved, 0) == (48, False)
+    rot = [torch.zeros_like(c) for c in caches]
+    w3 = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=server)
+    w3.register_kv_caches(_named(rot))
+    step(w3, moved, [3, 6, 8, 0], 48)
+    torch.cuda.synchronize()
+    recs = _file_records(tmp_path / "daser.store", 1, 3).copy()
+    ref = [np.zeros_like(to_bits_np(c, "bf16")) for c in caches]
+    oracle.scatter_rerotate(ref, [3, 6, 8], np.arange(3) * SHAPE.slot_bytes, recs,
+                            SHAPE.layer_bytes, dtype=oracle.BF16, rot_dim=64, style=oracle.NEOX,
+                            stored_pos=np.zeros(3, np.int64), new_pos=np.full(3, 700),
+                            rotate=np.ones(3), theta=500000.0)
+    for l in range(SHAPE.num_layers):
+        got = to_bits_np(rot[l], "bf16")
+        assert torch.equal(rot[l][1][[3, 6, 8]], caches[l][1][[5, 9, 2]])
+        ok, msg = oracle.rotation_within_tolerance(got[0][[3, 6, 8]], ref[l][0][[3, 6, 8]],
+                                                   oracle.BF16)
+        assert ok, f"layer {l}: {msg}"
+    for w in (worker, w2, w3):
+        w.shutdown()
+
+
+def test_uncommitted_chunk_is_never_loaded(gpu, tmp_path):
+    """With async_save the chunk is committed only after its records are in
+    the file, so a lookup before that misses."""
+    print("case: connector commit after write", flush=True)
+    server = _FakeServer(SHAPE.slot_bytes)
+    extra = dict(store_path=str(tmp_path / "daser.store"), io_slot_mb=0.03125, io_slots=3,
+                 async_save=True)
+    cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(kv_connector_extra_config=extra))
+    sched = C.DaserConnector(cfg, C.KVConnectorRole.SCHEDULER, ipc_client=server)
+    w = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=server)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=42)
+    w.register_kv_caches(_named(caches))
+    req = SimpleNamespace(request_id="r", prompt_token_ids=list(range(32)))
+    assert sched.get_num_new_matched_tokens(req, 0) == (0, False)
+    assert server.pending and not server.committed  # allocated, not visible
+    w.shutdown()
