@@ -254,6 +254,26 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
         torch.cuda.synchronize()
         extra = {"gather_ms": tg.mean_ms(),
                  "gather_GBps": 2 * P / (tg.mean_ms() * 1e-3) / 1e9}
+        if shape.num_heads * shape.head_dim * shape.elem_bytes <= 512:
+            # small rows: the token-form kernels over the same pages, all
+            # tokens valid (slot = block * bs + t, record row t)
+            bs = shape.block_size
+            row = shape.num_heads * shape.head_dim * shape.elem_bytes
+            t = torch.arange(wl.n_pages * bs, device=dev)
+            sm = ids.to(torch.int64).repeat_interleave(bs) * bs + t % bs
+            ro = roffs.repeat_interleave(bs) + (t % bs) * row
+            tsg, tss = Timer(torch), Timer(torch)
+            for _ in range(warmup):
+                ops.gather_slots(table, sm, ro, recs)
+            for _ in range(steps):
+                with tsg:
+                    ops.gather_slots(table, sm, ro, recs)
+            for _ in range(steps):
+                with tss:
+                    ops.scatter_slots(table, sm, ro, recs)
+            torch.cuda.synchronize()
+            extra.update({"slots_gather_GBps": 2 * P / (tsg.mean_ms() * 1e-3) / 1e9,
+                          "slots_scatter_GBps": 2 * P / (tss.mean_ms() * 1e-3) / 1e9})
         src = recs
     del full, caches, table, src
     torch.cuda.empty_cache()
@@ -565,6 +585,9 @@ def main() -> int:
                 "same_pages_plain_scatter_GBps": round(r["plain_scatter_GBps"], 1),
                 **({"same_pages_gather_GBps": round(r["gather_GBps"], 1)}
                    if "gather_GBps" in r else {}),
+                **({"same_pages_slots_gather_GBps": round(r["slots_gather_GBps"], 1),
+                    "same_pages_slots_scatter_GBps": round(r["slots_scatter_GBps"], 1)}
+                   if "slots_gather_GBps" in r else {}),
                 "kernel": ROT_KERNEL[c],
                 "traffic": pmc_traffic(ROT_KERNEL[c], c, r["pages"]),
                 "algorithmic_bytes": 2 * r["payload_bytes"]}
