@@ -152,7 +152,8 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
  *   head_dim, rot_dim   rot_dim even, <= head_dim, page_bytes a multiple of
  *                       one row; see DSR_ERR_SHAPE for vector constraints
  *   k_scale   [device] per-layer fp32 scales, indexed layer0 + l; required
- *             for fp8, ignored otherwise (may be null)
+ *             for fp8, ignored otherwise (may be null). There is no V scale:
+ *             V is copied as raw bytes, never decoded.
  */
 int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          int64_t kv_stride, int64_t page_stride,
