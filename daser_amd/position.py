@@ -137,14 +137,18 @@ def yarn_inv_freq(rot_dim: int, theta: float, factor: float, original_max_positi
 
 def inv_freq_for(rope_scaling: Optional[dict], rot_dim: int, theta: float) -> np.ndarray:
     """inv_freq of a model's RoPE from its HF-style ``rope_scaling`` entry
-    (None / "default", "linear", "llama3", "yarn"). Scalings whose
+    (None / "default", "mrope", "linear", "llama3", "yarn"). Scalings whose
     frequencies depend on the sequence length at prefill ("dynamic",
     "longrope") leave no single rotation between two positions and are
     rejected."""
     if not rope_scaling:
         return rope_inv_freq(rot_dim, theta)
     kind = rope_scaling.get("rope_type", rope_scaling.get("type", "default"))
-    if kind == "default":
+    if kind in ("default", "mrope"):
+        # M-RoPE (Qwen2-VL) splits the rotary dims into temporal / height /
+        # width sections driven by three position components, with the
+        # plain frequencies. Moving a cached chunk shifts all three by the
+        # same delta, so one delta rotation with these frequencies is exact.
         return rope_inv_freq(rot_dim, theta)
     if kind == "linear":
         return rope_inv_freq(rot_dim, theta) / float(rope_scaling["factor"])

@@ -54,3 +54,20 @@ def test_data_plane_takes_scaling(tmp_path):
     np.testing.assert_array_equal(p.inv_freq, position.inv_freq_for(sc, 128, 5e5))
     with pytest.raises(ValueError, match="sequence length"):
         KVDataPlane(str(tmp_path / "s"), rope_scaling={"rope_type": "dynamic", "factor": 2.0})
+
+
+def test_mrope_uses_plain_frequencies():
+    """Qwen2-VL's M-RoPE: three position components over sections of the
+    rotary dims, plain frequencies; a chunk moved by d shifts every
+    component by d, which is one rotation by d on every pair."""
+    sc = {"type": "mrope", "mrope_section": [16, 24, 24]}
+    np.testing.assert_array_equal(position.inv_freq_for(sc, 128, 1e6),
+                                  position.rope_inv_freq(128, 1e6))
+    # the composed rotation of the three sections at positions (p+d, p+d, p+d)
+    # after (p, p, p) equals the rotation by d
+    inv = position.rope_inv_freq(128, 1e6)
+    bounds = np.cumsum([0] + sc["mrope_section"])
+    p, d = np.array([7, 3, 11]), 250
+    ang_before = np.concatenate([p[i] * inv[bounds[i]:bounds[i + 1]] for i in range(3)])
+    ang_after = np.concatenate([(p[i] + d) * inv[bounds[i]:bounds[i + 1]] for i in range(3)])
+    np.testing.assert_allclose(ang_after - ang_before, d * inv, rtol=1e-12)
