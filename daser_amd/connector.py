@@ -21,7 +21,10 @@ assembled into one request, each with its own positions).
 
 Extra ``kv_connector_extra_config`` keys: ``rope_theta`` (default 10000),
 ``rope_style`` ("neox" | "gptj"), ``rotary_dim`` (default head_dim),
-``rope_scaling`` (the model's HF ``rope_scaling`` dict: linear, llama3, yarn),
+``rope_scaling`` (the model's HF ``rope_scaling`` dict: linear, llama3, yarn,
+mrope), ``rope_layers`` (per model layer: None for no RoPE, or
+{"rope_theta", "rope_scaling"}; for models whose layers differ), all three
+read from ``vllm_config.model_config.hf_config`` when not given,
 ``save_mode`` ("per_layer" | "deferred": one all-layer gather in
 wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry), ``io_readers``
 (rings reading a load in parallel, default 4),
@@ -218,7 +221,8 @@ class KVDataPlane:
                  save_mode: str = "per_layer",
                  io_slot_bytes: int = 4 << 20, io_slots: int = 8,
                  io_backend: str = "native", save_stream: str = "side",
-                 k_scales: Optional[torch.Tensor] = None, io_readers: int = 4) -> None:
+                 k_scales: Optional[torch.Tensor] = None, io_readers: int = 4,
+                 layer_rope: Optional[list] = None) -> None:
         if save_mode not in ("per_layer", "deferred"):
             raise ValueError("save_mode must be 'per_layer' or 'deferred'")
         if io_backend not in ("native", "direct", "python"):
@@ -234,6 +238,10 @@ class KVDataPlane:
         self.rotary_dim = rotary_dim
         self.inv_freq = inv_freq
         self.rope_scaling = rope_scaling
+        # per model layer: None (no RoPE) or {"rope_theta", "rope_scaling"}
+        self.layer_rope = layer_rope
+        self._layer_group: Optional[torch.Tensor] = None
+        self._group_inv: list[np.ndarray] = []
         if rope_scaling and inv_freq is None:
             from daser_amd.position import inv_freq_for
 
@@ -278,6 +286,8 @@ class KVDataPlane:
             from daser_amd.position import inv_freq_for
 
             self.inv_freq = inv_freq_for(self.rope_scaling, self.rotary_dim, self.rope_theta)
+        if self.layer_rope is not None:
+            self._register_layer_rope()
         preallocate_store(self.store_path, max(self.slot_bytes * 1024, 64 << 20))
         if self.save_stream == "side" and lay.device.type == "cuda" and self._side is None:
             self._side = torch.cuda.Stream(lay.device)  # default priority
@@ -287,6 +297,28 @@ class KVDataPlane:
         if self.io is None:
             self.io = self._open_ring(lay.device)
         return self.slot_bytes
+
+    def _register_layer_rope(self) -> None:
+        """Groups of layers sharing RoPE frequencies (layer_rope is indexed
+        by the model's layer number, read from names like
+        "model.layers.12.self_attn.attn", else by registration order)."""
+        import re
+
+        from daser_amd.position import layer_rope_groups
+
+        specs = []
+        for pos, name in enumerate(self.layer_names):
+            m = re.search(r"layers\.(\d+)\.", name)
+            idx = int(m.group(1)) if m else pos
+            if idx >= len(self.layer_rope):
+                raise ValueError(f"layer_rope has no entry for layer {idx} ({name})")
+            specs.append(self.layer_rope[idx])
+        groups, invs = layer_rope_groups(specs, self.rotary_dim, self.rope_theta)
+        if len(invs) == 1 and (groups >= 0).all():
+            self.inv_freq = invs[0]  # one RoPE after all: the single-table path
+            return
+        self._group_inv = invs
+        self._layer_group = torch.from_numpy(groups).to(self.table.layout.device)
 
     def _open_ring(self, device: torch.device):
         from daser_amd.store_io import NativeRingIO, PinnedRingIO
@@ -414,7 +446,12 @@ class KVDataPlane:
             return
         arena = torch.empty(plan.arena_bytes, dtype=torch.uint8, device=self.device)
         tabs = None
-        if plan.deltas:
+        if plan.deltas and self._layer_group is not None:
+            if self._group_inv:  # [groups, tables, rot/2, 2]; layers in group -1 keep K
+                tabs = torch.stack([position.delta_tables(plan.deltas, self.rotary_dim,
+                                                          inv_freq=inv, device=self.device)
+                                    for inv in self._group_inv])
+        elif plan.deltas:
             tabs = position.delta_tables(plan.deltas, self.rotary_dim, self.rope_theta,
                                          inv_freq=self.inv_freq, device=self.device)
         page_read = plan.page_read if plan.page_read.size else np.zeros(plan.page_ids.size,
@@ -437,7 +474,8 @@ class KVDataPlane:
             else:
                 ops.scatter_rerotate(self.table, plan.page_ids[sel], plan.src_offsets[sel],
                                      arena, tabs, plan.rope_idx[sel], rot_dim=self.rotary_dim,
-                                     style=self.rope_style, k_scale=self.k_scales)
+                                     style=self.rope_style, k_scale=self.k_scales,
+                                     layer_group=self._layer_group)
 
     def _read_batch(self, arena: torch.Tensor, reads: list[tuple[int, int, int]]) -> None:
         """Reads (arena_off, nbytes, file_off) ranges into the arena with the
@@ -548,12 +586,18 @@ class DaserConnector(KVConnectorBase_V1):
         else:
             self._ipc_async = ipc_async if ipc_async is not None else _default_ipc(
                 "async", self._socket_path)
+            from daser_amd.position import layer_rope_from_hf, model_rope_from_hf
+
+            hf = getattr(getattr(vllm_config, "model_config", None), "hf_config", None)
+            hf_theta, hf_scaling = model_rope_from_hf(hf) if hf is not None else (None, None)
             self._plane = KVDataPlane(
                 self._store_path,
-                rope_theta=float(extra.get("rope_theta", 10000.0)),
+                rope_theta=float(extra.get("rope_theta", hf_theta or 10000.0)),
                 rope_style=extra.get("rope_style", "neox"),
                 rotary_dim=extra.get("rotary_dim"),
-                rope_scaling=extra.get("rope_scaling"),
+                rope_scaling=extra.get("rope_scaling", hf_scaling),
+                layer_rope=extra.get("rope_layers",
+                                     layer_rope_from_hf(hf) if hf is not None else None),
                 save_mode=extra.get("save_mode", "per_layer"),
                 io_slot_bytes=int(float(extra.get("io_slot_mb", 4)) * (1 << 20)),
                 io_slots=int(extra.get("io_slots", 8)),

@@ -309,7 +309,8 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          int n_pages, const void* staging,
                          int64_t staging_bytes, int64_t layer_bytes,
                          int layer0, const float* cos_sin,
-                         const int32_t* rope_idx, int n_tables, int head_dim,
+                         const int32_t* rope_idx, int n_tables,
+                         const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
                          const float* k_scale, dsr_stream_t stream) {
   int rc = check_common(layer_base, n_layers, kv_stride, page_stride, page_bytes,
@@ -331,7 +332,7 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
     default:
       return DSR_ERR_ARG;
   }
-  if (n_tables < 0) return DSR_ERR_ARG;
+  if (n_tables < 0 || (layer_group && n_groups < 1)) return DSR_ERR_ARG;
   if (head_dim <= 0 || rot_dim <= 0 || rot_dim > head_dim || (rot_dim & 1) ||
       rot_dim / 2 > kMaxRotHalf)
     return DSR_ERR_SHAPE;
@@ -357,6 +358,8 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
   ra.cos_sin = reinterpret_cast<const float2*>(cos_sin);
   ra.rope_idx = rope_idx;
   ra.n_tables = n_tables;
+  ra.layer_group = layer_group;
+  ra.n_groups = layer_group ? n_groups : 1;
   ra.row_vecs = (int)(row_bytes / 16);
   ra.rot_half = rot_dim / 2;
   ra.task_vecs = task_vecs;

@@ -127,6 +127,8 @@ struct RotArgs {
   const float2* cos_sin;
   const int32_t* rope_idx;
   int32_t n_tables;
+  const int32_t* layer_group;  // per record layer: table block, -1 = no RoPE (null: all 0)
+  int32_t n_groups;
   int32_t row_vecs;    // 16-byte vectors per K row (head_dim * e / 16)
   int32_t rot_half;    // rot_dim / 2 (pairs per row)
   int32_t task_vecs;   // rotation tasks per row
@@ -136,6 +138,17 @@ struct RotArgs {
   int32_t half_vecs;  // neox: vectors from a first-half vector to its partner
   const float* k_scale;
 };
+
+// Table of unit (page p, layer l): page p's delta table inside layer l's
+// group block (cos_sin holds n_groups blocks of n_tables tables), or -1 when
+// the page keeps its position or the layer has no RoPE (K copied as is).
+__device__ __forceinline__ int rope_table(const RotArgs& ra, int64_t p, int l) {
+  const int ti = ra.rope_idx[p];
+  if (ti < 0 || ti >= ra.n_tables) return -1;
+  if (!ra.layer_group) return ti;
+  const int g = ra.layer_group[ra.u.layer0 + l];
+  return g < 0 || g >= ra.n_groups ? -1 : g * ra.n_tables + ti;
+}
 
 // Rotates the K page (rows of head_dim elements) from src into dst.
 // neox task c: vector c of the first half and its partner at +rot_half;
@@ -262,9 +275,9 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
   const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
   if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
   const int64_t p = u / ra.u.n_layers;
-  const int ti = ra.rope_idx[p];
+  const int ti = rope_table(ra, p, l);
   const int64_t pb = ra.u.page_bytes;
-  if (ti < 0 || ti >= ra.n_tables) {
+  if (ti < 0) {
     copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
     return;
   }
@@ -386,9 +399,9 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
   const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
   if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
   const int64_t p = u / ra.u.n_layers;
-  const int ti = ra.rope_idx[p];
+  const int ti = rope_table(ra, p, l);
   const int64_t pb = ra.u.page_bytes;
-  if (ti < 0 || ti >= ra.n_tables) {
+  if (ti < 0) {
     copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
     return;
   }
@@ -437,9 +450,9 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_rows_kernel(RotA
   const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
   if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
   const int64_t p = u / ra.u.n_layers;
-  const int ti = ra.rope_idx[p];
+  const int ti = rope_table(ra, p, l);
   const int64_t pb = ra.u.page_bytes;
-  if (ti < 0 || ti >= ra.n_tables) {
+  if (ti < 0) {
     copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
     return;
   }
@@ -530,17 +543,17 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
     rv[k] = bload(make_rsrc(u.rec + a.page_bytes, u.n), off[k]);
     kd[k] = make_rsrc(u.cache, u.n);
     vd[k] = make_rsrc(u.cache + a.kv_stride, u.n);
-    const int ti = u.n ? ra.rope_idx[u.p] : -1;
-    tj[k] = ti >= 0 && ti < ra.n_tables ? j : -1;
+    tj[k] = u.n && rope_table(ra, u.p, u.l) >= 0 ? j : -1;
     sc[k] = DT == DSR_DTYPE_FP8_E4M3 && u.n ? ra.k_scale[a.layer0 + u.l] : 1.0f;
   }
   // tables of the group's units, fetched while the page loads are in flight
   for (int e = threadIdx.x; e < (int)n_here * ra.rot_half; e += kThreads) {
     const int jj = e / ra.rot_half;
-    const int64_t p = (p0 + jj) % n_pages;
-    const int ti = ra.rope_idx[p];
-    if (ti >= 0 && ti < ra.n_tables)
-      tab[e] = ra.cos_sin[(int64_t)ti * ra.rot_half + (e - jj * ra.rot_half)];
+    int64_t p;
+    int l;
+    unit_at<false>(a, n_pages, p0, l0, jj, &p, &l);
+    const int ti = rope_table(ra, p, l);
+    if (ti >= 0) tab[e] = ra.cos_sin[(int64_t)ti * ra.rot_half + (e - jj * ra.rot_half)];
   }
 #pragma unroll
   for (int k = 0; k < U; ++k) bstore(vd[k], off[k], rv[k]);

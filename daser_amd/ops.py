@@ -262,27 +262,40 @@ def scatter_rerotate(
     k_scale: Optional[torch.Tensor] = None,
     layer0: int = 0,
     layers: Optional[tuple[int, int]] = None,
+    layer_group=None,
 ) -> None:
     """Scatter with K re-rotated by ``cos_sin[rope_idx[p]]`` (-1 = copy).
 
     ``cos_sin`` is a float32 tensor ``[n_tables, rot_dim/2, 2]`` from
     :func:`daser_amd.position.delta_tables`; ``k_scale`` holds per-layer
-    fp32 scales (fp8 caches only).
+    fp32 scales (fp8 caches only). For models whose layers differ in RoPE
+    (other frequencies, or none), ``cos_sin`` is ``[n_groups, n_tables,
+    rot_dim/2, 2]`` and ``layer_group[layer0 + l]`` picks layer l's group
+    (-1: no RoPE, K copied).
     """
     lay = table.layout
     if lay.dtype not in _DTYPE_CODES:
         raise TypeError(f"re-rotation does not support KV dtype {lay.dtype}")
     rot_dim = lay.head_dim if rot_dim is None else rot_dim
-    if cos_sin.dtype != torch.float32 or cos_sin.dim() != 3 or cos_sin.shape[1:] != (
-        rot_dim // 2,
-        2,
-    ):
-        raise ValueError(f"cos_sin must be float32 [n, {rot_dim // 2}, 2]")
+    grouped = layer_group is not None
+    if cos_sin.dtype != torch.float32 or cos_sin.dim() != (4 if grouped else 3) or \
+            cos_sin.shape[-2:] != (rot_dim // 2, 2):
+        shape = "[groups, n, {}, 2]" if grouped else "[n, {}, 2]"
+        raise ValueError("cos_sin must be float32 " + shape.format(rot_dim // 2))
     if cos_sin.device != lay.device or not cos_sin.is_contiguous():
         raise ValueError("cos_sin must be a contiguous device tensor")
+    n_groups = cos_sin.shape[0] if grouped else 1
+    n_tables = cos_sin.shape[-3]
     ridx = _host_array(rope_idx, np.int64)
-    if ridx is not None and ridx.size and (ridx.max() >= cos_sin.shape[0] or ridx.min() < -1):
+    if ridx is not None and ridx.size and (ridx.max() >= n_tables or ridx.min() < -1):
         raise IndexError("rope_idx outside [-1, n_tables)")
+    lg_d = None
+    if grouped:
+        lg = _host_array(layer_group, np.int64)
+        if lg is not None and (lg.size < layer0 + lay.num_layers or
+                               (lg.size and (lg.min() < -1 or lg.max() >= n_groups))):
+            raise IndexError("layer_group needs one group in [-1, n_groups) per layer")
+        lg_d = _as_device_table(layer_group, torch.int32, lay.device, "layer_group")
     page_ids, slot_offsets, rope_idx = dest_order(page_ids, slot_offsets, rope_idx)
     args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
     ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")
@@ -303,7 +316,9 @@ def scatter_rerotate(
         *args,
         cos_sin.data_ptr(),
         ridx_d.data_ptr(),
-        cos_sin.shape[0],
+        n_tables,
+        None if lg_d is None else lg_d.data_ptr(),
+        n_groups if grouped else 0,
         lay.head_dim,
         rot_dim,
         ROPE_STYLES[style],

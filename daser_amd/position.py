@@ -167,6 +167,98 @@ def inv_freq_for(rope_scaling: Optional[dict], rot_dim: int, theta: float) -> np
                      "cannot be re-rotated by a position delta")
 
 
+def layer_rope_groups(specs: Sequence[Optional[dict]], rot_dim: int,
+                      default_theta: float = 10000.0) -> tuple[np.ndarray, list[np.ndarray]]:
+    """Per-layer RoPE specs -> (group of each layer, inv_freq of each group).
+
+    ``specs[l]`` is None for a layer without RoPE (group -1), else a dict with
+    ``rope_theta`` and optionally ``rope_scaling``; layers with the same
+    frequencies share a group.
+    """
+    groups: list[np.ndarray] = []
+    keys: dict[bytes, int] = {}
+    out = np.full(len(specs), -1, np.int32)
+    for l, spec in enumerate(specs):
+        if spec is None:
+            continue
+        inv = inv_freq_for(spec.get("rope_scaling"), rot_dim,
+                           float(spec.get("rope_theta", default_theta)))
+        k = inv.tobytes()
+        if k not in keys:
+            keys[k] = len(groups)
+            groups.append(inv)
+        out[l] = keys[k]
+    return out, groups
+
+
+def _text_config(hf_config):
+    return getattr(hf_config, "text_config", None) or hf_config
+
+
+def model_rope_from_hf(hf_config) -> tuple[Optional[float], Optional[dict]]:
+    """(rope_theta, rope_scaling) of a HF config, in either form
+    transformers uses: ``rope_theta`` / ``rope_scaling`` attributes, or one
+    ``rope_parameters`` dict (which carries ``rope_theta`` itself). For
+    per-layer-type parameters the full-attention entry is returned."""
+    cfg = _text_config(hf_config)
+    rp = getattr(cfg, "rope_parameters", None)
+    if isinstance(rp, dict) and rp:
+        if all(isinstance(v, dict) for v in rp.values()):
+            rp = rp.get("full_attention") or next(iter(rp.values()))
+        theta = rp.get("rope_theta")
+        return (None if theta is None else float(theta)), dict(rp)
+    theta = getattr(cfg, "rope_theta", None)
+    return (None if theta is None else float(theta)), getattr(cfg, "rope_scaling", None)
+
+
+def layer_rope_from_hf(hf_config) -> Optional[list[Optional[dict]]]:
+    """Per-layer RoPE of models whose layers differ, from a HF config; None
+    when every layer uses the model's one RoPE.
+
+    * local / global attention layers with their own bases (Gemma 3):
+      ``rope_parameters`` keyed by layer type, or ``rope_local_base_freq``
+      (unscaled) for "sliding_attention" layers in ``layer_types``;
+    * layers without RoPE (Llama 4: ``no_rope_layers[l] == 0``).
+    """
+    cfg = _text_config(hf_config)
+    n = getattr(cfg, "num_hidden_layers", None)
+    if not n:
+        return None
+    theta, scaling = model_rope_from_hf(hf_config)
+    base = {"rope_theta": theta if theta is not None else 10000.0, "rope_scaling": scaling}
+    specs: list[Optional[dict]] = [dict(base) for _ in range(n)]
+    differs = False
+    types = getattr(cfg, "layer_types", None)
+    rp = getattr(cfg, "rope_parameters", None)
+    per_type = isinstance(rp, dict) and rp and all(isinstance(v, dict) for v in rp.values())
+    local = getattr(cfg, "rope_local_base_freq", None)
+    if types:
+        for l, t in enumerate(list(types)[:n]):
+            if per_type and t in rp:
+                spec = {"rope_theta": float(rp[t].get("rope_theta", base["rope_theta"])),
+                        "rope_scaling": dict(rp[t])}
+            elif t == "sliding_attention" and local is not None:
+                spec = {"rope_theta": float(local), "rope_scaling": None}
+            else:
+                continue
+            if spec != specs[l]:
+                specs[l] = spec
+                differs = True
+    no_rope = getattr(cfg, "no_rope_layers", None)
+    if no_rope:
+        for l, use in enumerate(list(no_rope)[:n]):
+            if not use:
+                specs[l] = None
+                differs = True
+    if differs:
+        # compared on 64 dims (a 2-dim probe has the frequency 1 for any base)
+        inv = [None if sp is None else inv_freq_for(sp.get("rope_scaling"), 64, sp["rope_theta"])
+               for sp in specs]
+        if all(x is not None for x in inv) and all(np.array_equal(x, inv[0]) for x in inv):
+            return None  # written per layer type, but the same everywhere
+    return specs if differs else None
+
+
 def delta_tables(
     deltas: Sequence[int],
     rot_dim: int,

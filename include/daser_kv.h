@@ -44,7 +44,7 @@ extern "C" {
 
 typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 
-#define DSR_ABI_VERSION 1
+#define DSR_ABI_VERSION 2
 
 /*
  * Kernel choice and launch shape follow from the geometry; these environment
@@ -146,9 +146,18 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
  * only carries an integer offset, which this path consumes); the copy it
  * fuses into replaces daser/connector/daser_connector.py:536-551.
  *
- *   cos_sin   [device] n_tables * (rot_dim/2) float pairs (cos, sin)
- *   rope_idx  [device] n_pages int32 table index per page, -1 = no rotation
- *   n_tables  number of tables (bounds rope_idx)
+ * Models whose layers use different RoPE frequencies (e.g. local and global
+ * attention layers with different bases) or no RoPE on some layers pass
+ * layer_group: layer l of the record rotates with block layer_group[layer0 +
+ * l] of the tables, and a layer with group -1 is copied unchanged.
+ *
+ *   cos_sin     [device] n_groups * n_tables * (rot_dim/2) float pairs
+ *               (cos, sin): table t of group g at (g * n_tables + t)
+ *   rope_idx    [device] n_pages int32 table index per page, -1 = no rotation
+ *   n_tables    tables per group (bounds rope_idx)
+ *   layer_group [device] int32 group of each record layer (indexed layer0 +
+ *               l), -1 = no RoPE on that layer; null: one group for all
+ *   n_groups    groups in cos_sin (>= 1 when layer_group is given)
  *   head_dim, rot_dim   rot_dim even, <= head_dim, page_bytes a multiple of
  *                       one row; see DSR_ERR_SHAPE for vector constraints
  *   k_scale   [device] per-layer fp32 scales, indexed layer0 + l; required
@@ -162,7 +171,8 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          int n_pages, const void* staging,
                          int64_t staging_bytes, int64_t layer_bytes,
                          int layer0, const float* cos_sin,
-                         const int32_t* rope_idx, int n_tables, int head_dim,
+                         const int32_t* rope_idx, int n_tables,
+                         const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
                          const float* k_scale, dsr_stream_t stream);
 

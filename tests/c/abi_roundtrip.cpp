@@ -96,7 +96,8 @@ int main() {
   REQUIRE(hipMalloc(&ridx, n * sizeof(int32_t)) == hipSuccess, "hipMalloc");
   hipMemset(ridx, 0xff, n * sizeof(int32_t));
   rc = dsr_scatter_rerotate(bases + L, L, NB * page, page, page, NB, d_ids, d_offs, n, stg,
-                            n * slot, layer_bytes, 0, tab, ridx, 1, D, D, DSR_ROPE_NEOX,
+                            n * slot, layer_bytes, 0, tab, ridx, 1, nullptr, 0, D, D,
+                            DSR_ROPE_NEOX,
                             DSR_DTYPE_BF16, nullptr, nullptr);
   REQUIRE(rc == 0, dsr_error_string(rc));
   std::vector<uint8_t> c3(L * cache_bytes);

@@ -64,9 +64,10 @@ def test_rerotate_argument_errors():
     lib = _lib.lib()
     base = [16, 1, 4096, 4096, 4096, 8, 32, 48, 1, 64, 1 << 20, 8192, 0]
 
-    def call(head_dim=128, rot_dim=128, style=0, dtype=0, k_scale=80, n_tables=1):
-        return lib.dsr_scatter_rerotate(*base, 96, 112, n_tables, head_dim, rot_dim,
-                                        style, dtype, k_scale, None)
+    def call(head_dim=128, rot_dim=128, style=0, dtype=0, k_scale=80, n_tables=1,
+             layer_group=None, n_groups=0):
+        return lib.dsr_scatter_rerotate(*base, 96, 112, n_tables, layer_group, n_groups,
+                                        head_dim, rot_dim, style, dtype, k_scale, None)
 
     assert call(style=7) == _lib.DSR_ERR_ARG
     assert call(dtype=9) == _lib.DSR_ERR_ARG
@@ -75,6 +76,7 @@ def test_rerotate_argument_errors():
     assert call(head_dim=100, rot_dim=100) == _lib.DSR_ERR_SHAPE  # page not whole rows
     assert call(dtype=2, rot_dim=48, head_dim=64) == _lib.DSR_ERR_SHAPE
     assert call(dtype=2, k_scale=None) == _lib.DSR_ERR_ARG
+    assert call(layer_group=128, n_groups=0) == _lib.DSR_ERR_ARG  # groups without a count
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

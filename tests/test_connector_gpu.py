@@ -480,3 +480,41 @@ def test_uncommitted_chunk_is_never_loaded(gpu, tmp_path):
     assert sched.get_num_new_matched_tokens(req, 0) == (0, False)
     assert server.pending and not server.committed  # allocated, not visible
     w.shutdown()
+
+
+def test_load_rerotates_each_layer_with_its_rope(gpu, tmp_path):
+    """rope_layers (local / global bases, a layer without RoPE): a moved
+    chunk's K is rotated per layer with that layer's frequencies, and left
+    as stored on the layer without RoPE."""
+    print("case: connector per-layer rope", flush=True)
+    rope = [{"rope_theta": 10000.0}, None, {"rope_theta": 1000000.0}]
+    w, _ = _worker(tmp_path)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=43)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    _save(w, named, _store_reqs())
+    slot = SHAPE.slot_bytes
+    recs = _file_records(tmp_path / "daser.store", 3, 3).copy()
+    fresh = [torch.zeros_like(c) for c in caches]
+    w2, _ = _worker(tmp_path, rope_layers=rope)
+    w2.register_kv_caches(_named(fresh))
+    w2.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_load={
+        "x": C.ReqLoadSpec("ka", 3, 3, [1, 12, 4], 3 * slot, 40, pos_offset=100, new_pos=9000)}))
+    w2.start_load_kv(None)
+    torch.cuda.synchronize()
+    for l, spec in enumerate(rope):
+        ref = [np.zeros_like(to_bits_np(caches[l], "bf16"))]
+        oracle.scatter_rerotate(ref, [1, 12, 4], np.arange(3) * slot, recs, SHAPE.layer_bytes,
+                                dtype=oracle.BF16, rot_dim=64, style=oracle.NEOX,
+                                stored_pos=np.full(3, 100), new_pos=np.full(3, 9000),
+                                rotate=np.full(3, spec is not None),
+                                theta=spec["rope_theta"] if spec else 1.0, layer0=l)
+        got = to_bits_np(fresh[l], "bf16")
+        assert np.array_equal(got[1][[1, 12, 4]], ref[0][1][[1, 12, 4]])
+        if spec is None:
+            assert np.array_equal(got[0][[1, 12, 4]], ref[0][0][[1, 12, 4]])
+        ok, msg = oracle.rotation_within_tolerance(got[0][[1, 12, 4]], ref[0][0][[1, 12, 4]],
+                                                   oracle.BF16)
+        assert ok, f"layer {l}: {msg}"
+    w.shutdown()
+    w2.shutdown()

@@ -795,3 +795,55 @@ def test_random_geometry_slots_parity(gpu, dt, D, H, bs, style, R, L, seed):
     assert np.array_equal(st.cpu().numpy(), ref)
     for l in range(L):
         assert np.array_equal(to_bits_np(dst[l], dt), dref[l]), f"layer {l}"
+
+
+@pytest.mark.parametrize("heads,head_dim,dt,kernel", [
+    (8, 128, "bf16", None),    # grouped kernel, one unit per workgroup
+    (1, 128, "bf16", None),    # grouped, several units per workgroup
+    (8, 128, "e4m3", None),    # contig kernel
+    (4, 96, "bf16", None),     # row-aligned kernel
+    (4, 96, "bf16", "pairs"),  # pair-task kernel
+    (16, 128, "bf16", None),   # 64 KiB pages: contig kernel in rounds
+])
+def test_rerotate_per_layer_groups(gpu, monkeypatch, heads, head_dim, dt, kernel):
+    """Layers with different RoPE bases (local / global attention) and layers
+    without RoPE: layer_group picks each layer's table block; group -1
+    copies K. Each layer matches the oracle run with its own base."""
+    print(f"case: rerotate layer groups H{heads} D{head_dim} {dt} {kernel}", flush=True)
+    if kernel:
+        monkeypatch.setenv("DSR_ROT_KERNEL", kernel)
+    L = 6
+    groups = np.array([0, 1, -1, 0, 1, -1], np.int32)
+    thetas = [10000.0, 1000000.0]
+    shape = KVShape(L, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    rng = np.random.default_rng(heads * 1000 + head_dim)
+    nb, n = 24, 10
+    src = rand_caches(shape, nb, dt, gpu, seed=91, scale=40.0 if dt == "e4m3" else 1.0)
+    st = torch.zeros(n * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    offs = np.arange(n, dtype=np.int64) * shape.slot_bytes
+    ops.gather(ops.LayerTable(src), rng.permutation(nb)[:n].astype(np.int32), offs, st)
+    deltas = rng.integers(1, 32768, size=n) * (np.arange(n) % 4 != 0)  # some pages unmoved
+    ridx, uniq = position.page_rope_index([1] * n, deltas)
+    tabs = torch.stack([position.delta_tables(uniq, head_dim, t, device=gpu) for t in thetas])
+    ks_np = (rng.random(L).astype(np.float32) * 0.5 + 0.01) if dt == "e4m3" else None
+    ks = torch.from_numpy(ks_np).to(gpu) if ks_np is not None else None
+    dst_ids = rng.permutation(nb)[:n].astype(np.int32)
+    out = [torch.zeros_like(c) for c in src]
+    ops.scatter_rerotate(ops.LayerTable(out), dst_ids, offs, st, tabs, ridx, k_scale=ks,
+                         layer_group=groups)
+    recs = st.cpu().numpy()
+    d = np.asarray(deltas, np.int64)
+    torch.cuda.synchronize()
+    for l in range(L):
+        ref = [np.zeros_like(to_bits_np(src[l], dt))]
+        g = groups[l]
+        oracle.scatter_rerotate(ref, dst_ids, offs, recs, shape.layer_bytes, dtype=ORC_DT[dt],
+                                rot_dim=head_dim, style=0, stored_pos=np.zeros(n, np.int64),
+                                new_pos=d, rotate=(d != 0) & (g >= 0),
+                                theta=thetas[max(g, 0)], k_scale=ks_np, layer0=l)
+        got = to_bits_np(out[l], dt)
+        assert np.array_equal(got[1], ref[0][1]), f"V layer {l}"
+        if g < 0:
+            assert np.array_equal(got[0], ref[0][0]), f"no-RoPE layer {l} must be a copy"
+        ok, msg = rotation_within_tolerance(got[0], ref[0][0], dt)
+        assert ok, f"K layer {l} (group {g}): {msg}"

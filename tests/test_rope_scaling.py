@@ -71,3 +71,63 @@ def test_mrope_uses_plain_frequencies():
     ang_before = np.concatenate([p[i] * inv[bounds[i]:bounds[i + 1]] for i in range(3)])
     ang_after = np.concatenate([(p[i] + d) * inv[bounds[i]:bounds[i + 1]] for i in range(3)])
     np.testing.assert_allclose(ang_after - ang_before, d * inv, rtol=1e-12)
+
+
+def test_per_layer_rope_from_hf_configs():
+    """Gemma 3 (local / global bases) and Llama 4 (layers without RoPE) give
+    layer groups; a plain Llama config gives none."""
+    from transformers import Gemma3TextConfig, Llama4TextConfig
+
+    specs = position.layer_rope_from_hf(Gemma3TextConfig(num_hidden_layers=12))
+    groups, invs = position.layer_rope_groups(specs, 256)
+    assert groups.tolist() == [0, 0, 0, 0, 0, 1] * 2
+    np.testing.assert_allclose(invs[0], position.rope_inv_freq(256, 10000.0))
+    np.testing.assert_allclose(invs[1], position.rope_inv_freq(256, 1e6))
+    specs = position.layer_rope_from_hf(Llama4TextConfig(num_hidden_layers=8))
+    groups, invs = position.layer_rope_groups(specs, 128)
+    assert groups.tolist() == [0, 0, 0, -1, 0, 0, 0, -1] and len(invs) == 1
+    assert position.layer_rope_from_hf(_cfg(5e5, None, 8192)) is None
+    assert position.model_rope_from_hf(_cfg(5e5, None, 8192))[0] == 5e5
+
+
+def test_data_plane_layer_groups(tmp_path):
+    """Registered layers are mapped to model layers by their names; a
+    per-layer list with one RoPE collapses to the single-table path."""
+    import torch
+
+    from daser_amd.connector import KVDataPlane
+
+    caches = {f"model.layers.{i}.self_attn.attn": torch.zeros(2, 4, 16, 1, 64,
+                                                              dtype=torch.bfloat16)
+              for i in (0, 1, 2, 3)}
+    rope = [{"rope_theta": 1e4}, None, {"rope_theta": 1e6}, {"rope_theta": 1e4}]
+    p = KVDataPlane(str(tmp_path / "s"), io_backend="python", layer_rope=rope)
+    p.register(caches)
+    assert p._layer_group.tolist() == [0, -1, 1, 0]
+    p.close()
+    same = [{"rope_theta": 5e5}] * 4
+    q = KVDataPlane(str(tmp_path / "t"), io_backend="python", layer_rope=same)
+    q.register(caches)
+    assert q._layer_group is None
+    np.testing.assert_array_equal(q.inv_freq, position.rope_inv_freq(64, 5e5))
+    q.close()
+    r = KVDataPlane(str(tmp_path / "u"), io_backend="python", layer_rope=rope[:2])
+    with pytest.raises(ValueError, match="no entry for layer 2"):
+        r.register(caches)
+
+
+def test_connector_reads_rope_from_model_config(tmp_path):
+    from types import SimpleNamespace
+
+    from daser_amd import connector as C
+
+    hf = _cfg(5e5, {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+                    "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}, 131072)
+    cfg = SimpleNamespace(
+        model_config=SimpleNamespace(hf_config=hf),
+        kv_transfer_config=SimpleNamespace(kv_connector_extra_config=dict(
+            store_path=str(tmp_path / "s"), io_backend="python")))
+    w = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=object())
+    assert w._plane.rope_theta == 5e5
+    assert w._plane.rope_scaling["rope_type"] == "llama3"
+    w.shutdown()
