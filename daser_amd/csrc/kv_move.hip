@@ -26,7 +26,8 @@
 //     KiB and 16-bit pages of exactly U * 4 KiB; kv_scatter_rerotate_contig_
 //     kernel for larger pages with a power-of-two partner distance;
 //     kv_scatter_rerotate_rows_kernel for other neox rows of <= 64 vectors;
-//     the pair-task kv_scatter_rerotate_kernel otherwise.
+//     the pair-task kv_scatter_rerotate_kernel otherwise; rotary widths that
+//     are not whole 16-byte vectors: kv_scatter_rerotate_lds_kernel.
 //   token form (dsr_gather_slots / dsr_scatter_slots): kv_slots_small_kernel
 //     for rows of <= 32 vectors, kv_slots_kernel above.
 // Calls too large for one launch run as several over page (token) ranges.
@@ -177,10 +178,21 @@ size_t rot_occupancy_lds(int wg_per_cu) {
 }
 
 template <int DT>
-int launch_rerotate(const RotArgs& ra, int n_pages, int style, hipStream_t s) {
+int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipStream_t s) {
   const int h = ra.half_vecs;
   int wg = rot_wg_per_cu<DT>();
   if (const char* e = getenv("DSR_ROT_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
+  if (!vec_ok) {  // rotary width not in whole vectors: the LDS kernel
+    return launch_page_ranges(ra.u, n_pages, 1, [&](const UnitArgs& b, unsigned grid) {
+      RotArgs rb = ra;
+      rb.u = b;
+      rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
+      if (style == DSR_ROPE_NEOX)
+        kv_scatter_rerotate_lds_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, 0, s>>>(rb);
+      else
+        kv_scatter_rerotate_lds_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, 0, s>>>(rb);
+    });
+  }
   const bool contig = style == DSR_ROPE_GPTJ ||
                       (h > 0 && h <= 32 && (h & (h - 1)) == 0 && ra.row_vecs % (2 * h) == 0);
   const int G = contig ? units_per_group(ra.u.page_bytes, rot_contig_unroll<DT>(),
@@ -338,15 +350,13 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
     return DSR_ERR_SHAPE;
   const int64_t row_bytes = (int64_t)head_dim * esize;
   if (row_bytes % 16 || page_bytes % row_bytes) return DSR_ERR_SHAPE;
-  if (((int64_t)(head_dim - rot_dim) * esize) % 16) return DSR_ERR_SHAPE;
-  int task_vecs;
-  if (rope_style == DSR_ROPE_NEOX) {
-    if ((rot_dim / 2) % ve) return DSR_ERR_SHAPE;
-    task_vecs = rot_dim / 2 / ve;
-  } else {
-    if (rot_dim % ve) return DSR_ERR_SHAPE;
-    task_vecs = rot_dim / ve;
-  }
+  // Whole 16-byte vectors of rotated (and, neox, half-rotated) elements use
+  // the vector kernels; other even rotary widths the LDS kernel.
+  const bool vec_ok = ((int64_t)(head_dim - rot_dim) * esize) % 16 == 0 &&
+                      (rope_style == DSR_ROPE_NEOX ? (rot_dim / 2) % ve == 0 : rot_dim % ve == 0);
+  if (!vec_ok && row_bytes / 16 > 2048) return DSR_ERR_SHAPE;  // one row per LDS chunk
+  const int task_vecs = !vec_ok ? 0 : rope_style == DSR_ROPE_NEOX ? rot_dim / 2 / ve
+                                                                   : rot_dim / ve;
   if (n_pages == 0 || n_layers == 0) return DSR_OK;
   if (!rope_idx || (n_tables > 0 && !cos_sin)) return DSR_ERR_ARG;
   if (dtype == DSR_DTYPE_FP8_E4M3 && !k_scale) return DSR_ERR_ARG;
@@ -366,16 +376,16 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
   ra.tail_vec0 = rot_dim * esize / 16;
   ra.tasks_per_row = task_vecs + (head_dim - rot_dim) * esize / 16;
   ra.rot_vecs = rot_dim * esize / 16;
-  ra.half_vecs = rope_style == DSR_ROPE_NEOX ? rot_dim / 2 * esize / 16 : 0;
+  ra.half_vecs = rope_style == DSR_ROPE_NEOX && vec_ok ? rot_dim / 2 * esize / 16 : 0;
   ra.k_scale = k_scale;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case DSR_DTYPE_BF16:
-      return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, s);
+      return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, vec_ok, s);
     case DSR_DTYPE_FP16:
-      return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, s);
+      return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, vec_ok, s);
     default:
-      return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, s);
+      return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, vec_ok, s);
   }
 }
 

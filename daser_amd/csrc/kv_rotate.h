@@ -509,6 +509,104 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_rows_kernel(RotA
   }
 }
 
+// Any even rot_dim and either style, for rotary widths that do not fill
+// whole 16-byte vectors (partial rotary of 24 or 20 dims, ...). A chunk of
+// the page's K rows is staged in LDS; each lane decodes one output vector,
+// rotates its elements below rot_dim with partners read element by element
+// from LDS (a neox partner may straddle vectors), re-encodes, and keeps the
+// raw bits of the elements at or past rot_dim through a bit mask. One unit
+// per workgroup, layer-major; V is copied alongside.
+template <int DT>
+__device__ __forceinline__ float elem_decode(uint32_t bits) {
+  if (DT == DSR_DTYPE_BF16) return bf16_to_f32(bits);
+  if (DT == DSR_DTYPE_FP16) return fp16_to_f32(bits);
+  return __builtin_amdgcn_cvt_pk_f32_fp8((int)bits, false)[0];
+}
+
+template <int DT, int STYLE>
+__global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_lds_kernel(RotArgs ra) {
+  using C = Codec<DT>;
+  constexpr int VE = C::VE;
+  constexpr int EB = DT == DSR_DTYPE_FP8_E4M3 ? 8 : 16;  // bits per element
+  constexpr int PER = 32 / EB;                           // elements per dword
+  constexpr bool kScaled = DT == DSR_DTYPE_FP8_E4M3;
+  constexpr int kChunkVecs = 2048;  // 32 KiB of K rows per pass
+  __shared__ u32x4 buf[kChunkVecs];
+  __shared__ float2 tab[kMaxRotHalf];
+  uint8_t *cache, *rec;
+  int l;
+  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
+  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  const int64_t p = u / ra.u.n_layers;
+  const int ti = rope_table(ra, p, l);
+  const int64_t pb = ra.u.page_bytes;
+  if (ti < 0) {
+    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    return;
+  }
+  const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
+  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const int nvec = (int)(pb >> 4);
+  {
+    VRound<kRotCopyUnroll> v;  // V: a plain copy
+    for (int base = threadIdx.x; base < nvec; base += kThreads * kRotCopyUnroll) {
+      v.load(vs, base, nvec);
+      v.store(vd, base, nvec);
+    }
+  }
+  const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
+  for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
+  float scale = 1.0f, inv_scale = 1.0f;
+  if (kScaled) {
+    scale = ra.k_scale[ra.u.layer0 + l];
+    inv_scale = 1.0f / scale;
+  }
+  const uint32_t* bw = reinterpret_cast<const uint32_t*>(buf);
+  const int rv = ra.row_vecs, half = ra.rot_half, rot = 2 * ra.rot_half;
+  const int rows = nvec / rv, rpc = kChunkVecs / rv;
+  for (int r0 = 0; r0 < rows; r0 += rpc) {
+    const int nv = (rows - r0 < rpc ? rows - r0 : rpc) * rv;
+    __syncthreads();  // the previous chunk's readers are done (and the table is in)
+    for (int i = threadIdx.x; i < nv; i += kThreads) buf[i] = bload(ks, (r0 * rv + i) << 4);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nv; i += kThreads) {
+      const int row = i / rv, c = i - row * rv;
+      const u32x4 own = buf[i];
+      float x[VE];
+      C::decode(own, x);
+      u32x4 mask = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        const int j = c * VE + e;
+        if (j >= rot) continue;
+        int pj, jj;
+        float sg;
+        if (STYLE == DSR_ROPE_NEOX) {
+          const bool first = j < half;
+          pj = first ? j + half : j - half;
+          jj = first ? j : j - half;
+          sg = first ? -1.0f : 1.0f;
+        } else {
+          pj = j ^ 1;
+          jj = j >> 1;
+          sg = (j & 1) ? 1.0f : -1.0f;
+        }
+        const int pe = pj % VE;
+        const uint32_t word = bw[(row * rv + pj / VE) * 4 + pe / PER];
+        const float pv = elem_decode<DT>((word >> (EB * (pe % PER))) & ((1u << EB) - 1u));
+        const float2 cs = tab[jj];
+        const float xo = kScaled ? x[e] * scale : x[e];
+        const float xp = kScaled ? pv * scale : pv;
+        const float y = xo * cs.x + sg * (xp * cs.y);
+        x[e] = kScaled ? y * inv_scale : y;
+        mask[e / PER] |= ((1u << EB) - 1u) << (EB * (e % PER));
+      }
+      const u32x4 enc = C::encode(x);
+      bstore(kd, (r0 * rv + i) << 4, (enc & mask) | (own & ~mask));
+    }
+  }
+}
+
 // Re-rotation over G units per workgroup (layer-major order, as the one-unit
 // kernel). The group's (cos, sin) tables are staged in LDS, one rot_half
 // stretch per unit; G * rot_half <= kMaxRotHalf. K of an un-rotated unit is

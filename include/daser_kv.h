@@ -158,8 +158,8 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
  *   layer_group [device] int32 group of each record layer (indexed layer0 +
  *               l), -1 = no RoPE on that layer; null: one group for all
  *   n_groups    groups in cos_sin (>= 1 when layer_group is given)
- *   head_dim, rot_dim   rot_dim even, <= head_dim, page_bytes a multiple of
- *                       one row; see DSR_ERR_SHAPE for vector constraints
+ *   head_dim, rot_dim   rot_dim even, <= head_dim; head_dim * element size a
+ *                       multiple of 16 bytes; page_bytes a multiple of one row
  *   k_scale   [device] per-layer fp32 scales, indexed layer0 + l; required
  *             for fp8, ignored otherwise (may be null). There is no V scale:
  *             V is copied as raw bytes, never decoded.

@@ -241,6 +241,13 @@ def _rerotate_case(gpu, dt, style, head_dim, rot_dim, heads=4, layers=3, seed=0,
         ("bf16", "neox", 80, 80),
         ("fp16", "neox", 96, 96),
         ("e4m3", "neox", 192, 192),
+        # rotary widths that are not whole vectors: the LDS kernel
+        ("bf16", "neox", 96, 24),
+        ("bf16", "neox", 80, 20),
+        ("fp16", "gptj", 80, 20),
+        ("e4m3", "neox", 128, 40),
+        ("e4m3", "gptj", 64, 24),
+        ("bf16", "neox", 256, 254),
     ],
 )
 def test_rerotate_matches_oracle(gpu, dt, style, head_dim, rot_dim):
@@ -323,10 +330,10 @@ def test_rerotate_bad_geometry_rejected(gpu):
     shape = KVShape(1, 1, 64, 16, 1)
     caches = rand_caches(shape, 2, "e4m3", gpu, seed=22)
     st = torch.zeros(shape.slot_bytes, dtype=torch.uint8, device=gpu)
-    tabs = position.delta_tables([5], 48, device=gpu)
+    tabs = position.delta_tables([5], 66, device=gpu)
     with pytest.raises(DaserKVError):
-        # neox fp8 needs rot_dim/2 to be a multiple of 16 elements
-        ops.scatter_rerotate(ops.LayerTable(caches), [0], [0], st, tabs, [0], rot_dim=48,
+        # a rotary width beyond head_dim
+        ops.scatter_rerotate(ops.LayerTable(caches), [0], [0], st, tabs, [0], rot_dim=66,
                              k_scale=torch.ones(1, device=gpu))
 
 
@@ -699,9 +706,11 @@ def _random_cases(n, seed):
         H = int(rng.choice([1, 2, 3, 4, 8]))
         bs = int(rng.choice([1, 4, 8, 16, 32]))
         style = "gptj" if rng.random() < 0.25 else "neox"
-        R = D if rng.random() < 0.75 else D // 2
+        u = rng.random()
+        R = D if u < 0.6 else D // 2 if u < 0.8 else 2 * int(rng.integers(1, D // 2 + 1))
         if (R // 2) % ve or (R % ve if style == "gptj" else 0) or ((D - R) * e) % 16:
-            continue
+            if rng.random() < 0.5:  # keep some widths for the LDS kernel, skip others
+                continue
         if (bs * H * D * e) % 16:
             continue
         cases.append((dt, D, H, bs, style, R, int(rng.integers(1, 6)), int(rng.integers(1 << 30))))
@@ -804,13 +813,17 @@ def test_random_geometry_slots_parity(gpu, dt, D, H, bs, style, R, L, seed):
     (4, 96, "bf16", None),     # row-aligned kernel
     (4, 96, "bf16", "pairs"),  # pair-task kernel
     (16, 128, "bf16", None),   # 64 KiB pages: contig kernel in rounds
+    (4, 96, "bf16", "lds24"),  # rotary width 24 of 96: the LDS kernel
 ])
 def test_rerotate_per_layer_groups(gpu, monkeypatch, heads, head_dim, dt, kernel):
     """Layers with different RoPE bases (local / global attention) and layers
     without RoPE: layer_group picks each layer's table block; group -1
     copies K. Each layer matches the oracle run with its own base."""
     print(f"case: rerotate layer groups H{heads} D{head_dim} {dt} {kernel}", flush=True)
-    if kernel:
+    rot = head_dim
+    if kernel == "lds24":
+        rot = 24
+    elif kernel:
         monkeypatch.setenv("DSR_ROT_KERNEL", kernel)
     L = 6
     groups = np.array([0, 1, -1, 0, 1, -1], np.int32)
@@ -824,13 +837,13 @@ def test_rerotate_per_layer_groups(gpu, monkeypatch, heads, head_dim, dt, kernel
     ops.gather(ops.LayerTable(src), rng.permutation(nb)[:n].astype(np.int32), offs, st)
     deltas = rng.integers(1, 32768, size=n) * (np.arange(n) % 4 != 0)  # some pages unmoved
     ridx, uniq = position.page_rope_index([1] * n, deltas)
-    tabs = torch.stack([position.delta_tables(uniq, head_dim, t, device=gpu) for t in thetas])
+    tabs = torch.stack([position.delta_tables(uniq, rot, t, device=gpu) for t in thetas])
     ks_np = (rng.random(L).astype(np.float32) * 0.5 + 0.01) if dt == "e4m3" else None
     ks = torch.from_numpy(ks_np).to(gpu) if ks_np is not None else None
     dst_ids = rng.permutation(nb)[:n].astype(np.int32)
     out = [torch.zeros_like(c) for c in src]
     ops.scatter_rerotate(ops.LayerTable(out), dst_ids, offs, st, tabs, ridx, k_scale=ks,
-                         layer_group=groups)
+                         layer_group=groups, rot_dim=rot)
     recs = st.cpu().numpy()
     d = np.asarray(deltas, np.int64)
     torch.cuda.synchronize()
@@ -838,7 +851,7 @@ def test_rerotate_per_layer_groups(gpu, monkeypatch, heads, head_dim, dt, kernel
         ref = [np.zeros_like(to_bits_np(src[l], dt))]
         g = groups[l]
         oracle.scatter_rerotate(ref, dst_ids, offs, recs, shape.layer_bytes, dtype=ORC_DT[dt],
-                                rot_dim=head_dim, style=0, stored_pos=np.zeros(n, np.int64),
+                                rot_dim=rot, style=0, stored_pos=np.zeros(n, np.int64),
                                 new_pos=d, rotate=(d != 0) & (g >= 0),
                                 theta=thetas[max(g, 0)], k_scale=ks_np, layer0=l)
         got = to_bits_np(out[l], dt)
