@@ -1,5 +1,5 @@
 // kv_rotate.h -- element codecs and the re-rotation kernels (contiguous,
-// row-aligned, pair-task and grouped).
+// row-aligned, pair-task, element-wise LDS and grouped).
 // Part of libdaser_kv: included by kv_move.hip, one translation unit.
 
 #pragma once
