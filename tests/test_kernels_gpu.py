@@ -860,3 +860,44 @@ def test_rerotate_per_layer_groups(gpu, monkeypatch, heads, head_dim, dt, kernel
             assert np.array_equal(got[0], ref[0][0]), f"no-RoPE layer {l} must be a copy"
         ok, msg = rotation_within_tolerance(got[0], ref[0][0], dt)
         assert ok, f"K layer {l} (group {g}): {msg}"
+
+
+def test_concurrent_streams_match_sequential(gpu):
+    """The entry points hold no state between calls: gathers and re-rotating
+    scatters issued on two streams at once write what the same calls write
+    one after the other."""
+    print("case: two streams", flush=True)
+    shape = KVShape(4, 8, 128, 16, 2)
+    wl = workloads.ragged(shape, 6, 200, 900, seed=15, num_blocks=512)
+    src = rand_caches(shape, wl.num_blocks, "bf16", gpu, seed=95)
+    table = ops.LayerTable(src)
+    halves = np.array_split(np.arange(wl.n_pages), 2)
+    tabs = position.delta_tables([77, 20001], 128, 500000.0, device=gpu)
+    ridx = (np.arange(wl.n_pages) % 3 - 1).astype(np.int32)
+
+    def work(dsts, outs, streams):
+        for h, (idx, s) in enumerate(zip(halves, streams)):
+            with torch.cuda.stream(s):
+                ops.gather(table, wl.page_ids[idx], wl.slot_offsets[idx], outs[h])
+                ops.scatter_rerotate(ops.LayerTable(dsts[h]), wl.page_ids[idx],
+                                     wl.slot_offsets[idx], outs[h], tabs, ridx[idx])
+
+    def fresh():
+        return ([[torch.zeros_like(c) for c in src] for _ in range(2)],
+                [torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+                 for _ in range(2)])
+
+    seq_d, seq_o = fresh()
+    cur = torch.cuda.current_stream(gpu)
+    work(seq_d, seq_o, [cur, cur])
+    torch.cuda.synchronize()
+    par_d, par_o = fresh()
+    streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
+    for s in streams:
+        s.wait_stream(cur)
+    work(par_d, par_o, streams)
+    torch.cuda.synchronize()
+    for h in range(2):
+        assert torch.equal(seq_o[h], par_o[h])
+        for a, b in zip(seq_d[h], par_d[h]):
+            assert torch.equal(a, b)
