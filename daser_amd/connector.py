@@ -437,14 +437,13 @@ class KVDataPlane:
     # -- load
     def load(self, plan: LoadPlan, batch_bytes: int = 256 << 20) -> None:
         """Reads the plan's records and scatters them. Reads are grouped into
-        batches of about ``batch_bytes``; each batch is scattered as soon as
-        it has landed, so the GPU scatters batch i while the reader rings
-        read batch i+1."""
+        batches of about ``batch_bytes`` (a read larger than that is a batch
+        of its own); each batch is scattered as soon as it has landed, so the
+        GPU scatters batch i while the reader rings read batch i+1."""
         from daser_amd import ops, position
 
         if plan.page_ids.size == 0:
             return
-        arena = torch.empty(plan.arena_bytes, dtype=torch.uint8, device=self.device)
         tabs = None
         if plan.deltas and self._layer_group is not None:
             if self._group_inv:  # [groups, tables, rot/2, 2]; layers in group -1 keep K
@@ -456,26 +455,45 @@ class KVDataPlane:
                                          inv_freq=self.inv_freq, device=self.device)
         page_read = plan.page_read if plan.page_read.size else np.zeros(plan.page_ids.size,
                                                                          np.int64)
-        first, acc = 0, 0
+        # Two batch buffers, alternating: batch k is read into buffer k % 2
+        # once the scatter that last read that buffer (batch k - 2) has run,
+        # so device staging stays near 2 * batch_bytes whatever the step
+        # loads, and reading batch k overlaps scattering batch k - 1.
+        bufs: list[Optional[torch.Tensor]] = [None, None]
+        done: list[Optional[torch.cuda.Event]] = [None, None]
+        first, acc, k = 0, 0, 0
         batch: list[tuple[int, int, int]] = []
         for r, (off, nbytes, file_off) in enumerate(plan.reads):
             batch.append((off, nbytes, file_off))
             acc += nbytes
             if acc < batch_bytes and r + 1 < len(plan.reads):
                 continue
-            self._read_batch(arena, batch)
+            base = batch[0][0]
+            size = batch[-1][0] + batch[-1][1] - base  # reads are packed back to back
+            i = k % 2
+            if done[i] is not None:
+                done[i].synchronize()
+            if bufs[i] is None or bufs[i].numel() < size:
+                bufs[i] = torch.empty(max(size, batch_bytes), dtype=torch.uint8,
+                                      device=self.device)
+            buf = bufs[i]
+            self._read_batch(buf, [(o - base, n, f) for o, n, f in batch])
             batch = []
             sel = np.nonzero((page_read >= first) & (page_read <= r))[0]
-            first, acc = r + 1, 0
+            first, acc, k = r + 1, 0, k + 1
             if sel.size == 0:
                 continue
+            src = plan.src_offsets[sel] - base
             if tabs is None:
-                ops.scatter(self.table, plan.page_ids[sel], plan.src_offsets[sel], arena)
+                ops.scatter(self.table, plan.page_ids[sel], src, buf)
             else:
-                ops.scatter_rerotate(self.table, plan.page_ids[sel], plan.src_offsets[sel],
-                                     arena, tabs, plan.rope_idx[sel], rot_dim=self.rotary_dim,
+                ops.scatter_rerotate(self.table, plan.page_ids[sel], src, buf, tabs,
+                                     plan.rope_idx[sel], rot_dim=self.rotary_dim,
                                      style=self.rope_style, k_scale=self.k_scales,
                                      layer_group=self._layer_group)
+            if self.device.type == "cuda":
+                done[i] = torch.cuda.Event()
+                done[i].record(torch.cuda.current_stream(self.device))
 
     def _read_batch(self, arena: torch.Tensor, reads: list[tuple[int, int, int]]) -> None:
         """Reads (arena_off, nbytes, file_off) ranges into the arena with the
