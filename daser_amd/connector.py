@@ -27,7 +27,9 @@ mrope), ``rope_layers`` (per model layer: None for no RoPE, or
 read from ``vllm_config.model_config.hf_config`` when not given,
 ``save_mode`` ("per_layer" | "deferred": one all-layer gather in
 wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry), ``io_readers``
-(rings reading a load in parallel, default 4),
+(rings reading a load in parallel, default 4), ``io_timeout_s`` (a blocking
+store read or write raises TimeoutError after this long, default 120 as in
+the reference; None: wait forever),
 ``io_backend`` ("native": the C++ io_uring ring of libdaser_kv, default;
 "direct": the same ring with the store file opened O_DIRECT;
 "python": the threaded ring of store_io.PinnedRingIO), ``k_scale`` (one K
@@ -222,7 +224,8 @@ class KVDataPlane:
                  io_slot_bytes: int = 4 << 20, io_slots: int = 8,
                  io_backend: str = "native", save_stream: str = "side",
                  k_scales: Optional[torch.Tensor] = None, io_readers: int = 4,
-                 layer_rope: Optional[list] = None) -> None:
+                 layer_rope: Optional[list] = None,
+                 io_timeout: Optional[float] = 120.0) -> None:
         if save_mode not in ("per_layer", "deferred"):
             raise ValueError("save_mode must be 'per_layer' or 'deferred'")
         if io_backend not in ("native", "direct", "python"):
@@ -257,6 +260,8 @@ class KVDataPlane:
         self._writer = None  # background writer of flush_async, with its own ring
         self._wio = None
         self._io_readers = max(1, int(io_readers))  # parallel rings of load()
+        self.io_timeout = io_timeout  # seconds a blocking transfer may take (None: no limit)
+        self._sync_pool = None
         self._reader_pool = None
         self._readers: list = []
         self._idle_stream: Optional[torch.cuda.Stream] = None
@@ -427,12 +432,41 @@ class KVDataPlane:
     def flush(self, plan: StorePlan, arena: torch.Tensor) -> list[str]:
         """Writes each request's records at its file offset; returns the
         chunk keys written (to commit)."""
-        keys = []
-        producer = self._side  # None: the current stream
-        for key, off, nbytes, file_off in plan.transfers:
-            self.io.write_from_device(arena[off:off + nbytes], file_off, producer)
-            keys.append(key)
+        keys: list[str] = []
+        producer = self._side
+        if producer is None and self.device.type == "cuda":
+            producer = torch.cuda.current_stream(self.device)  # resolved on this thread
+
+        def run() -> None:
+            for key, off, nbytes, file_off in plan.transfers:
+                self.io.write_from_device(arena[off:off + nbytes], file_off, producer)
+                keys.append(key)
+
+        self._io_call(run, "store write")
         return keys
+
+    def _io_call(self, fn, what: str) -> None:
+        """Runs a blocking store transfer; with io_timeout set it runs on a
+        helper thread and raises TimeoutError if it does not return in time
+        (the reference's worker I/O waits 120 s, daser_connector.py:526-528,
+        670-672)."""
+        if self.io_timeout is None:
+            fn()
+            return
+        if self._sync_pool is None:
+            from concurrent.futures import ThreadPoolExecutor
+
+            self._sync_pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="daser-sync")
+        self._wait(self._sync_pool.submit(fn), what)
+
+    def _wait(self, fut, what: str) -> None:
+        from concurrent.futures import TimeoutError as FutTimeout
+
+        try:
+            fut.result(timeout=self.io_timeout)
+        except FutTimeout:
+            raise TimeoutError(f"{what} did not finish within {self.io_timeout} s "
+                               f"({self.store_path})") from None
 
     # -- load
     def load(self, plan: LoadPlan, batch_bytes: int = 256 << 20) -> None:
@@ -505,8 +539,11 @@ class KVDataPlane:
                  for k in range(0, n, piece)]
         consumer = torch.cuda.current_stream(self.device) if self.device.type == "cuda" else None
         if self._io_readers <= 1 or len(parts) == 1:
-            for o, n, f in parts:
-                self.io.read_into_device(arena[o:o + n], f, consumer)
+            def run_one() -> None:
+                for o, n, f in parts:
+                    self.io.read_into_device(arena[o:o + n], f, consumer)
+
+            self._io_call(run_one, "store read")
             return
         if self._reader_pool is None:
             from concurrent.futures import ThreadPoolExecutor
@@ -522,10 +559,13 @@ class KVDataPlane:
                 ring.read_into_device(arena[o:o + n], f, consumer)
 
         for fut in [self._reader_pool.submit(run, i) for i in range(len(self._readers))]:
-            fut.result()
+            self._wait(fut, "store read")
 
     def close(self) -> None:
         self.drain()
+        if self._sync_pool is not None:
+            self._sync_pool.shutdown(wait=False)
+            self._sync_pool = None
         if self._reader_pool is not None:
             self._reader_pool.shutdown(wait=True)
             self._reader_pool = None
@@ -620,6 +660,7 @@ class DaserConnector(KVConnectorBase_V1):
                 io_slot_bytes=int(float(extra.get("io_slot_mb", 4)) * (1 << 20)),
                 io_slots=int(extra.get("io_slots", 8)),
                 io_readers=int(extra.get("io_readers", 4)),
+                io_timeout=extra.get("io_timeout_s", 120.0),
                 io_backend=extra.get("io_backend", "native"),
                 save_stream=extra.get("save_stream", "side"),
             )

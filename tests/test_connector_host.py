@@ -328,3 +328,40 @@ def test_uint8_fp8_cache_viewed_as_e4m3(tmp_path, cache_dtype, expect):
     w.register_kv_caches({"model.layers.0.self_attn.attn": t})
     assert str(w._plane.table.layout.dtype) == f"torch.{expect}"
     w.shutdown()
+
+
+def test_stalled_store_io_times_out(tmp_path):
+    """A store write or read that does not return raises TimeoutError after
+    io_timeout (the reference's worker I/O waits 120 s), forced here with a
+    ring whose file writes stall."""
+    import threading
+    import time
+
+    import torch
+
+    from daser_amd import connector as C
+    from daser_amd.store_io import PinnedRingIO
+
+    release = threading.Event()
+
+    def stall(kind, n, off):
+        release.wait(5.0)
+
+    caches = {f"model.layers.{i}.self_attn.attn": torch.zeros(2, 8, 16, 1, 64,
+                                                              dtype=torch.bfloat16)
+              for i in range(2)}
+    p = C.KVDataPlane(str(tmp_path / "s"), io_backend="python", io_timeout=0.3, io_readers=1)
+    slot = p.register(caches)
+    p.io.close()
+    p.io = PinnedRingIO(p.store_path, "cpu", slot_bytes=4096, n_slots=2, io_hook=stall)
+    plan = C.plan_store({"r": C.ReqStoreSpec("k", 0, 2, [1, 3], 0, 32)}, slot)
+    arena = p.new_store_arena(plan)
+    t0 = time.monotonic()
+    with pytest.raises(TimeoutError, match="store write"):
+        p.flush(plan, arena)
+    assert time.monotonic() - t0 < 3.0
+    lp = C.plan_load({"r": C.ReqLoadSpec("k", 0, 2, [1, 3], 0, 32)}, slot)
+    with pytest.raises(TimeoutError, match="store read"):
+        p.load(lp)
+    release.set()
+    p.close()
