@@ -1,0 +1,477 @@
+"""MI355X data plane of the DaseR connector: per-step plans (which pages
+move where) and ``KVDataPlane``, which owns the layer table of vLLM's caches,
+the staging buffers and the store I/O rings, and runs the HIP kernels of
+libdaser_kv on torch's current stream.
+
+The connector (daser_amd.connector.DaserConnector) keeps the reference's
+interface and calls into this module from its worker hooks; the plans
+restate the reference's record layout (daser/connector/daser_connector.py:
+498-551 load, 610-684 save).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import TYPE_CHECKING, Optional
+
+import numpy as np
+import torch
+
+if TYPE_CHECKING:  # the request specs live with the connector's metadata
+    from daser_amd.connector import ReqLoadSpec, ReqStoreSpec
+
+
+# ---------------------------------------------------------------------------
+# planning (host side, no device work): which pages move where
+
+
+@dataclass
+class StorePlan:
+    """Pages of every store request packed back to back in one arena."""
+
+    page_ids: np.ndarray  # int32 block ids
+    slot_offsets: np.ndarray  # int64 record offsets in the arena
+    transfers: list[tuple[str, int, int, int]]  # (chunk_key, arena_off, nbytes, file_off)
+    arena_bytes: int
+    device_tables: Optional[tuple] = None  # (page_ids, slot_offsets) on the device
+
+
+@dataclass
+class LoadPlan:
+    """Records read into one arena, then scattered into pages."""
+
+    page_ids: np.ndarray
+    src_offsets: np.ndarray
+    rope_idx: np.ndarray  # int32, -1 = no rotation
+    deltas: list[int]  # table order
+    reads: list[tuple[int, int, int]]  # (arena_off, nbytes, file_off)
+    arena_bytes: int
+    page_read: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int64))  # read of each page
+
+
+def plan_store(reqs: dict[str, ReqStoreSpec], slot_bytes: int) -> StorePlan:
+    """Record of request r's slot i at arena_r + i * SLOT, written to the file
+    at start_slot * SLOT (reference :616-632, :652)."""
+    ids, transfers = [], []
+    base = 0
+    for spec in reqs.values():
+        n = len(spec.block_ids)
+        if n == 0:
+            continue
+        ids.extend(spec.block_ids)
+        transfers.append((spec.chunk_key, base, n * slot_bytes, spec.start_slot * slot_bytes))
+        base += n * slot_bytes
+    # records are packed back to back: page k of the step at k * SLOT
+    offs = np.arange(len(ids), dtype=np.int64) * slot_bytes
+    return StorePlan(np.asarray(ids, np.int32), offs, transfers, base)
+
+
+def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
+    """Each segment's records are read once into the arena; page j of a
+    segment scatters record j into block_ids[block_offset + j]. A segment
+    whose new position differs from its stored one gets a rotation table for
+    delta = new_pos - pos_offset (reference :498-551 for the unrotated part)."""
+    ids: list[int] = []
+    seg_pages, seg_table, reads = [], [], []
+    table: dict[int, int] = {}
+    base = 0
+    for spec in reqs.values():
+        blocks = spec.block_ids
+        if not blocks:
+            continue
+        for seg in spec.resolved_segments():
+            n = seg.num_slots
+            if n <= 0:
+                continue
+            if seg.block_offset < 0 or seg.block_offset + n > len(blocks):
+                raise ValueError(f"segment of {spec.chunk_key[:8]} exceeds its block list")
+            reads.append((base, n * slot_bytes, seg.start_slot * slot_bytes))
+            delta = 0 if seg.new_pos is None else int(seg.new_pos) - int(seg.pos_offset)
+            seg_table.append(-1 if delta == 0 else table.setdefault(delta, len(table)))
+            seg_pages.append(n)
+            ids.extend(blocks[seg.block_offset:seg.block_offset + n])
+            base += n * slot_bytes
+    # segments' records are packed back to back: page k at k * SLOT
+    counts = np.asarray(seg_pages, np.int64)
+    return LoadPlan(np.asarray(ids, np.int32),
+                    np.arange(len(ids), dtype=np.int64) * slot_bytes,
+                    np.repeat(np.asarray(seg_table, np.int32), counts), list(table.keys()),
+                    reads, base, np.repeat(np.arange(len(reads), dtype=np.int64), counts))
+
+
+# ---------------------------------------------------------------------------
+# worker data plane
+
+
+class KVDataPlane:
+    """Worker-side movement of KV pages between vLLM's caches and the store.
+
+    Owns the layer table of the registered caches, the per-step staging
+    arenas and the store I/O; every device operation is enqueued on torch's
+    current stream of the caches' device.
+    """
+
+    def __init__(self, store_path: str, *, rope_theta: float = 10000.0,
+                 rope_style: str = "neox", rotary_dim: Optional[int] = None,
+                 inv_freq: Optional[np.ndarray] = None, rope_scaling: Optional[dict] = None,
+                 save_mode: str = "per_layer",
+                 io_slot_bytes: int = 4 << 20, io_slots: int = 8,
+                 io_backend: str = "native", save_stream: str = "side",
+                 k_scales: Optional[torch.Tensor] = None, io_readers: int = 4,
+                 layer_rope: Optional[list] = None,
+                 io_timeout: Optional[float] = 120.0) -> None:
+        if save_mode not in ("per_layer", "deferred"):
+            raise ValueError("save_mode must be 'per_layer' or 'deferred'")
+        if io_backend not in ("native", "direct", "python"):
+            raise ValueError("io_backend must be 'native', 'direct' or 'python'")
+        if save_stream not in ("side", "current"):
+            raise ValueError("save_stream must be 'side' or 'current'")
+        self.io_backend = io_backend
+        self.save_stream = save_stream
+        self._side: Optional[torch.cuda.Stream] = None
+        self.store_path = store_path
+        self.rope_theta = float(rope_theta)
+        self.rope_style = rope_style
+        self.rotary_dim = rotary_dim
+        self.inv_freq = inv_freq
+        self.rope_scaling = rope_scaling
+        # per model layer: None (no RoPE) or {"rope_theta", "rope_scaling"}
+        self.layer_rope = layer_rope
+        self._layer_group: Optional[torch.Tensor] = None
+        self._group_inv: list[np.ndarray] = []
+        if rope_scaling and inv_freq is None:
+            from daser_amd.position import inv_freq_for
+
+            # Unsupported scalings fail here, not at the first load.
+            probe_dim = int(rotary_dim) if rotary_dim else 2
+            scaled = inv_freq_for(rope_scaling, probe_dim, rope_theta)
+            if rotary_dim:
+                self.inv_freq = scaled
+        self.save_mode = save_mode
+        self._io_slot_bytes = io_slot_bytes
+        self._io_slots = io_slots
+        self.k_scales = k_scales
+        self._writer = None  # background writer of flush_async, with its own ring
+        self._wio = None
+        self._io_readers = max(1, int(io_readers))  # parallel rings of load()
+        self.io_timeout = io_timeout  # seconds a blocking transfer may take (None: no limit)
+        self._sync_pool = None
+        self._reader_pool = None
+        self._readers: list = []
+        self._idle_stream: Optional[torch.cuda.Stream] = None
+        self._pending_writes: list = []
+        self.table = None
+        self.layer_names: list[str] = []
+        self.layer_idx: dict[str, int] = {}
+        self.slot_bytes = 0
+        self.io = None
+
+    # -- registration (reference register_kv_caches :383-429)
+    def register(self, kv_caches: dict[str, torch.Tensor], slot_size: int = 0) -> int:
+        from daser_amd import ops
+        from daser_amd.store_io import preallocate_store
+
+        self.layer_names = list(kv_caches.keys())
+        self.layer_idx = {n: i for i, n in enumerate(self.layer_names)}
+        self.table = ops.LayerTable([kv_caches[n] for n in self.layer_names])
+        lay = self.table.layout
+        derived = lay.slot_bytes
+        if slot_size and slot_size != derived:
+            raise ValueError(f"configured slot_size {slot_size} != derived {derived}")
+        self.slot_bytes = derived
+        if self.rotary_dim is None:
+            self.rotary_dim = lay.head_dim
+        if self.inv_freq is None and self.rope_scaling:
+            from daser_amd.position import inv_freq_for
+
+            self.inv_freq = inv_freq_for(self.rope_scaling, self.rotary_dim, self.rope_theta)
+        if self.layer_rope is not None:
+            self._register_layer_rope()
+        preallocate_store(self.store_path, max(self.slot_bytes * 1024, 64 << 20))
+        if self.save_stream == "side" and lay.device.type == "cuda" and self._side is None:
+            self._side = torch.cuda.Stream(lay.device)  # default priority
+        if self.io_backend == "direct" and self.slot_bytes % 4096:
+            raise ValueError("io_backend='direct' needs a slot record size that is a "
+                             "multiple of 4096 bytes")
+        if self.io is None:
+            self.io = self._open_ring(lay.device)
+        return self.slot_bytes
+
+    def _register_layer_rope(self) -> None:
+        """Groups of layers sharing RoPE frequencies (layer_rope is indexed
+        by the model's layer number, read from names like
+        "model.layers.12.self_attn.attn", else by registration order)."""
+        import re
+
+        from daser_amd.position import layer_rope_groups
+
+        specs = []
+        for pos, name in enumerate(self.layer_names):
+            m = re.search(r"layers\.(\d+)\.", name)
+            idx = int(m.group(1)) if m else pos
+            if idx >= len(self.layer_rope):
+                raise ValueError(f"layer_rope has no entry for layer {idx} ({name})")
+            specs.append(self.layer_rope[idx])
+        groups, invs = layer_rope_groups(specs, self.rotary_dim, self.rope_theta)
+        if len(invs) == 1 and (groups >= 0).all():
+            self.inv_freq = invs[0]  # one RoPE after all: the single-table path
+            return
+        self._group_inv = invs
+        self._layer_group = torch.from_numpy(groups).to(self.table.layout.device)
+
+    def _open_ring(self, device: torch.device):
+        from daser_amd.store_io import NativeRingIO, PinnedRingIO
+
+        if self.io_backend == "python":
+            return PinnedRingIO(self.store_path, device, slot_bytes=self._io_slot_bytes,
+                                n_slots=self._io_slots)
+        return NativeRingIO(self.store_path, device, slot_bytes=self._io_slot_bytes,
+                            n_slots=self._io_slots, direct=self.io_backend == "direct")
+
+    @property
+    def device(self) -> torch.device:
+        return self.table.layout.device
+
+    # -- save
+    def new_store_arena(self, plan: StorePlan) -> torch.Tensor:
+        """Staging arena of a step's store requests. The plan's page tables are
+        validated and uploaded once here and reused by every layer's gather."""
+        from daser_amd import ops
+
+        arena = torch.empty(max(plan.arena_bytes, 16), dtype=torch.uint8, device=self.device)
+        if plan.page_ids.size:
+            ops._validate(self.table.layout, plan.page_ids, plan.slot_offsets, arena, 0,
+                          self.table.layout.num_layers, True)
+            plan.device_tables = (torch.from_numpy(plan.page_ids).to(self.device),
+                                  torch.from_numpy(plan.slot_offsets).to(self.device))
+        return arena
+
+    def _on_save_stream(self, arena: torch.Tensor):
+        """Context for the gathers: the side stream, ordered after the work
+        the model's stream has enqueued so far (the layer's KV writes)."""
+        import contextlib
+
+        if self._side is None:
+            return contextlib.nullcontext()
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        self._side.wait_event(ev)
+        arena.record_stream(self._side)
+        return torch.cuda.stream(self._side)
+
+    def save_layer(self, layer_name: str, plan: StorePlan, arena: torch.Tensor) -> None:
+        """Gathers one layer's pages of every store request. With
+        save_stream="side" the gather runs on a side stream after the KV
+        writes already enqueued, overlapping the model's later layers."""
+        from daser_amd import ops
+
+        if plan.page_ids.size == 0:
+            return
+        l = self.layer_idx[layer_name]
+        ids, offs = plan.device_tables
+        with self._on_save_stream(arena):
+            ops.gather(self.table, ids, offs, arena, layers=(l, 1))
+
+    def save_all(self, plan: StorePlan, arena: torch.Tensor) -> None:
+        from daser_amd import ops
+
+        if plan.page_ids.size == 0:
+            return
+        ids, offs = plan.device_tables
+        with self._on_save_stream(arena):
+            ops.gather(self.table, ids, offs, arena)
+
+    def flush_async(self, plan: StorePlan, arena: torch.Tensor, done) -> None:
+        """Like flush, but the file writes run on a background writer thread
+        (one, so steps are written in order) and this returns at once. The
+        current stream is first ordered after the step's gathers, so vLLM may
+        reuse the cache blocks as soon as the gathers have run; the arena
+        keeps the records until they are written. ``done(keys, error)`` is
+        called on the writer thread with the chunk keys fully written (all
+        of them unless ``error``)."""
+        from concurrent.futures import ThreadPoolExecutor
+
+        cur = torch.cuda.current_stream(self.device)
+        ev = torch.cuda.Event()
+        ev.record(self._side if self._side is not None else cur)
+        if self._side is not None:
+            cur.wait_event(ev)
+        if self._writer is None:
+            self._writer = ThreadPoolExecutor(max_workers=1, thread_name_prefix="daser-save")
+            self._idle_stream = torch.cuda.Stream(self.device)  # never given work
+            # its own ring: a load (start_load_kv) never waits behind a write
+            self._wio = self._open_ring(self.table.layout.device)
+
+        def job() -> None:
+            keys: list[str] = []
+            err: Optional[BaseException] = None
+            try:
+                ev.synchronize()  # the gathers into this arena have run
+                for key, off, nbytes, file_off in plan.transfers:
+                    self._wio.write_from_device(arena[off:off + nbytes], file_off,
+                                                self._idle_stream)
+                    keys.append(key)
+            except BaseException as e:  # reported, never lost on the thread
+                err = e
+            done(keys, err)
+
+        self._pending_writes.append(self._writer.submit(job))
+
+    def drain(self, timeout: Optional[float] = None) -> None:
+        """Waits for every write started by flush_async."""
+        pending, self._pending_writes = self._pending_writes, []
+        for f in pending:
+            f.result(timeout=timeout)
+
+    def flush(self, plan: StorePlan, arena: torch.Tensor) -> list[str]:
+        """Writes each request's records at its file offset; returns the
+        chunk keys written (to commit)."""
+        keys: list[str] = []
+        producer = self._side
+        if producer is None and self.device.type == "cuda":
+            producer = torch.cuda.current_stream(self.device)  # resolved on this thread
+
+        def run() -> None:
+            for key, off, nbytes, file_off in plan.transfers:
+                self.io.write_from_device(arena[off:off + nbytes], file_off, producer)
+                keys.append(key)
+
+        self._io_call(run, "store write")
+        return keys
+
+    def _io_call(self, fn, what: str) -> None:
+        """Runs a blocking store transfer; with io_timeout set it runs on a
+        helper thread and raises TimeoutError if it does not return in time
+        (the reference's worker I/O waits 120 s, daser_connector.py:526-528,
+        670-672)."""
+        if self.io_timeout is None:
+            fn()
+            return
+        if self._sync_pool is None:
+            from concurrent.futures import ThreadPoolExecutor
+
+            self._sync_pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="daser-sync")
+        self._wait(self._sync_pool.submit(fn), what)
+
+    def _wait(self, fut, what: str) -> None:
+        from concurrent.futures import TimeoutError as FutTimeout
+
+        try:
+            fut.result(timeout=self.io_timeout)
+        except FutTimeout:
+            raise TimeoutError(f"{what} did not finish within {self.io_timeout} s "
+                               f"({self.store_path})") from None
+
+    # -- load
+    def load(self, plan: LoadPlan, batch_bytes: int = 256 << 20) -> None:
+        """Reads the plan's records and scatters them. Reads are grouped into
+        batches of about ``batch_bytes`` (a read larger than that is a batch
+        of its own); each batch is scattered as soon as it has landed, so the
+        GPU scatters batch i while the reader rings read batch i+1."""
+        from daser_amd import ops, position
+
+        if plan.page_ids.size == 0:
+            return
+        tabs = None
+        if plan.deltas and self._layer_group is not None:
+            if self._group_inv:  # [groups, tables, rot/2, 2]; layers in group -1 keep K
+                tabs = torch.stack([position.delta_tables(plan.deltas, self.rotary_dim,
+                                                          inv_freq=inv, device=self.device)
+                                    for inv in self._group_inv])
+        elif plan.deltas:
+            tabs = position.delta_tables(plan.deltas, self.rotary_dim, self.rope_theta,
+                                         inv_freq=self.inv_freq, device=self.device)
+        page_read = plan.page_read if plan.page_read.size else np.zeros(plan.page_ids.size,
+                                                                         np.int64)
+        # Two batch buffers, alternating: batch k is read into buffer k % 2
+        # once the scatter that last read that buffer (batch k - 2) has run,
+        # so device staging stays near 2 * batch_bytes whatever the step
+        # loads, and reading batch k overlaps scattering batch k - 1.
+        bufs: list[Optional[torch.Tensor]] = [None, None]
+        done: list[Optional[torch.cuda.Event]] = [None, None]
+        first, acc, k = 0, 0, 0
+        batch: list[tuple[int, int, int]] = []
+        for r, (off, nbytes, file_off) in enumerate(plan.reads):
+            batch.append((off, nbytes, file_off))
+            acc += nbytes
+            if acc < batch_bytes and r + 1 < len(plan.reads):
+                continue
+            base = batch[0][0]
+            size = batch[-1][0] + batch[-1][1] - base  # reads are packed back to back
+            i = k % 2
+            if done[i] is not None:
+                done[i].synchronize()
+            if bufs[i] is None or bufs[i].numel() < size:
+                bufs[i] = torch.empty(max(size, batch_bytes), dtype=torch.uint8,
+                                      device=self.device)
+            buf = bufs[i]
+            self._read_batch(buf, [(o - base, n, f) for o, n, f in batch])
+            batch = []
+            sel = np.nonzero((page_read >= first) & (page_read <= r))[0]
+            first, acc, k = r + 1, 0, k + 1
+            if sel.size == 0:
+                continue
+            src = plan.src_offsets[sel] - base
+            if tabs is None:
+                ops.scatter(self.table, plan.page_ids[sel], src, buf)
+            else:
+                ops.scatter_rerotate(self.table, plan.page_ids[sel], src, buf, tabs,
+                                     plan.rope_idx[sel], rot_dim=self.rotary_dim,
+                                     style=self.rope_style, k_scale=self.k_scales,
+                                     layer_group=self._layer_group)
+            if self.device.type == "cuda":
+                done[i] = torch.cuda.Event()
+                done[i].record(torch.cuda.current_stream(self.device))
+
+    def _read_batch(self, arena: torch.Tensor, reads: list[tuple[int, int, int]]) -> None:
+        """Reads (arena_off, nbytes, file_off) ranges into the arena with the
+        reader rings in parallel (page-cache reads measured 15-18 GB/s on
+        one ring, 32-37 GB/s on four), in pieces of at most 16 MiB. On
+        return the current stream is ordered after every copy."""
+        piece = 16 << 20  # a multiple of 4 KiB: O_DIRECT reads stay aligned
+        parts = [(o + k, min(piece, n - k), f + k) for o, n, f in reads
+                 for k in range(0, n, piece)]
+        consumer = torch.cuda.current_stream(self.device) if self.device.type == "cuda" else None
+        if self._io_readers <= 1 or len(parts) == 1:
+            def run_one() -> None:
+                for o, n, f in parts:
+                    self.io.read_into_device(arena[o:o + n], f, consumer)
+
+            self._io_call(run_one, "store read")
+            return
+        if self._reader_pool is None:
+            from concurrent.futures import ThreadPoolExecutor
+
+            self._readers = [self.io] + [self._open_ring(self.device)
+                                         for _ in range(self._io_readers - 1)]
+            self._reader_pool = ThreadPoolExecutor(max_workers=self._io_readers,
+                                                   thread_name_prefix="daser-load")
+
+        def run(i: int) -> None:
+            ring = self._readers[i]
+            for o, n, f in parts[i::len(self._readers)]:
+                ring.read_into_device(arena[o:o + n], f, consumer)
+
+        for fut in [self._reader_pool.submit(run, i) for i in range(len(self._readers))]:
+            self._wait(fut, "store read")
+
+    def close(self) -> None:
+        self.drain()
+        if self._sync_pool is not None:
+            self._sync_pool.shutdown(wait=False)
+            self._sync_pool = None
+        if self._reader_pool is not None:
+            self._reader_pool.shutdown(wait=True)
+            self._reader_pool = None
+            for ring in self._readers[1:]:
+                ring.close()
+            self._readers = []
+        if self._writer is not None:
+            self._writer.shutdown(wait=True)
+            self._writer = None
+        if self._wio is not None:
+            self._wio.close()
+            self._wio = None
+        if self.io is not None:
+            self.io.close()
+            self.io = None
