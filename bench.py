@@ -347,6 +347,149 @@ def bench_io(torch, dev, budget_bytes: int = 2 << 30, reps: int = 3) -> dict:
                       f"best of {reps}, store file under {tempfile.gettempdir()}"}
 
 
+class _BenchIPC:
+    """Stands in for the store server's async client: commits succeed."""
+
+    async def commit_chunk(self, key):
+        return {"ok": True}
+
+
+def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int = 16,
+                  hit_pages: int = 128) -> dict:
+    """Host cost and latency of the connector's worker hooks on serving-shaped
+    steps at config 2's shape (Llama-3-8B bf16), through DaserConnector with
+    the native ring and a store file under $TMPDIR:
+    save step = bind metadata, save_kv_layer for each of the 32 layers, then
+    wait_for_save, for n_req requests storing one 256-token chunk each
+    (blocking and async_save);
+    load step = start_load_kv of n_req requests hitting hit_pages pages each,
+    placed at a new position (fused re-rotation), until the device is done.
+    Beside it, the reference's per-(page, layer) copy loops for the same
+    pages (daser_connector.py:625-632 and :536-551) on the same GPU."""
+    import shutil
+    import tempfile
+    from types import SimpleNamespace
+
+    from daser_amd import connector as C
+    from daser_amd import workloads
+    from daser_amd.store_io import preallocate_store
+
+    shape = workloads.LLAMA3_8B
+    nb = n_req * hit_pages + 64
+    full, caches, _ = fill_caches(torch, shape, nb, "bf16", dev, seed=11)
+    named = {f"model.layers.{i}.self_attn.attn": c for i, c in enumerate(caches)}
+    rng = np.random.default_rng(5)
+    d = tempfile.mkdtemp(prefix="daser_serving_")
+    store = os.path.join(d, "daser.store")
+    slot = shape.slot_bytes
+    preallocate_store(store, n_req * hit_pages * slot)
+    with open(store, "r+b") as f:  # loads read written records, not file holes
+        piece = np.random.default_rng(6).integers(0, 256, 1 << 24, dtype=np.uint8).tobytes()
+        for _ in range(n_req * hit_pages * slot // len(piece)):
+            f.write(piece)
+    out = {}
+
+    def worker(**extra):
+        cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(kv_connector_extra_config=dict(
+            store_path=store, rope_theta=500000.0, **extra)))
+        w = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=_BenchIPC())
+        w.register_kv_caches(named)
+        return w
+
+    def store_meta():
+        blocks = rng.permutation(nb)[:n_req * chunk_pages].tolist()
+        reqs = {}
+        for r in range(n_req):
+            s0 = r * chunk_pages
+            reqs[f"s{r}"] = C.ReqStoreSpec(f"k{r}", s0, chunk_pages,
+                                           blocks[s0:s0 + chunk_pages], s0 * slot,
+                                           chunk_pages * 16)
+        return C.DaserConnectorMeta(reqs_to_store=reqs)
+
+    try:
+        for mode in ("blocking", "async_save"):
+            w = worker(async_save=mode == "async_save")
+            hook_us, wait_ms, step_ms = [], [], []
+            for it in range(steps + 1):
+                meta = store_meta()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                w.bind_connector_metadata(meta)
+                for name, t in named.items():
+                    h0 = time.perf_counter()
+                    w.save_kv_layer(name, t, None)
+                    hook_us.append((time.perf_counter() - h0) * 1e6)
+                h1 = time.perf_counter()
+                w.wait_for_save()
+                t1 = time.perf_counter()
+                w.clear_connector_metadata()
+                if it:  # the first step opens the rings
+                    wait_ms.append((t1 - h1) * 1e3)
+                    step_ms.append((t1 - t0) * 1e3)
+                else:
+                    hook_us.clear()
+            w._plane.drain(timeout=120.0)
+            w.shutdown()
+            out[f"save_{mode}"] = {
+                "save_kv_layer_host_us_median": round(float(np.median(hook_us)), 1),
+                "wait_for_save_ms_median": round(float(np.median(wait_ms)), 3),
+                "step_ms_median": round(float(np.median(step_ms)), 3),
+                "bytes_per_step": n_req * chunk_pages * slot}
+
+        w = worker()
+        load_ms = []
+        for it in range(steps + 1):
+            blocks = rng.permutation(nb)[:n_req * hit_pages].tolist()
+            reqs = {}
+            for r in range(n_req):
+                s0 = r * hit_pages
+                reqs[f"l{r}"] = C.ReqLoadSpec(f"k{r}", s0, hit_pages, blocks[s0:s0 + hit_pages],
+                                              s0 * slot, hit_pages * 16, pos_offset=0,
+                                              new_pos=int(rng.integers(1, 32768)))
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            w.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_load=reqs))
+            w.start_load_kv(None)
+            torch.cuda.synchronize()
+            if it:
+                load_ms.append((time.perf_counter() - t0) * 1e3)
+            w.clear_connector_metadata()
+        w.shutdown()
+        lb = n_req * hit_pages * slot
+        out["load_rerotate"] = {"start_load_kv_ms_median": round(float(np.median(load_ms)), 3),
+                                "GBps_file_inclusive": round(lb / np.median(load_ms) / 1e6, 2),
+                                "bytes_per_step": lb}
+
+        # the reference's loops for the same step sizes (device copies only, no I/O)
+        layer = shape.layer_bytes
+        pages = rng.permutation(nb)[:n_req * chunk_pages].tolist()
+        staging = torch.empty(len(pages) * slot, dtype=torch.uint8, device=dev)
+
+        def ref_save():
+            for l, t in enumerate(caches):  # one save_kv_layer per layer
+                for i, b in enumerate(pages):
+                    src = t[:, b]
+                    o = i * slot + l * layer
+                    staging[o:o + src.nbytes].copy_(src.reshape(-1).view(torch.uint8))
+
+        ref_save()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            ref_save()
+        torch.cuda.synchronize()
+        out["reference_save_loop_ms"] = round((time.perf_counter() - t0) / 3 * 1e3, 3)
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+        del full, caches, named
+        torch.cuda.empty_cache()
+    out["sample"] = (f"{steps} steps each after one warm-up; save: {n_req} requests x "
+                     f"{chunk_pages} pages (256 tokens); load: {n_req} requests x {hit_pages} "
+                     f"pages re-rotated to new positions; store file under "
+                     f"{tempfile.gettempdir()} (page cache)")
+    return out
+
+
 def reference_loop(torch, dev, budget_s: float = 6.0) -> dict:
     """The reference's own copy path, timed on `dev` (the GPU, or "cpu"):
     save = for each page, for each layer,
@@ -499,6 +642,9 @@ def main() -> int:
     ap.add_argument("--io", action="store_true",
                     help="also time the PCIe/file-inclusive save and load of the "
                          "connector's data plane on a 2 GiB sample")
+    ap.add_argument("--serving", action="store_true",
+                    help="also time the connector's worker hooks on serving-shaped "
+                         "steps (host cost per hook, save and load latency)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 4 GiB device copy (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -604,7 +750,7 @@ def main() -> int:
                            "tokens": r["tokens"], "payload_bytes": r["payload_bytes"],
                            "traffic_rerotate": pmc_traffic("kv_scatter_rerotate_contig_kernel", 4,
                                                            r["pages"])}
-    if "value" not in out:
+    if "value" not in out and configs:
         r = res[configs[0]]
         out.update({"value": round(r.get("tokens_per_s", 0.0)), "unit": "tokens/s",
                     "ms_per_step": round(r.get("kernel_ms", 0.0), 3), "dtype": "bf16",
@@ -613,6 +759,10 @@ def main() -> int:
         log("[bench] io: PCIe/file-inclusive save and load")
         out["pcie_inclusive"] = bench_io(torch, dev)
         log(f"[bench] io: {json.dumps(out['pcie_inclusive'])}")
+    if args.serving:
+        log("[bench] serving: connector worker hooks per step")
+        out["serving"] = bench_serving(torch, dev)
+        log(f"[bench] serving: {json.dumps(out['serving'])}")
     if not args.no_ref_loop:
         log("[bench] reference copy loop on the GPU")
         out["reference_loop_gpu"] = reference_loop(torch, dev)

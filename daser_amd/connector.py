@@ -39,7 +39,9 @@ the gathers are enqueued and ordered before the next step's KV writes; file
 writes and commits finish on a background writer; default False, the
 reference's blocking behaviour), ``save_stream``
 ("side": per-layer gathers on a side stream after the layer's KV writes,
-overlapping later layers, default; "current": on the model's stream).
+overlapping later layers; "current": on the model's stream; "auto", default:
+the side stream when one layer's gather moves at least 32 MiB, else the
+model's stream, where a small gather costs less than ordering a side stream).
 """
 
 from __future__ import annotations
@@ -218,7 +220,7 @@ class DaserConnector(KVConnectorBase_V1):
                 io_readers=int(extra.get("io_readers", 4)),
                 io_timeout=extra.get("io_timeout_s", 120.0),
                 io_backend=extra.get("io_backend", "native"),
-                save_stream=extra.get("save_stream", "side"),
+                save_stream=extra.get("save_stream", "auto"),
             )
             self._k_scale_cfg = extra.get("k_scale")  # uniform fp8 K scale, optional
             self._async_save = bool(extra.get("async_save", False))
@@ -376,6 +378,7 @@ class DaserConnector(KVConnectorBase_V1):
         if self._store_plan is None:
             self._store_plan = plan_store(self._meta.reqs_to_store, self._slot_size)
             self._store_arena = self._plane.new_store_arena(self._store_plan)
+            self._pending_commits.update(s.chunk_key for s in self._meta.reqs_to_store.values())
         return True
 
     def save_kv_layer(self, layer_name: str, kv_layer: torch.Tensor, attn_metadata: Any,
@@ -383,8 +386,6 @@ class DaserConnector(KVConnectorBase_V1):
         """Enqueues this layer's gather for every store request."""
         if not self._ensure_store_plan():
             return
-        for spec in self._meta.reqs_to_store.values():
-            self._pending_commits.add(spec.chunk_key)
         if layer_name not in self._plane.layer_idx:
             logger.warning("[CONNECTOR] save_kv_layer: unknown layer %s, skipping", layer_name)
             return
@@ -399,8 +400,6 @@ class DaserConnector(KVConnectorBase_V1):
         record is written with unset bytes."""
         if self._flushed or not self._ensure_store_plan():
             return
-        for spec in self._meta.reqs_to_store.values():
-            self._pending_commits.add(spec.chunk_key)
         if self._plane.save_mode == "deferred":
             self._plane.save_all(self._store_plan, self._store_arena)
         else:

@@ -33,7 +33,8 @@ class StorePlan:
     slot_offsets: np.ndarray  # int64 record offsets in the arena
     transfers: list[tuple[str, int, int, int]]  # (chunk_key, arena_off, nbytes, file_off)
     arena_bytes: int
-    device_tables: Optional[tuple] = None  # (page_ids, slot_offsets) on the device
+    gather: Optional[object] = None  # ops.PreparedGather bound to the step's arena
+    on_side: bool = False  # gathers run on the plane's side stream
 
 
 @dataclass
@@ -102,6 +103,13 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
 # ---------------------------------------------------------------------------
 # worker data plane
 
+# save_stream="auto": a step's gathers go to the side stream only when one
+# layer's gather moves at least this much. Ordering the side stream after the
+# model's stream costs about 11 us of host time per layer (an event record
+# and a stream wait), more than the device time of a smaller gather (32 MiB
+# per layer is about 10 us at 6 TB/s), which then runs on the current stream.
+SIDE_STREAM_MIN_LAYER_BYTES = 32 << 20
+
 
 class KVDataPlane:
     """Worker-side movement of KV pages between vLLM's caches and the store.
@@ -116,7 +124,7 @@ class KVDataPlane:
                  inv_freq: Optional[np.ndarray] = None, rope_scaling: Optional[dict] = None,
                  save_mode: str = "per_layer",
                  io_slot_bytes: int = 4 << 20, io_slots: int = 8,
-                 io_backend: str = "native", save_stream: str = "side",
+                 io_backend: str = "native", save_stream: str = "auto",
                  k_scales: Optional[torch.Tensor] = None, io_readers: int = 4,
                  layer_rope: Optional[list] = None,
                  io_timeout: Optional[float] = 120.0) -> None:
@@ -124,11 +132,12 @@ class KVDataPlane:
             raise ValueError("save_mode must be 'per_layer' or 'deferred'")
         if io_backend not in ("native", "direct", "python"):
             raise ValueError("io_backend must be 'native', 'direct' or 'python'")
-        if save_stream not in ("side", "current"):
-            raise ValueError("save_stream must be 'side' or 'current'")
+        if save_stream not in ("side", "current", "auto"):
+            raise ValueError("save_stream must be 'side', 'current' or 'auto'")
         self.io_backend = io_backend
         self.save_stream = save_stream
         self._side: Optional[torch.cuda.Stream] = None
+        self._save_ev: Optional[torch.cuda.Event] = None
         self.store_path = store_path
         self.rope_theta = float(rope_theta)
         self.rope_style = rope_style
@@ -188,7 +197,7 @@ class KVDataPlane:
         if self.layer_rope is not None:
             self._register_layer_rope()
         preallocate_store(self.store_path, max(self.slot_bytes * 1024, 64 << 20))
-        if self.save_stream == "side" and lay.device.type == "cuda" and self._side is None:
+        if self.save_stream != "current" and lay.device.type == "cuda" and self._side is None:
             self._side = torch.cuda.Stream(lay.device)  # default priority
         if self.io_backend == "direct" and self.slot_bytes % 4096:
             raise ValueError("io_backend='direct' needs a slot record size that is a "
@@ -235,51 +244,50 @@ class KVDataPlane:
     # -- save
     def new_store_arena(self, plan: StorePlan) -> torch.Tensor:
         """Staging arena of a step's store requests. The plan's page tables are
-        validated and uploaded once here and reused by every layer's gather."""
+        validated, uploaded and bound to the arena once here; every layer's
+        gather reuses them."""
         from daser_amd import ops
 
         arena = torch.empty(max(plan.arena_bytes, 16), dtype=torch.uint8, device=self.device)
         if plan.page_ids.size:
             ops._validate(self.table.layout, plan.page_ids, plan.slot_offsets, arena, 0,
                           self.table.layout.num_layers, True)
-            plan.device_tables = (torch.from_numpy(plan.page_ids).to(self.device),
-                                  torch.from_numpy(plan.slot_offsets).to(self.device))
+            plan.gather = ops.PreparedGather(
+                self.table, torch.from_numpy(plan.page_ids).to(self.device),
+                torch.from_numpy(plan.slot_offsets).to(self.device), arena)
+            per_layer = plan.page_ids.size * self.table.layout.layer_bytes
+            plan.on_side = self._side is not None and (
+                self.save_stream == "side" or per_layer >= SIDE_STREAM_MIN_LAYER_BYTES)
+            if plan.on_side:
+                arena.record_stream(self._side)  # freed only after the side stream's gathers
         return arena
 
-    def _on_save_stream(self, arena: torch.Tensor):
-        """Context for the gathers: the side stream, ordered after the work
-        the model's stream has enqueued so far (the layer's KV writes)."""
-        import contextlib
-
-        if self._side is None:
-            return contextlib.nullcontext()
-        ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.device))
-        self._side.wait_event(ev)
-        arena.record_stream(self._side)
-        return torch.cuda.stream(self._side)
+    def _save_stream(self, plan: StorePlan) -> int:
+        """HIP stream handle for the plan's gathers: the side stream, first
+        ordered after the work the model's stream has enqueued so far (the
+        layer's KV writes); or the current stream."""
+        cur = torch.cuda.current_stream(self.device)
+        if not plan.on_side:
+            return cur.cuda_stream
+        if self._save_ev is None:
+            self._save_ev = torch.cuda.Event()
+        # one event serves every layer: a wait binds the record made just before it
+        self._save_ev.record(cur)
+        self._side.wait_event(self._save_ev)
+        return self._side.cuda_stream
 
     def save_layer(self, layer_name: str, plan: StorePlan, arena: torch.Tensor) -> None:
         """Gathers one layer's pages of every store request. With
         save_stream="side" the gather runs on a side stream after the KV
         writes already enqueued, overlapping the model's later layers."""
-        from daser_amd import ops
-
-        if plan.page_ids.size == 0:
+        if plan.gather is None:
             return
-        l = self.layer_idx[layer_name]
-        ids, offs = plan.device_tables
-        with self._on_save_stream(arena):
-            ops.gather(self.table, ids, offs, arena, layers=(l, 1))
+        plan.gather(self.layer_idx[layer_name], 1, self._save_stream(plan))
 
     def save_all(self, plan: StorePlan, arena: torch.Tensor) -> None:
-        from daser_amd import ops
-
-        if plan.page_ids.size == 0:
+        if plan.gather is None:
             return
-        ids, offs = plan.device_tables
-        with self._on_save_stream(arena):
-            ops.gather(self.table, ids, offs, arena)
+        plan.gather(0, self.table.layout.num_layers, self._save_stream(plan))
 
     def flush_async(self, plan: StorePlan, arena: torch.Tensor, done) -> None:
         """Like flush, but the file writes run on a background writer thread
@@ -293,8 +301,8 @@ class KVDataPlane:
 
         cur = torch.cuda.current_stream(self.device)
         ev = torch.cuda.Event()
-        ev.record(self._side if self._side is not None else cur)
-        if self._side is not None:
+        ev.record(self._side if plan.on_side else cur)
+        if plan.on_side:
             cur.wait_event(ev)
         if self._writer is None:
             self._writer = ThreadPoolExecutor(max_workers=1, thread_name_prefix="daser-save")
@@ -327,7 +335,7 @@ class KVDataPlane:
         """Writes each request's records at its file offset; returns the
         chunk keys written (to commit)."""
         keys: list[str] = []
-        producer = self._side
+        producer = self._side if plan.on_side else None
         if producer is None and self.device.type == "cuda":
             producer = torch.cuda.current_stream(self.device)  # resolved on this thread
 

@@ -233,6 +233,34 @@ def gather(
     _lib.check("dsr_gather", rc)
 
 
+class PreparedGather:
+    """A gather of fixed page tables into a fixed staging buffer, checked and
+    converted once; each call launches it for a layer range. For callers
+    that launch the same gather once per layer (the connector's
+    save_kv_layer runs 32-80 times a step), so that a call costs one ctypes
+    launch and no table checks or conversions."""
+
+    def __init__(self, table: LayerTable, page_ids, slot_offsets, staging: torch.Tensor,
+                 *, layer0: int = 0) -> None:
+        args, self._keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, None,
+                                      records_written=True)
+        self._table = table
+        self._staging = staging
+        self._mid = args[2:12]  # strides, page geometry, tables, staging
+        self._layer0 = layer0
+        self._n_layers = table.layout.num_layers
+        self._fn = _lib.lib().dsr_gather
+
+    def __call__(self, first: int, count: int, stream: int) -> None:
+        """Gathers table layers [first, first + count) on ``stream`` (a HIP
+        stream handle, e.g. ``torch.cuda.current_stream().cuda_stream``)."""
+        if first < 0 or count < 0 or first + count > self._n_layers:
+            raise IndexError("layer range outside the registered caches")
+        rc = self._fn(self._table.ptr(first), count, *self._mid, self._layer0 + first, stream)
+        if rc:
+            _lib.check("dsr_gather", rc)
+
+
 def scatter(
     table: LayerTable,
     page_ids,

@@ -67,10 +67,23 @@ def _file_records(path, start_slot, n):
 @pytest.mark.parametrize("mode,backend,stream", [
     ("per_layer", "native", "side"), ("deferred", "native", "side"),
     ("per_layer", "python", "side"), ("per_layer", "native", "current"),
-    ("deferred", "python", "current"), ("per_layer", "direct", "side")])
-def test_save_writes_reference_layout(gpu, tmp_path, mode, backend, stream):
+    ("deferred", "python", "current"), ("per_layer", "direct", "side"),
+    ("per_layer", "native", "auto-side"), ("per_layer", "native", "auto-current")])
+def test_save_writes_reference_layout(gpu, tmp_path, monkeypatch, mode, backend, stream):
     print(f"case: connector save {mode} {backend} {stream}", flush=True)
-    w, ipc = _worker(tmp_path, save_mode=mode, io_backend=backend, save_stream=stream)
+    if stream.startswith("auto"):
+        from daser_amd import data_plane
+
+        # a step's per-layer gather here is 4 pages x 8 KiB: the side stream is
+        # chosen when the threshold is below that
+        monkeypatch.setattr(data_plane, "SIDE_STREAM_MIN_LAYER_BYTES",
+                            1 if stream == "auto-side" else 1 << 40)
+        seen = []
+        orig = data_plane.KVDataPlane._save_stream
+        monkeypatch.setattr(data_plane.KVDataPlane, "_save_stream",
+                            lambda self, plan: seen.append(plan.on_side) or orig(self, plan))
+    w, ipc = _worker(tmp_path, save_mode=mode, io_backend=backend,
+                     save_stream=stream.split("-")[0])
     caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=31)
     named = _named(caches)
     w.register_kv_caches(named)
@@ -83,6 +96,8 @@ def test_save_writes_reference_layout(gpu, tmp_path, mode, backend, stream):
                       SHAPE.layer_bytes)
         assert np.array_equal(_file_records(tmp_path / "daser.store", start, len(blocks)), ref)
     assert sorted(ipc.committed) == ["ka", "kb"]
+    if stream.startswith("auto"):
+        assert seen and all(x == (stream == "auto-side") for x in seen)
     w.shutdown()
 
 

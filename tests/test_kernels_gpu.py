@@ -91,6 +91,38 @@ def test_per_layer_launches_match_all_layer_launch(gpu):
     assert torch.equal(full, per)
 
 
+def test_prepared_gather_matches_gather(gpu):
+    """ops.PreparedGather (tables bound once, one launch per layer on a given
+    stream, as save_kv_layer uses it) writes what ops.gather writes, and
+    rejects layer ranges outside the caches."""
+    print("case: prepared gather", flush=True)
+    wl = workloads.config(1)
+    caches = rand_caches(wl.shape, wl.num_blocks, "bf16", gpu, seed=6)
+    table = ops.LayerTable(caches)
+    full = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(table, wl.page_ids, wl.slot_offsets, full)
+    per = torch.zeros_like(full)
+    side = torch.cuda.Stream(gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    pg = ops.PreparedGather(table, torch.from_numpy(wl.page_ids).to(gpu),
+                            torch.from_numpy(wl.slot_offsets).to(gpu), per)
+    for l in reversed(range(wl.shape.num_layers)):
+        pg(l, 1, side.cuda_stream)
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(full, per)
+    whole = torch.zeros_like(full)
+    ops.PreparedGather(table, wl.page_ids, wl.slot_offsets, whole)(
+        0, wl.shape.num_layers, torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(full, whole)
+    for first, count in ((-1, 1), (wl.shape.num_layers, 1), (0, wl.shape.num_layers + 1)):
+        with pytest.raises(IndexError):
+            pg(first, count, side.cuda_stream)
+    with pytest.raises(IndexError):  # tables checked once, at construction
+        ops.PreparedGather(table, [wl.num_blocks], [0], per)
+
+
 @pytest.mark.parametrize("heads,head_dim,dt", [
     (8, 128, "bf16"),   # 32 KiB pages: grouped kernel, one unit per workgroup
     (1, 128, "bf16"),   # 4 KiB: grouped, 8 units per workgroup
