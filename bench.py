@@ -437,28 +437,34 @@ def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int 
                 "bytes_per_step": n_req * chunk_pages * slot}
 
         w = worker()
-        load_ms = []
-        for it in range(steps + 1):
-            blocks = rng.permutation(nb)[:n_req * hit_pages].tolist()
-            reqs = {}
-            for r in range(n_req):
-                s0 = r * hit_pages
-                reqs[f"l{r}"] = C.ReqLoadSpec(f"k{r}", s0, hit_pages, blocks[s0:s0 + hit_pages],
-                                              s0 * slot, hit_pages * 16, pos_offset=0,
-                                              new_pos=int(rng.integers(1, 32768)))
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            w.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_load=reqs))
-            w.start_load_kv(None)
-            torch.cuda.synchronize()
-            if it:
-                load_ms.append((time.perf_counter() - t0) * 1e3)
-            w.clear_connector_metadata()
+
+        def load_case(n, pages, rotate):
+            ms = []
+            for it in range(steps + 1):
+                blocks = rng.permutation(nb)[:n * pages].tolist()
+                reqs = {}
+                for r in range(n):
+                    s0 = r * pages
+                    reqs[f"l{r}"] = C.ReqLoadSpec(
+                        f"k{r}", s0, pages, blocks[s0:s0 + pages], s0 * slot, pages * 16,
+                        pos_offset=0, new_pos=int(rng.integers(1, 32768)) if rotate else None)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                w.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_load=reqs))
+                w.start_load_kv(None)
+                torch.cuda.synchronize()
+                if it:
+                    ms.append((time.perf_counter() - t0) * 1e3)
+                w.clear_connector_metadata()
+            b = n * pages * slot
+            return {"start_load_kv_ms_median": round(float(np.median(ms)), 3),
+                    "GBps_file_inclusive": round(b / np.median(ms) / 1e6, 2),
+                    "bytes_per_step": b}
+
+        out["load_rerotate"] = load_case(n_req, hit_pages, True)
+        out["load_one_chunk_rerotate"] = load_case(1, chunk_pages, True)
+        out["load_one_chunk"] = load_case(1, chunk_pages, False)
         w.shutdown()
-        lb = n_req * hit_pages * slot
-        out["load_rerotate"] = {"start_load_kv_ms_median": round(float(np.median(load_ms)), 3),
-                                "GBps_file_inclusive": round(lb / np.median(load_ms) / 1e6, 2),
-                                "bytes_per_step": lb}
 
         # the reference's loops for the same step sizes (device copies only, no I/O)
         layer = shape.layer_bytes
@@ -485,7 +491,8 @@ def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int 
         torch.cuda.empty_cache()
     out["sample"] = (f"{steps} steps each after one warm-up; save: {n_req} requests x "
                      f"{chunk_pages} pages (256 tokens); load: {n_req} requests x {hit_pages} "
-                     f"pages re-rotated to new positions; store file under "
+                     f"pages re-rotated to new positions, and one 256-token chunk with and without a "
+                     f"position change; store file under "
                      f"{tempfile.gettempdir()} (page cache)")
     return out
 
