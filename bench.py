@@ -239,7 +239,19 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
     torch.cuda.synchronize()
     copy_ms = tc.mean_ms()
     P = wl.n_pages * shape.slot_bytes
-    extra = {}
+    # the same pages as 3-D caches with split-x K pages (vLLM's PagedAttention
+    # layout): same memory, the kx re-rotation entry point
+    flat = ops.LayerTable([c.reshape(2, c.shape[1], -1) for c in caches],
+                          block_size=shape.block_size, head_dim=shape.head_dim)
+    tk = Timer(torch)
+    for _ in range(warmup):
+        ops.scatter_rerotate(flat, ids, offs, src, tabs, ridx_d, k_scale=k_scale)
+    for _ in range(steps):
+        with tk:
+            ops.scatter_rerotate(flat, ids, offs, src, tabs, ridx_d, k_scale=k_scale)
+    torch.cuda.synchronize()
+    extra = {"kx_kernel_ms": tk.mean_ms(), "kx_GBps": 2 * P / (tk.mean_ms() * 1e-3) / 1e9}
+    del flat
     if P < torch.cuda.mem_get_info(dev)[0] // 2:
         # the save direction over the same pages into one record per page
         del src
@@ -252,8 +264,8 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
             with tg:
                 ops.gather(table, ids, roffs, recs)
         torch.cuda.synchronize()
-        extra = {"gather_ms": tg.mean_ms(),
-                 "gather_GBps": 2 * P / (tg.mean_ms() * 1e-3) / 1e9}
+        extra.update({"gather_ms": tg.mean_ms(),
+                      "gather_GBps": 2 * P / (tg.mean_ms() * 1e-3) / 1e9})
         if shape.num_heads * shape.head_dim * shape.elem_bytes <= 512:
             # small rows: the token-form kernels over the same pages, all
             # tokens valid (slot = block * bs + t, record row t)
@@ -736,6 +748,7 @@ def main() -> int:
                 "GBps": round(r["GBps"], 1), "frac": round(r["frac_hbm_peak"], 4),
                 "kernel_ms": round(r["kernel_ms"], 4), "tokens": r["tokens"],
                 "same_pages_plain_scatter_GBps": round(r["plain_scatter_GBps"], 1),
+                "split_x_k_layout_GBps": round(r["kx_GBps"], 1),
                 **({"same_pages_gather_GBps": round(r["gather_GBps"], 1)}
                    if "gather_GBps" in r else {}),
                 **({"same_pages_slots_gather_GBps": round(r["slots_gather_GBps"], 1),

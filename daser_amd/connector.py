@@ -41,7 +41,12 @@ reference's blocking behaviour), ``save_stream``
 ("side": per-layer gathers on a side stream after the layer's KV writes,
 overlapping later layers; "current": on the model's stream; "auto", default:
 the side stream when one layer's gather moves at least 32 MiB, else the
-model's stream, where a small gather costs less than ordering a side stream).
+model's stream, where a small gather costs less than ordering a side stream),
+``block_size`` / ``head_dim`` / ``kv_layout`` (head geometry of caches whose
+shape does not carry it: the 3-D (2, NB, block_size * H * D) caches of vLLM's
+PagedAttention backend, whose K pages use the split-x layout, "kx"; read
+from cache_config.block_size and the hf_config when not given; copies of
+such caches need none of it).
 """
 
 from __future__ import annotations
@@ -202,10 +207,19 @@ class DaserConnector(KVConnectorBase_V1):
         else:
             self._ipc_async = ipc_async if ipc_async is not None else _default_ipc(
                 "async", self._socket_path)
-            from daser_amd.position import layer_rope_from_hf, model_rope_from_hf
+            from daser_amd.position import head_dim_from_hf, layer_rope_from_hf, model_rope_from_hf
 
             hf = getattr(getattr(vllm_config, "model_config", None), "hf_config", None)
             hf_theta, hf_scaling = model_rope_from_hf(hf) if hf is not None else (None, None)
+            cache_cfg = getattr(vllm_config, "cache_config", None)
+            # head geometry of caches whose shape does not carry it (3-D)
+            geometry = {
+                "block_size": extra.get("block_size", getattr(cache_cfg, "block_size", None)
+                                        or self._block_tokens),
+                "head_dim": extra.get("head_dim", head_dim_from_hf(hf) if hf is not None
+                                      else None),
+                "k_layout": extra.get("kv_layout"),
+            }
             self._plane = KVDataPlane(
                 self._store_path,
                 rope_theta=float(extra.get("rope_theta", hf_theta or 10000.0)),
@@ -221,11 +235,11 @@ class DaserConnector(KVConnectorBase_V1):
                 io_timeout=extra.get("io_timeout_s", 120.0),
                 io_backend=extra.get("io_backend", "native"),
                 save_stream=extra.get("save_stream", "auto"),
+                cache_geometry=geometry,
             )
             self._k_scale_cfg = extra.get("k_scale")  # uniform fp8 K scale, optional
             self._async_save = bool(extra.get("async_save", False))
             self._commit_futs: list = []
-            cache_cfg = getattr(vllm_config, "cache_config", None)
             self._cache_dtype = str(getattr(cache_cfg, "cache_dtype", "auto"))
             self._meta: Optional[DaserConnectorMeta] = None
             self._store_plan: Optional[StorePlan] = None

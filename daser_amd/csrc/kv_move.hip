@@ -178,7 +178,8 @@ size_t rot_occupancy_lds(int wg_per_cu) {
 }
 
 template <int DT>
-int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipStream_t s) {
+int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipStream_t s,
+                    bool kx = false) {
   const int h = ra.half_vecs;
   int wg = rot_wg_per_cu<DT>();
   if (const char* e = getenv("DSR_ROT_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
@@ -193,7 +194,9 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
         kv_scatter_rerotate_lds_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, 0, s>>>(rb);
     });
   }
-  const bool contig = style == DSR_ROPE_GPTJ ||
+  // split-x K (kx): the caller checked the kx_phys conditions, which make
+  // every neox partner lane ^ 32
+  const bool contig = kx || style == DSR_ROPE_GPTJ ||
                       (h > 0 && h <= 32 && (h & (h - 1)) == 0 && ra.row_vecs % (2 * h) == 0);
   const int G = contig ? units_per_group(ra.u.page_bytes, rot_contig_unroll<DT>(),
                                          kMaxRotHalf / ra.rot_half)
@@ -225,20 +228,44 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
     rb.u = b;
     rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
     if (grouped) {
-      if (style == DSR_ROPE_NEOX)
-        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb, G);
+      if (style == DSR_ROPE_NEOX && kx)
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX, true><<<grid, kThreads, dyn, s>>>(rb, G);
+      else if (style == DSR_ROPE_NEOX)
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX, false><<<grid, kThreads, dyn, s>>>(rb, G);
+      else if (kx)
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ, true><<<grid, kThreads, dyn, s>>>(rb, G);
       else
-        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(rb, G);
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ, false><<<grid, kThreads, dyn, s>>>(rb, G);
     } else if (contig) {
-      if (style == DSR_ROPE_NEOX)
-        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb);
+      if (style == DSR_ROPE_NEOX && kx)
+        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX, true><<<grid, kThreads, dyn, s>>>(rb);
+      else if (style == DSR_ROPE_NEOX)
+        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX, false><<<grid, kThreads, dyn, s>>>(rb);
+      else if (kx)
+        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ, true><<<grid, kThreads, dyn, s>>>(rb);
       else
-        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(rb);
+        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ, false><<<grid, kThreads, dyn, s>>>(rb);
     } else if (rows_ok) {
       kv_scatter_rerotate_rows_kernel<DT><<<grid, kThreads, dyn, s>>>(rb);
     } else {
       kv_scatter_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb);
     }
+  });
+}
+
+// The pair-task kernel alone: the split-x K layout, whose rotation partners
+// are a whole block of vectors apart.
+template <int DT>
+int launch_rerotate_pairs(const RotArgs& ra, int n_pages, int style, hipStream_t s) {
+  const size_t dyn = rot_occupancy_lds(rot_wg_per_cu<DT>());
+  return launch_page_ranges(ra.u, n_pages, 1, [&](const UnitArgs& b, unsigned grid) {
+    RotArgs rb = ra;
+    rb.u = b;
+    rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
+    if (style == DSR_ROPE_NEOX)
+      kv_scatter_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb);
+    else
+      kv_scatter_rerotate_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(rb);
   });
 }
 
@@ -314,7 +341,13 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   });
 }
 
-int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
+}  // extern "C"
+
+namespace {
+
+// Both K layouts: kx_block = 0 for token-major K rows (block_size x H x D),
+// kx_block = block_size for the split-x K layout (H x D/X x block_size x X).
+int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
                          int64_t kv_stride, int64_t page_stride,
                          int64_t page_bytes, int64_t num_blocks,
                          const int32_t* page_ids, const int64_t* slot_offsets,
@@ -324,7 +357,7 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          const int32_t* rope_idx, int n_tables,
                          const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
-                         const float* k_scale, dsr_stream_t stream) {
+                         const float* k_scale, int kx_block, dsr_stream_t stream) {
   int rc = check_common(layer_base, n_layers, kv_stride, page_stride, page_bytes,
                         num_blocks, page_ids, slot_offsets, n_pages, staging,
                         staging_bytes, layer_bytes, layer0);
@@ -355,6 +388,11 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
   const bool vec_ok = ((int64_t)(head_dim - rot_dim) * esize) % 16 == 0 &&
                       (rope_style == DSR_ROPE_NEOX ? (rot_dim / 2) % ve == 0 : rot_dim % ve == 0);
   if (!vec_ok && row_bytes / 16 > 2048) return DSR_ERR_SHAPE;  // one row per LDS chunk
+  // split-x K: a head's block of block_size tokens is the rotation "row";
+  // only whole-vector rotary widths (the pair-task kernel) are supported
+  if (kx_block < 0 || (kx_block > 0 && (!vec_ok || page_bytes % (row_bytes * kx_block))))
+    return DSR_ERR_SHAPE;
+  const int cd = kx_block > 0 ? kx_block : 1;
   const int task_vecs = !vec_ok ? 0 : rope_style == DSR_ROPE_NEOX ? rot_dim / 2 / ve
                                                                    : rot_dim / ve;
   if (n_pages == 0 || n_layers == 0) return DSR_OK;
@@ -370,15 +408,47 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
   ra.n_tables = n_tables;
   ra.layer_group = layer_group;
   ra.n_groups = layer_group ? n_groups : 1;
-  ra.row_vecs = (int)(row_bytes / 16);
+  ra.row_vecs = (int)(row_bytes / 16) * cd;
   ra.rot_half = rot_dim / 2;
-  ra.task_vecs = task_vecs;
-  ra.tail_vec0 = rot_dim * esize / 16;
-  ra.tasks_per_row = task_vecs + (head_dim - rot_dim) * esize / 16;
+  ra.task_vecs = task_vecs * cd;
+  ra.tail_vec0 = rot_dim * esize / 16 * cd;
+  ra.tasks_per_row = (task_vecs + (head_dim - rot_dim) * esize / 16) * cd;
+  ra.col_div = cd;
   ra.rot_vecs = rot_dim * esize / 16;
   ra.half_vecs = rope_style == DSR_ROPE_NEOX && vec_ok ? rot_dim / 2 * esize / 16 : 0;
   ra.k_scale = k_scale;
   hipStream_t s = (hipStream_t)stream;
+  if (kx_block > 0) {
+    // vector kernels when the head block is a power-of-two number of
+    // vectors (>= one wave), block_size a power of two and the neox partner
+    // distance a multiple of 32 vectors (kx_phys); the pair-task kernel else
+    const int64_t hv = row_bytes / 16 * kx_block;  // vectors per head block
+    const int dist = rope_style == DSR_ROPE_NEOX ? task_vecs * kx_block : 0;
+    const bool pow2 = (hv & (hv - 1)) == 0 && (kx_block & (kx_block - 1)) == 0;
+    if (pow2 && hv >= kWave && dist % 32 == 0 && page_bytes % 1024 == 0 &&
+        !(getenv("DSR_ROT_KERNEL") && !strcmp(getenv("DSR_ROT_KERNEL"), "pairs"))) {
+      ra.kx_row_shift = __builtin_ctzll((unsigned long long)hv);
+      ra.kx_bs_shift = __builtin_ctz((unsigned)kx_block);
+      ra.kx_dist = dist;
+      ra.row_vecs = (int)hv;
+      switch (dtype) {
+        case DSR_DTYPE_BF16:
+          return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, true, s, true);
+        case DSR_DTYPE_FP16:
+          return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, true, s, true);
+        default:
+          return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, true, s, true);
+      }
+    }
+    switch (dtype) {
+      case DSR_DTYPE_BF16:
+        return launch_rerotate_pairs<DSR_DTYPE_BF16>(ra, n_pages, rope_style, s);
+      case DSR_DTYPE_FP16:
+        return launch_rerotate_pairs<DSR_DTYPE_FP16>(ra, n_pages, rope_style, s);
+      default:
+        return launch_rerotate_pairs<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, s);
+    }
+  }
   switch (dtype) {
     case DSR_DTYPE_BF16:
       return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, vec_ok, s);
@@ -387,6 +457,47 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
     default:
       return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, vec_ok, s);
   }
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
+                         int64_t kv_stride, int64_t page_stride,
+                         int64_t page_bytes, int64_t num_blocks,
+                         const int32_t* page_ids, const int64_t* slot_offsets,
+                         int n_pages, const void* staging,
+                         int64_t staging_bytes, int64_t layer_bytes,
+                         int layer0, const float* cos_sin,
+                         const int32_t* rope_idx, int n_tables,
+                         const int32_t* layer_group, int n_groups, int head_dim,
+                         int rot_dim, int rope_style, int dtype,
+                         const float* k_scale, dsr_stream_t stream) {
+  return scatter_rerotate_any(layer_base, n_layers, kv_stride, page_stride, page_bytes,
+                              num_blocks, page_ids, slot_offsets, n_pages, staging,
+                              staging_bytes, layer_bytes, layer0, cos_sin, rope_idx, n_tables,
+                              layer_group, n_groups, head_dim, rot_dim, rope_style, dtype,
+                              k_scale, 0, stream);
+}
+
+int dsr_scatter_rerotate_kx(const uint64_t* layer_base, int n_layers,
+                            int64_t kv_stride, int64_t page_stride,
+                            int64_t page_bytes, int64_t num_blocks,
+                            const int32_t* page_ids, const int64_t* slot_offsets,
+                            int n_pages, const void* staging,
+                            int64_t staging_bytes, int64_t layer_bytes,
+                            int layer0, const float* cos_sin,
+                            const int32_t* rope_idx, int n_tables,
+                            const int32_t* layer_group, int n_groups, int head_dim,
+                            int rot_dim, int rope_style, int dtype,
+                            const float* k_scale, int block_size, dsr_stream_t stream) {
+  if (block_size <= 0) return DSR_ERR_ARG;
+  return scatter_rerotate_any(layer_base, n_layers, kv_stride, page_stride, page_bytes,
+                              num_blocks, page_ids, slot_offsets, n_pages, staging,
+                              staging_bytes, layer_bytes, layer0, cos_sin, rope_idx, n_tables,
+                              layer_group, n_groups, head_dim, rot_dim, rope_style, dtype,
+                              k_scale, block_size, stream);
 }
 
 namespace {

@@ -137,7 +137,39 @@ struct RotArgs {
   int32_t rot_vecs;   // 16-byte vectors of a row inside the rotated region
   int32_t half_vecs;  // neox: vectors from a first-half vector to its partner
   const float* k_scale;
+  // Pair-task kernel only: task columns per table column. 1 for token-major
+  // K rows; block_size for the split-x K layout, where a row is one head's
+  // [head_dim / X][block_size][X] block and vector c holds dims
+  // (c / block_size) * X ... + X - 1 of token c % block_size.
+  int32_t col_div = 1;
+  // Contig and grouped kernels on split-x K pages (KX = true): head blocks
+  // of 2^kx_row_shift vectors, block_size 2^kx_bs_shift, neox partners
+  // kx_dist vectors apart (0 for gptj).
+  int32_t kx_row_shift = 0;
+  int32_t kx_bs_shift = 0;
+  int32_t kx_dist = 0;
 };
+
+// Split-x K: the lane-consecutive vector index i of a page -> the vector it
+// moves. Inside a head block the rotated region is walked in 64-vector runs
+// whose lanes 0-31 take 32 consecutive first-half vectors and lanes 32-63
+// their partners kx_dist vectors on, so a neox partner is always lane ^ 32
+// and each half-wave still reads 512 contiguous bytes. Tail vectors (and all
+// of gptj) keep their index. Needs kx_dist % 32 == 0 and 64 | block vectors.
+__device__ __forceinline__ int kx_phys(const RotArgs& ra, int i) {
+  const int q = i & ((1 << ra.kx_row_shift) - 1);
+  if (q >= 2 * ra.kx_dist) return i;
+  const int w = q & 63;
+  return i - q + ((q >> 6) << 5) + (w & 31) + (w >= 32 ? ra.kx_dist : 0);
+}
+
+// Table column (dims c * VE ...) of physical K vector p: token-major rows
+// have row_vecs vectors of consecutive dims; split-x head blocks hold
+// block_size vectors per column.
+template <bool KX>
+__device__ __forceinline__ int k_column(const RotArgs& ra, int p) {
+  return KX ? (p & ((1 << ra.kx_row_shift) - 1)) >> ra.kx_bs_shift : p % ra.row_vecs;
+}
 
 // Table of unit (page p, layer l): page p's delta table inside layer l's
 // group block (cos_sin holds n_groups blocks of n_tables tables), or -1 when
@@ -150,16 +182,14 @@ __device__ __forceinline__ int rope_table(const RotArgs& ra, int64_t p, int l) {
   return g < 0 || g >= ra.n_groups ? -1 : g * ra.n_tables + ti;
 }
 
-// Rotates the K page (rows of head_dim elements) from src into dst.
-// neox task c: vector c of the first half and its partner at +rot_half;
-// gptj task c: vector c, whose VE/2 adjacent pairs rotate in place;
-// tail task: one un-rotated 16-byte vector, copied.
 // K-page rotation in rounds of kRotUnroll tasks per lane. Task t covers row
 // t / tasks_per_row, column c = t % tasks_per_row:
 //   neox, c < task_vecs: vector c of the rotated first half and its partner
 //                        at +rot_half elements;
 //   gptj, c < task_vecs: vector c, whose VE/2 adjacent pairs rotate in place;
 //   c >= task_vecs:      one un-rotated 16-byte tail vector, copied.
+// The table column of task column c is c / col_div (split-x K: the rows,
+// columns and half distance are all counted in vectors of the head block).
 template <int DT, int STYLE>
 struct KRound {
   static constexpr int VE = Codec<DT>::VE;
@@ -181,7 +211,7 @@ struct KRound {
       if (t < ntask) {
         const int row = t / ra.tasks_per_row;
         const int c = t - row * ra.tasks_per_row;
-        c_of[k] = c;
+        c_of[k] = ra.col_div == 1 ? c : c / ra.col_div;
         if (c < ra.task_vecs) {
           kind[k] = 0;
           off[k] = row * row_bytes + (c << 4);
@@ -260,6 +290,14 @@ struct VRound {
       if (i < nvec) bstore(rd, i << 4, r[k]);
     }
   }
+  // K of a split-x page: vector i of the round is physical vector kx_phys(i)
+  __device__ __forceinline__ void load_kx(const RotArgs& ra, rsrc_t rs, int base, int nvec) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * kThreads;
+      r[k] = i < nvec ? bload(rs, kx_phys(ra, i) << 4) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
 };
 
 // One workgroup per (page, layer) unit in page-list order. V, and K of pages
@@ -286,7 +324,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
   const int nvec = (int)(pb >> 4);
   const int row_bytes = ra.row_vecs << 4;
   const int ntask = (int)(pb / row_bytes) * ra.tasks_per_row;
-  const int half_off = ra.rot_half * 16 / Codec<DT>::VE;
+  const int half_off = ra.rot_half * 16 / Codec<DT>::VE * ra.col_div;
 
   VRound<kScatterUnroll> v;
   KRound<DT, STYLE> k;
@@ -365,7 +403,7 @@ __device__ __forceinline__ u32x4 rotate_vec(const RotArgs& ra, u32x4 own, u32x4 
 // shuffle. Valid when half_vecs is a power of two <= 32 dividing the row
 // evenly (rows then start on 2*half_vecs lane boundaries), and always for
 // gptj, whose pairs sit inside one vector.
-template <int DT, int STYLE, int U>
+template <int DT, int STYLE, int U, bool KX>
 __device__ __forceinline__ void rotate_contig_round(const RotArgs& ra, VRound<U>& kk,
                                                     int base, int nvec, rsrc_t kd,
                                                     const float2* tab, float scale,
@@ -375,11 +413,13 @@ __device__ __forceinline__ void rotate_contig_round(const RotArgs& ra, VRound<U>
     const int i = base + k * kThreads;
     u32x4 q = kk.r[k];
     if (STYLE == DSR_ROPE_NEOX) {  // whole wave takes part in the shuffle
+      const int dist = KX ? 32 : ra.half_vecs;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) q[w] = (unsigned)__shfl_xor((int)kk.r[k][w], ra.half_vecs);
+      for (int w = 0; w < 4; ++w) q[w] = (unsigned)__shfl_xor((int)kk.r[k][w], dist);
     }
     if (i >= nvec) continue;
-    bstore(kd, i << 4, rotate_vec<DT, STYLE>(ra, kk.r[k], q, i % ra.row_vecs, tab, scale,
+    const int p = KX ? kx_phys(ra, i) : i;
+    bstore(kd, p << 4, rotate_vec<DT, STYLE>(ra, kk.r[k], q, k_column<KX>(ra, p), tab, scale,
                                              inv_scale));
   }
 }
@@ -391,7 +431,7 @@ constexpr int rot_contig_unroll() {
   return DT == DSR_DTYPE_FP8_E4M3 ? 4 : 8;
 }
 
-template <int DT, int STYLE>
+template <int DT, int STYLE, bool KX>
 __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(RotArgs ra) {
   __shared__ float2 tab[kMaxRotHalf];
   uint8_t *cache, *rec;
@@ -411,7 +451,10 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
   const int nvec = (int)(pb >> 4);
   VRound<U> v, kk;
   v.load(vs, threadIdx.x, nvec);
-  kk.load(ks, threadIdx.x, nvec);
+  if (KX)
+    kk.load_kx(ra, ks, threadIdx.x, nvec);
+  else
+    kk.load(ks, threadIdx.x, nvec);
   const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
   for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
   float scale = 1.0f, inv_scale = 1.0f;
@@ -425,10 +468,13 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
     const int base = r * kThreads * U + threadIdx.x;
     if (r > 0) {
       v.load(vs, base, nvec);
-      kk.load(ks, base, nvec);
+      if (KX)
+        kk.load_kx(ra, ks, base, nvec);
+      else
+        kk.load(ks, base, nvec);
     }
     v.store(vd, base, nvec);
-    rotate_contig_round<DT, STYLE, U>(ra, kk, base, nvec, kd, tab, scale, inv_scale);
+    rotate_contig_round<DT, STYLE, U, KX>(ra, kk, base, nvec, kd, tab, scale, inv_scale);
   }
 }
 
@@ -611,7 +657,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_lds_kernel(RotAr
 // kernel). The group's (cos, sin) tables are staged in LDS, one rot_half
 // stretch per unit; G * rot_half <= kMaxRotHalf. K of an un-rotated unit is
 // stored as loaded.
-template <int DT, int STYLE>
+template <int DT, int STYLE, bool KX>
 __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(RotArgs ra,
                                                                                int G) {
   constexpr int U = rot_contig_unroll<DT>();
@@ -631,13 +677,15 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
   int tj[U];    // LDS table slot of the vector's unit (-1: copy)
   float sc[U];  // its layer's K scale (e4m3)
   int off[U];
+  int koff[U];  // K: split-x pages move vector kx_phys(i) in lane slot i
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const int fw = k * kThreads + wave * kWave;
     const int j = fw / nvec;
     off[k] = (fw - j * nvec + lane) << 4;
+    koff[k] = KX ? kx_phys(ra, off[k] >> 4) << 4 : off[k];
     const UnitRsrc u = unit_rsrc<false>(a, n_pages, p0, l0, j, n_here);
-    rk[k] = bload(make_rsrc(u.rec, u.n), off[k]);
+    rk[k] = bload(make_rsrc(u.rec, u.n), koff[k]);
     rv[k] = bload(make_rsrc(u.rec + a.page_bytes, u.n), off[k]);
     kd[k] = make_rsrc(u.cache, u.n);
     vd[k] = make_rsrc(u.cache + a.kv_stride, u.n);
@@ -660,13 +708,14 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
   for (int k = 0; k < U; ++k) {
     u32x4 q = rk[k];
     if (STYLE == DSR_ROPE_NEOX) {
+      const int dist = KX ? 32 : ra.half_vecs;
 #pragma unroll
-      for (int x = 0; x < 4; ++x) q[x] = (unsigned)__shfl_xor((int)rk[k][x], ra.half_vecs);
+      for (int x = 0; x < 4; ++x) q[x] = (unsigned)__shfl_xor((int)rk[k][x], dist);
     }
     const int t = tj[k] < 0 ? 0 : tj[k];
-    const u32x4 r = rotate_vec<DT, STYLE>(ra, rk[k], q, (off[k] >> 4) % ra.row_vecs,
+    const u32x4 r = rotate_vec<DT, STYLE>(ra, rk[k], q, k_column<KX>(ra, koff[k] >> 4),
                                           tab + t * ra.rot_half, sc[k], 1.0f / sc[k]);
-    bstore(kd[k], off[k], tj[k] < 0 ? rk[k] : r);
+    bstore(kd[k], koff[k], tj[k] < 0 ? rk[k] : r);
   }
 }
 

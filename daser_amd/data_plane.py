@@ -127,7 +127,8 @@ class KVDataPlane:
                  io_backend: str = "native", save_stream: str = "auto",
                  k_scales: Optional[torch.Tensor] = None, io_readers: int = 4,
                  layer_rope: Optional[list] = None,
-                 io_timeout: Optional[float] = 120.0) -> None:
+                 io_timeout: Optional[float] = 120.0,
+                 cache_geometry: Optional[dict] = None) -> None:
         if save_mode not in ("per_layer", "deferred"):
             raise ValueError("save_mode must be 'per_layer' or 'deferred'")
         if io_backend not in ("native", "direct", "python"):
@@ -146,6 +147,9 @@ class KVDataPlane:
         self.rope_scaling = rope_scaling
         # per model layer: None (no RoPE) or {"rope_theta", "rope_scaling"}
         self.layer_rope = layer_rope
+        # block_size / head_dim / k_layout of caches that are not 5-D (vLLM's
+        # PagedAttention backend: (2, NB, block_size * H * D), split-x K)
+        self.cache_geometry = dict(cache_geometry or {})
         self._layer_group: Optional[torch.Tensor] = None
         self._group_inv: list[np.ndarray] = []
         if rope_scaling and inv_freq is None:
@@ -182,19 +186,23 @@ class KVDataPlane:
 
         self.layer_names = list(kv_caches.keys())
         self.layer_idx = {n: i for i, n in enumerate(self.layer_names)}
-        self.table = ops.LayerTable([kv_caches[n] for n in self.layer_names])
+        caches = [kv_caches[n] for n in self.layer_names]
+        geo = {}
+        if caches and caches[0].dim() != 5:  # the shape carries no head geometry
+            geo = {k: v for k, v in self.cache_geometry.items() if v is not None}
+        self.table = ops.LayerTable(caches, **geo)
         lay = self.table.layout
         derived = lay.slot_bytes
         if slot_size and slot_size != derived:
             raise ValueError(f"configured slot_size {slot_size} != derived {derived}")
         self.slot_bytes = derived
-        if self.rotary_dim is None:
+        if self.rotary_dim is None and lay.has_geometry:
             self.rotary_dim = lay.head_dim
-        if self.inv_freq is None and self.rope_scaling:
+        if self.inv_freq is None and self.rope_scaling and self.rotary_dim:
             from daser_amd.position import inv_freq_for
 
             self.inv_freq = inv_freq_for(self.rope_scaling, self.rotary_dim, self.rope_theta)
-        if self.layer_rope is not None:
+        if self.layer_rope is not None and self.rotary_dim:
             self._register_layer_rope()
         preallocate_store(self.store_path, max(self.slot_bytes * 1024, 64 << 20))
         if self.save_stream != "current" and lay.device.type == "cuda" and self._side is None:
@@ -380,6 +388,10 @@ class KVDataPlane:
 
         if plan.page_ids.size == 0:
             return
+        if plan.deltas and not self.rotary_dim:
+            raise ValueError("a load moves chunks to new positions but the caches' head "
+                             "geometry is unknown: give block_size and head_dim for caches "
+                             "that are not 5-D")
         tabs = None
         if plan.deltas and self._layer_group is not None:
             if self._group_inv:  # [groups, tables, rot/2, 2]; layers in group -1 keep K

@@ -35,17 +35,30 @@ ROPE_STYLES = {"neox": _lib.DSR_ROPE_NEOX, "gptj": _lib.DSR_ROPE_GPTJ}
 
 @dataclass(frozen=True)
 class PagedKVLayout:
-    """Geometry of vLLM's per-layer paged caches ``kv_l[2, NB, bs, H, D]``.
+    """Geometry of vLLM's per-layer paged caches ``kv_l[2, NB, ...]``.
 
     Built from the registered caches (reference ``register_kv_caches``,
     daser/connector/daser_connector.py:383-413): layer order is the dict's
     insertion order, every layer must share shape, dtype and strides, and a
-    page (``kv_l[0, b]``) must be contiguous.
+    page (``kv_l[0, b]``) must be contiguous. The reference moves
+    ``kv_l[:, b]`` of any cache shape as bytes (:545-550, :625-632), and so
+    do the page copies here. Re-rotation also needs the element layout of a
+    K page (``k_layout``):
+
+    * ``"nhd"``: ``[block_size][H][D]``, the 5-D caches
+      ``(2, NB, block_size, H, D)`` of vLLM's FlashAttention-style backends;
+    * ``"kx"``: ``[H][D / X][block_size][X]`` with X = 16 / element bytes,
+      the 3-D caches ``(2, NB, block_size * H * D)`` of vLLM's
+      PagedAttention kernels (its ROCm paged-attention backend).
+
+    A cache that is not 5-D carries no head geometry in its shape: pass
+    ``block_size`` and ``head_dim`` (``num_heads`` follows from the page
+    size); without them copies work and re-rotation is refused.
     """
 
     num_layers: int
     num_blocks: int
-    block_size: int
+    block_size: int  # 0: unknown (copies only)
     num_heads: int
     head_dim: int
     dtype: torch.dtype
@@ -55,33 +68,67 @@ class PagedKVLayout:
     page_stride: int  # bytes block b -> b + 1
     layer_bytes: int  # LAYER_SIZE of the slot record
     device: torch.device
+    k_layout: str = "nhd"
 
     @property
     def slot_bytes(self) -> int:
         """SLOT_SIZE: one block's record over all layers."""
         return self.layer_bytes * self.num_layers
 
+    @property
+    def has_geometry(self) -> bool:
+        return self.head_dim > 0 and self.block_size > 0
+
     @staticmethod
-    def from_caches(kv_caches: Sequence[torch.Tensor]) -> "PagedKVLayout":
+    def from_caches(kv_caches: Sequence[torch.Tensor], *, block_size: Optional[int] = None,
+                    head_dim: Optional[int] = None,
+                    k_layout: Optional[str] = None) -> "PagedKVLayout":
         if not kv_caches:
             raise ValueError("no KV caches registered")
         t0 = kv_caches[0]
-        if t0.dim() != 5 or t0.shape[0] != 2:
+        if t0.dim() < 3 or t0.shape[0] != 2:
             raise ValueError(
-                f"expected per-layer KV cache of shape (2, num_blocks, block_size, "
-                f"num_heads, head_dim), got {tuple(t0.shape)}"
+                f"expected per-layer KV cache of shape (2, num_blocks, ...) such as "
+                f"(2, num_blocks, block_size, num_heads, head_dim), got {tuple(t0.shape)}"
             )
         for t in kv_caches:
             if t.shape != t0.shape or t.dtype != t0.dtype or t.stride() != t0.stride():
                 raise ValueError("all layer caches must share shape, dtype and strides")
             if t.device != t0.device:
                 raise ValueError("all layer caches must live on one device")
-        _, nb, bs, h, d = t0.shape
+        nb = t0.shape[1]
         s = t0.stride()
-        if s[4] != 1 or s[3] != d or s[2] != h * d:
-            raise ValueError("a KV page (block_size, num_heads, head_dim) must be contiguous")
+        expect = 1
+        for dim in range(t0.dim() - 1, 1, -1):  # a page kv[0, b] is C-contiguous
+            if t0.shape[dim] != 1 and s[dim] != expect:
+                raise ValueError("a KV page kv[0, b] must be contiguous")
+            expect *= t0.shape[dim]
+        page_elems = expect
         e = t0.element_size()
-        page_bytes = bs * h * d * e
+        if t0.dim() == 5:
+            if k_layout not in (None, "nhd"):
+                raise ValueError("a 5-D cache (2, NB, block_size, H, D) has the 'nhd' K layout")
+            _, _, bs, h, d = t0.shape
+            if (block_size not in (None, bs)) or (head_dim not in (None, d)):
+                raise ValueError(f"cache shape {tuple(t0.shape)} disagrees with "
+                                 f"block_size={block_size}, head_dim={head_dim}")
+            layout = "nhd"
+        else:
+            layout = k_layout or ("kx" if t0.dim() == 3 else "nhd")
+            if layout not in ("nhd", "kx"):
+                raise ValueError("k_layout must be 'nhd' or 'kx'")
+            bs, d, h = int(block_size or 0), int(head_dim or 0), 0
+            if bs and d:
+                if page_elems % (bs * d):
+                    raise ValueError(f"a page of {page_elems} elements is not block_size "
+                                     f"{bs} x heads x head_dim {d}")
+                h = page_elems // (bs * d)
+                if layout == "kx" and (d * e) % 16:
+                    raise ValueError("the 'kx' K layout needs head_dim * element size to be "
+                                     "a multiple of 16 bytes")
+            else:
+                bs = d = 0
+        page_bytes = page_elems * e
         # LAYER_SIZE as the reference derives it (kv.nbytes // num_blocks).
         layer_bytes = t0.numel() * e // nb if nb else 2 * page_bytes
         return PagedKVLayout(
@@ -97,14 +144,17 @@ class PagedKVLayout:
             page_stride=s[1] * e,
             layer_bytes=layer_bytes,
             device=t0.device,
+            k_layout=layout,
         )
 
 
 class LayerTable:
     """Device array of per-layer cache base addresses (uint64)."""
 
-    def __init__(self, kv_caches: Sequence[torch.Tensor]) -> None:
-        self.layout = PagedKVLayout.from_caches(kv_caches)
+    def __init__(self, kv_caches: Sequence[torch.Tensor], **geometry) -> None:
+        """``geometry``: ``block_size``, ``head_dim``, ``k_layout`` for caches
+        that are not 5-D (see PagedKVLayout)."""
+        self.layout = PagedKVLayout.from_caches(kv_caches, **geometry)
         self._caches = list(kv_caches)  # keep the borrowed tensors alive
         ptrs = np.array([t.data_ptr() for t in kv_caches], dtype=np.uint64)
         self.table = torch.from_numpy(ptrs.view(np.int64)).to(self.layout.device)
@@ -304,6 +354,9 @@ def scatter_rerotate(
     lay = table.layout
     if lay.dtype not in _DTYPE_CODES:
         raise TypeError(f"re-rotation does not support KV dtype {lay.dtype}")
+    if not lay.has_geometry:
+        raise ValueError("re-rotation needs the K page geometry: register caches that are "
+                         "not 5-D with block_size and head_dim")
     rot_dim = lay.head_dim if rot_dim is None else rot_dim
     grouped = layer_group is not None
     if cos_sin.dtype != torch.float32 or cos_sin.dim() != (4 if grouped else 3) or \
@@ -340,26 +393,24 @@ def scatter_rerotate(
         ):
             raise ValueError("k_scale must be a float32 device tensor with one scale per layer")
         ks_ptr = k_scale.data_ptr()
-    rc = _lib.lib().dsr_scatter_rerotate(
-        *args,
-        cos_sin.data_ptr(),
-        ridx_d.data_ptr(),
-        n_tables,
-        None if lg_d is None else lg_d.data_ptr(),
-        n_groups if grouped else 0,
-        lay.head_dim,
-        rot_dim,
-        ROPE_STYLES[style],
-        _DTYPE_CODES[lay.dtype],
-        ks_ptr,
-        _stream_handle(lay.device),
-    )
-    _lib.check("dsr_scatter_rerotate", rc)
+    common = (*args, cos_sin.data_ptr(), ridx_d.data_ptr(), n_tables,
+              None if lg_d is None else lg_d.data_ptr(), n_groups if grouped else 0,
+              lay.head_dim, rot_dim, ROPE_STYLES[style], _DTYPE_CODES[lay.dtype], ks_ptr)
+    if lay.k_layout == "kx":
+        rc = _lib.lib().dsr_scatter_rerotate_kx(*common, lay.block_size,
+                                                _stream_handle(lay.device))
+        _lib.check("dsr_scatter_rerotate_kx", rc)
+    else:
+        rc = _lib.lib().dsr_scatter_rerotate(*common, _stream_handle(lay.device))
+        _lib.check("dsr_scatter_rerotate", rc)
 
 
 def _slots_args(table: LayerTable, slot_mapping, row_offsets, staging, layer0, layers,
                 records_written: bool):
     lay = table.layout
+    if not lay.has_geometry or lay.k_layout != "nhd":
+        raise ValueError("the token form needs token-major pages ([block_size][H][D]) of "
+                         "known geometry")
     first, count = (0, lay.num_layers) if layers is None else layers
     if first < 0 or count < 0 or first + count > lay.num_layers:
         raise IndexError("layer range outside the registered caches")

@@ -195,6 +195,19 @@ def _text_config(hf_config):
     return getattr(hf_config, "text_config", None) or hf_config
 
 
+def head_dim_from_hf(hf_config) -> Optional[int]:
+    """Attention head size of a HF config: ``head_dim`` when set, else
+    hidden_size / num_attention_heads; None when neither is there."""
+    cfg = _text_config(hf_config)
+    d = getattr(cfg, "head_dim", None)
+    if isinstance(d, int) and d > 0:
+        return d
+    hs, nh = getattr(cfg, "hidden_size", None), getattr(cfg, "num_attention_heads", None)
+    if isinstance(hs, int) and isinstance(nh, int) and nh > 0 and hs % nh == 0:
+        return hs // nh
+    return None
+
+
 def model_rope_from_hf(hf_config) -> tuple[Optional[float], Optional[dict]]:
     """(rope_theta, rope_scaling) of a HF config, in either form
     transformers uses: ``rope_theta`` / ``rope_scaling`` attributes, or one

@@ -44,7 +44,7 @@ extern "C" {
 
 typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 
-#define DSR_ABI_VERSION 2
+#define DSR_ABI_VERSION 3
 
 /*
  * Kernel choice and launch shape follow from the geometry; these environment
@@ -175,6 +175,35 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
                          const float* k_scale, dsr_stream_t stream);
+
+/*
+ * dsr_scatter_rerotate for caches whose K page uses the split-x layout of
+ * vLLM's PagedAttention kernels (its ROCm paged-attention backend: caches of
+ * shape (2, num_blocks, block_size * H * D), K viewed as
+ * [H][D / X][block_size][X] with X = 16 / element bytes, V as
+ * [H][D][block_size]). Element (token t, head h, dim d) of K sits at element
+ *     ((h * (D / X) + d / X) * block_size + t) * X + d % X
+ * of the page. The rotation is the same as dsr_scatter_rerotate's, per
+ * (t, h) over dims d < rot_dim; V and unrotated pages are copied bit-exactly
+ * (the copy entry points need no layout: they move whole pages).
+ *
+ * Replaces the same reference loop as dsr_scatter_rerotate
+ * (daser/connector/daser_connector.py:536-551, whose per-page copy_ moves
+ * kv[:, b] of any cache shape). Extra constraints: block_size > 0; page_bytes
+ * a multiple of block_size * head_dim * elem_bytes; rot_dim / 2 (neox) or
+ * rot_dim (gptj) a multiple of X; head_dim - rot_dim a multiple of X.
+ */
+int dsr_scatter_rerotate_kx(const uint64_t* layer_base, int n_layers,
+                            int64_t kv_stride, int64_t page_stride,
+                            int64_t page_bytes, int64_t num_blocks,
+                            const int32_t* page_ids, const int64_t* slot_offsets,
+                            int n_pages, const void* staging,
+                            int64_t staging_bytes, int64_t layer_bytes,
+                            int layer0, const float* cos_sin,
+                            const int32_t* rope_idx, int n_tables,
+                            const int32_t* layer_group, int n_groups, int head_dim,
+                            int rot_dim, int rope_style, int dtype,
+                            const float* k_scale, int block_size, dsr_stream_t stream);
 
 /*
  * Token-granular offload gather driven by vLLM's slot_mapping: for every

@@ -117,6 +117,33 @@ def scatter_rerotate(layers, page_ids, slot_offsets, staging: np.ndarray,
         float(theta), None if inv is None else _ptr(inv))
 
 
+def kx_to_nhd(pages: np.ndarray, block_size: int, num_heads: int, head_dim: int) -> np.ndarray:
+    """K pages of the split-x layout (vLLM's PagedAttention kernels: element
+    (t, h, d) at ((h * (D / X) + d / X) * block_size + t) * X + d % X, with
+    X = 16 / element bytes) as token-major pages [block_size][H][D]. The
+    last axis of ``pages`` is one page of element bits; the result has the
+    leading axes plus (block_size, H, D). The layout is vLLM's (external and
+    absent here); this function states it and a brute-force index test pins
+    it."""
+    x = 16 // pages.itemsize
+    lead = pages.shape[:-1]
+    v = pages.reshape(*lead, num_heads, head_dim // x, block_size, x)
+    n = len(lead)
+    perm = tuple(range(n)) + (n + 2, n, n + 1, n + 3)  # -> (t, h, d / X, d % X)
+    return np.ascontiguousarray(v.transpose(perm)).reshape(*lead, block_size, num_heads,
+                                                          head_dim)
+
+
+def nhd_to_kx(pages: np.ndarray) -> np.ndarray:
+    """Inverse of kx_to_nhd: (..., block_size, H, D) -> (..., page elements)."""
+    *lead, bs, h, d = pages.shape
+    x = 16 // pages.itemsize
+    v = pages.reshape(*lead, bs, h, d // x, x)
+    n = len(lead)
+    perm = tuple(range(n)) + (n + 1, n + 2, n, n + 3)  # -> (h, d / X, t, d % X)
+    return np.ascontiguousarray(v.transpose(perm)).reshape(*lead, bs * h * d)
+
+
 def _slots_call(fn, layers, slot_mapping, row_offsets, staging, layer_bytes, layer0):
     tab, kvs, ps, pb = _layer_table(layers)
     _, _, bs, h, d = layers[0].shape

@@ -2,7 +2,8 @@
 // hipMalloc, gathers a permuted page list into slot records with dsr_gather,
 // checks the records against a host memcpy of the same layout, scatters them
 // into a second cache with dsr_scatter and checks the pages, then re-rotates
-// with a zero table (rope_idx -1) and checks a bit-exact copy; gathers the
+// with a zero table (rope_idx -1) through both K layouts' entry points and
+// checks a bit-exact copy; gathers the
 // same records token by token with dsr_gather_slots; writes them to a store
 // file through the staging ring and reads them back. Exit code 0 on success;
 // prints the failing check otherwise.
@@ -103,6 +104,19 @@ int main() {
   std::vector<uint8_t> c3(L * cache_bytes);
   hipMemcpy(c3.data(), cache2, c3.size(), hipMemcpyDeviceToHost);
   REQUIRE(c3 == c2, "unrotated re-rotate scatter equals plain scatter");
+  // the split-x entry point on the same bytes: unrotated pages are copied too
+  hipMemset(cache2, 0, L * cache_bytes);
+  rc = dsr_scatter_rerotate_kx(bases + L, L, NB * page, page, page, NB, d_ids, d_offs, n, stg,
+                               n * slot, layer_bytes, 0, tab, ridx, 1, nullptr, 0, D, D,
+                               DSR_ROPE_NEOX, DSR_DTYPE_BF16, nullptr, bs, nullptr);
+  REQUIRE(rc == 0, dsr_error_string(rc));
+  hipMemcpy(c3.data(), cache2, c3.size(), hipMemcpyDeviceToHost);
+  REQUIRE(c3 == c2, "unrotated split-x re-rotate scatter equals plain scatter");
+  REQUIRE(dsr_scatter_rerotate_kx(bases + L, L, NB * page, page, page, NB, d_ids, d_offs, n,
+                                  stg, n * slot, layer_bytes, 0, tab, ridx, 1, nullptr, 0, D,
+                                  D, DSR_ROPE_NEOX, DSR_DTYPE_BF16, nullptr, 0,
+                                  nullptr) == DSR_ERR_ARG,
+          "split-x without a block size rejected");
 
   REQUIRE(dsr_gather(bases, L, 4100, page, page, NB, d_ids, d_offs, n, stg, n * slot,
                      layer_bytes, 0, nullptr) == DSR_ERR_ALIGN,

@@ -533,3 +533,53 @@ def test_load_rerotates_each_layer_with_its_rope(gpu, tmp_path):
         assert ok, f"layer {l}: {msg}"
     w.shutdown()
     w2.shutdown()
+
+
+def test_flat_caches_save_and_rerotate_load(gpu, tmp_path):
+    """vLLM's PagedAttention backend allocates (2, NB, block_size * H * D)
+    caches with split-x K pages: saves write kv[:, b] bytes as the reference
+    does, and a load at a new position re-rotates K in that layout, with the
+    head geometry taken from cache_config and the hf_config."""
+    print("case: connector 3-D caches", flush=True)
+    hf = SimpleNamespace(hidden_size=128, num_attention_heads=2, rope_theta=500000.0)
+    cfg = SimpleNamespace(
+        kv_transfer_config=SimpleNamespace(kv_connector_extra_config=dict(
+            store_path=str(tmp_path / "daser.store"), io_slot_mb=0.03125, io_slots=3)),
+        model_config=SimpleNamespace(hf_config=hf),
+        cache_config=SimpleNamespace(block_size=16, cache_dtype="auto"))
+    caches = [c.reshape(2, 16, -1) for c in rand_caches(SHAPE, 16, "bf16", gpu, seed=35)]
+    w = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=FakeAsyncIPC())
+    named = _named(caches)
+    w.register_kv_caches(named)
+    assert w._plane.table.layout.k_layout == "kx" and w._plane.table.layout.num_heads == 2
+    _save(w, named, _store_reqs())
+    slot = SHAPE.slot_bytes
+    recs = _file_records(tmp_path / "daser.store", 3, 3).copy()
+    want = np.concatenate([to_bits_np(c, "bf16")[:, b].reshape(-1).view(np.uint8)
+                           for b in (5, 9, 2) for c in caches])
+    assert np.array_equal(recs, want)  # bytes of kv[:, b], layer after layer
+
+    fresh = [torch.zeros_like(c) for c in caches]
+    w2 = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=FakeAsyncIPC())
+    w2.register_kv_caches(_named(fresh))
+    w2.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_load={
+        "x": C.ReqLoadSpec("ka", 3, 3, [1, 12, 4], 3 * slot, 40, pos_offset=100,
+                           new_pos=4196)}))
+    w2.start_load_kv(None)
+    torch.cuda.synchronize()
+    to_nhd = lambda a: oracle.kx_to_nhd(a, 16, 2, 64)  # noqa: E731
+    ref = [np.zeros((2, 16, 16, 2, 64), np.uint16) for _ in caches]
+    recs_nhd = np.ascontiguousarray(to_nhd(recs.view(np.uint16).reshape(3, 3, 2, -1)))
+    oracle.scatter_rerotate(ref, [1, 12, 4], np.arange(3) * slot,
+                            recs_nhd.reshape(-1).view(np.uint8), SHAPE.layer_bytes,
+                            dtype=oracle.BF16, rot_dim=64, style=oracle.NEOX,
+                            stored_pos=np.full(3, 100), new_pos=np.full(3, 4196),
+                            rotate=np.ones(3), theta=500000.0)
+    for l, f in enumerate(fresh):
+        got = to_nhd(to_bits_np(f, "bf16"))
+        assert np.array_equal(got[1][[1, 12, 4]], ref[l][1][[1, 12, 4]])
+        ok, msg = oracle.rotation_within_tolerance(got[0][[1, 12, 4]], ref[l][0][[1, 12, 4]],
+                                                   oracle.BF16)
+        assert ok, f"layer {l}: {msg}"
+    w.shutdown()
+    w2.shutdown()

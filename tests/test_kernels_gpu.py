@@ -933,3 +933,108 @@ def test_concurrent_streams_match_sequential(gpu):
         assert torch.equal(seq_o[h], par_o[h])
         for a, b in zip(seq_d[h], par_d[h]):
             assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# 3-D caches: byte copies for any page layout, re-rotation of split-x K pages
+
+
+def _flat_caches(shape, nb, dt, gpu, seed, scale=1.0):
+    """(2, NB, block_size * H * D) caches, as vLLM's PagedAttention backend
+    allocates them."""
+    return [c.reshape(2, nb, -1) for c in rand_caches(shape, nb, dt, gpu, seed, scale)]
+
+
+def test_flat_cache_copies_bit_exact(gpu):
+    """Gather/scatter move kv[:, b] of a 3-D cache as bytes, like the
+    reference's copy_ of any cache shape; no head geometry is needed."""
+    print("case: 3-D cache copies", flush=True)
+    shape = KVShape(3, 2, 64, 16, 2)
+    wl = workloads.ragged(shape, 4, 1, 120, seed=4, pool_slack=1.5)
+    caches = _flat_caches(shape, wl.num_blocks, "bf16", gpu, seed=12)
+    staging, ref = _gather_both(wl, caches, "bf16", gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(staging.cpu().numpy(), ref)
+    dst = [torch.zeros_like(c) for c in caches]
+    ops.scatter(ops.LayerTable(dst), wl.page_ids, wl.slot_offsets, staging)
+    torch.cuda.synchronize()
+    ids = torch.from_numpy(wl.page_ids.astype(np.int64)).to(gpu)
+    for l in range(shape.num_layers):
+        assert torch.equal(dst[l][:, ids], caches[l][:, ids])
+    table = ops.LayerTable(caches)
+    assert table.layout.k_layout == "kx" and not table.layout.has_geometry
+    tabs = position.delta_tables([3], 64, device=gpu)
+    with pytest.raises(ValueError):  # no head geometry: re-rotation refused
+        ops.scatter_rerotate(table, wl.page_ids[:1], wl.slot_offsets[:1], staging, tabs, [0])
+    with pytest.raises(ValueError):  # no token-major rows: the token form refused
+        ops.gather_slots(ops.LayerTable(caches, block_size=16, head_dim=64), [0], [0], staging)
+
+
+@pytest.mark.parametrize("dt,style,heads,head_dim,rot_dim", [
+    ("bf16", "neox", 4, 128, 128),
+    ("bf16", "neox", 1, 128, 64),    # partial rotary: tail vectors copied
+    ("bf16", "gptj", 2, 64, 64),
+    ("fp16", "neox", 8, 128, 128),
+    ("e4m3", "neox", 2, 128, 128),
+    ("e4m3", "gptj", 1, 128, 96),
+    ("bf16", "neox", 3, 96, 96),     # 12-vector columns: the pair-task kernel
+])
+@pytest.mark.parametrize("kernel", ["auto", "pairs"])
+def test_rerotate_kx_layout_matches_oracle(gpu, monkeypatch, dt, style, heads, head_dim,
+                                           rot_dim, kernel):
+    """Split-x K pages (vLLM PagedAttention layout) re-rotated by the kernel
+    equal the oracle's token-major re-rotation of the same pages moved into
+    [block_size][H][D] order and back (oracle.kx_to_nhd, pinned by a brute
+    force index test); V and unrotated pages bit-exact."""
+    print(f"case: kx re-rotate {dt} {style} H{heads} D{head_dim} R{rot_dim} {kernel}",
+          flush=True)
+    if kernel == "pairs":
+        monkeypatch.setenv("DSR_ROT_KERNEL", "pairs")
+    bs, L = 16, 3
+    shape = KVShape(L, heads, head_dim, bs, 1 if dt == "e4m3" else 2)
+    rng = np.random.default_rng(17)
+    deltas = (0, 5, 4097, 32767)
+    chunk_pages = [2, 1, 3, 2]
+    n = sum(chunk_pages)
+    nb = n + 5
+    geo = dict(block_size=bs, head_dim=head_dim)
+    src = _flat_caches(shape, nb, dt, gpu, seed=21, scale=2.0)
+    staging = torch.zeros(n * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    offs = np.arange(n, dtype=np.int64) * shape.slot_bytes
+    ops.gather(ops.LayerTable(src, **geo), rng.permutation(nb)[:n].astype(np.int32), offs,
+               staging)
+    dst = _flat_caches(shape, nb, dt, gpu, seed=22)
+    before = [to_bits_np(c, dt) for c in dst]
+    page_ids = rng.permutation(nb)[:n].astype(np.int32)
+    ridx, uniq = position.page_rope_index(chunk_pages, deltas)
+    tabs = position.delta_tables(uniq, rot_dim, 500000.0, device=gpu)
+    ks_np = k_scale = None
+    if dt == "e4m3":
+        ks_np = rng.random(L).astype(np.float32) * 0.5 + 0.01
+        k_scale = torch.from_numpy(ks_np).to(gpu)
+    table = ops.LayerTable(dst, **geo)
+    assert table.layout.k_layout == "kx" and table.layout.num_heads == heads
+    ops.scatter_rerotate(table, page_ids, offs, staging, tabs, ridx, rot_dim=rot_dim,
+                         style=style, k_scale=k_scale)
+    # oracle in token-major order: permute caches and records, rotate, compare
+    to_nhd = lambda a: oracle.kx_to_nhd(a, bs, heads, head_dim)  # noqa: E731
+    ref = [np.ascontiguousarray(to_nhd(b)) for b in before]
+    el = np.uint8 if dt == "e4m3" else np.uint16
+    recs = staging.cpu().numpy().view(el).reshape(n, L, 2, -1)
+    recs_nhd = np.ascontiguousarray(to_nhd(recs)).reshape(-1).view(np.uint8)
+    page_delta = np.repeat(np.asarray(deltas, np.int64), chunk_pages)
+    oracle.scatter_rerotate(
+        ref, page_ids, offs, recs_nhd, shape.layer_bytes, dtype=ORC_DT[dt], rot_dim=rot_dim,
+        style=0 if style == "neox" else 1, stored_pos=np.zeros(n, np.int64),
+        new_pos=page_delta, rotate=page_delta != 0, theta=500000.0, k_scale=ks_np)
+    torch.cuda.synchronize()
+    touched = np.zeros(nb, bool)
+    touched[page_ids] = True
+    for l in range(L):
+        got = to_nhd(to_bits_np(dst[l], dt))
+        assert np.array_equal(got[1], ref[l][1]), f"layer {l}: V"
+        assert np.array_equal(got[:, ~touched], ref[l][:, ~touched]), f"layer {l}: untouched"
+        ok, msg = rotation_within_tolerance(got[0][page_ids], ref[l][0][page_ids], dt)
+        assert ok, f"layer {l}: {msg}"
+        still = page_ids[page_delta == 0]
+        assert np.array_equal(got[0][still], ref[l][0][still]), f"layer {l}: delta 0 copy"

@@ -396,3 +396,22 @@ def test_slot_gather_equals_page_gather_on_valid_tokens():
         assert np.array_equal(bt[:, valid], ct[:, valid])
         others = np.setdiff1d(np.arange(nb * bs), valid)
         assert not bt[:, others].any()
+
+
+@pytest.mark.parametrize("itemsize,bs,h,d", [(2, 16, 2, 64), (1, 8, 3, 32), (2, 4, 1, 16)])
+def test_kx_layout_permutation_brute_force(itemsize, bs, h, d):
+    """kx_to_nhd / nhd_to_kx against the split-x index formula evaluated
+    element by element: (t, h, d) at ((h * (D/X) + d/X) * bs + t) * X + d % X."""
+    x = 16 // itemsize
+    dt = np.uint16 if itemsize == 2 else np.uint8
+    n = bs * h * d
+    page = (np.arange(2 * n) % (np.iinfo(dt).max + 1)).astype(dt).reshape(2, n)
+    nhd = oracle.kx_to_nhd(page, bs, h, d)
+    assert nhd.shape == (2, bs, h, d)
+    for p in range(2):
+        for t in range(bs):
+            for hh in range(h):
+                for dd in range(d):
+                    pos = ((hh * (d // x) + dd // x) * bs + t) * x + dd % x
+                    assert nhd[p, t, hh, dd] == page[p, pos]
+    assert np.array_equal(oracle.nhd_to_kx(nhd), page)
