@@ -28,8 +28,11 @@
 //     kv_scatter_rerotate_rows_kernel for other neox rows of <= 64 vectors;
 //     the pair-task kv_scatter_rerotate_kernel otherwise; rotary widths that
 //     are not whole 16-byte vectors: kv_scatter_rerotate_lds_kernel.
-//   token form (dsr_gather_slots / dsr_scatter_slots): kv_slots_small_kernel
-//     for rows of <= 32 vectors, kv_slots_kernel above.
+//   token form (dsr_gather_slots / dsr_scatter_slots): kv_slots_packed_kernel
+//     for power-of-two rows of <= 8 vectors, kv_slots_small_kernel for other
+//     rows of <= 32 vectors, kv_slots_kernel above.
+//   split-x K pages (dsr_scatter_rerotate_kx): the contig and grouped
+//     kernels with the KX flag, or the pair-task kernel.
 // Calls too large for one launch run as several over page (token) ranges.
 //
 // Reference being replaced: the Python per-(request, block, layer) torch
@@ -525,7 +528,16 @@ int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t 
   int tpw = vpr <= 16 ? 8 : vpr <= 32 ? 4 : 0;
   if (const char* e = getenv("DSR_SLOTS_TPW"))  // tuning override for small rows
     if (tpw && (atoi(e) == 4 || atoi(e) == 8 || atoi(e) == 16)) tpw = atoi(e);
-  const int tok_wg = tpw ? tpw * (kThreads / kWave) : kTokPerWg;
+  // power-of-two rows of <= 8 vectors: the packed kernel, U instructions
+  // per wave (4 and 8 measured alike; 16 spills)
+  int pk_u = vpr <= 8 && (vpr & (vpr - 1)) == 0 && (block_size & (block_size - 1)) == 0 ? 8 : 0;
+  if (const char* e = getenv("DSR_SLOTS_KERNEL"))
+    if (!strcmp(e, "small")) pk_u = 0;
+  if (const char* e = getenv("DSR_SLOTS_UNROLL"))
+    if (pk_u && (atoi(e) == 4 || atoi(e) == 8)) pk_u = atoi(e);
+  const int pk_s = pk_u ? __builtin_ctzll((unsigned long long)vpr) : 0;
+  const int tok_wg = pk_u ? (kWave >> pk_s) * pk_u * (kThreads / kWave)
+                     : tpw ? tpw * (kThreads / kWave) : kTokPerWg;
   const int64_t blocks = ((int64_t)n_tokens + tok_wg - 1) / tok_wg;
   if (blocks * n_layers > 0x7fffffffLL) return DSR_ERR_ARG;
   SlotArgs a;
@@ -556,7 +568,17 @@ int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t 
     b.n_tokens = (int32_t)(n_tokens - t0 < per ? n_tokens - t0 : per);
     const int64_t units = ((int64_t)b.n_tokens + tok_wg - 1) / tok_wg * n_layers;
     const unsigned grid = (unsigned)(gather ? units : (units + kXcds - 1) / kXcds * kXcds);
-    if (tpw == 16) {
+    if (pk_u == 8) {
+      if (gather)
+        kv_slots_packed_kernel<true, 8><<<grid, kThreads, 0, s>>>(b, pk_s);
+      else
+        kv_slots_packed_kernel<false, 8><<<grid, kThreads, 0, s>>>(b, pk_s);
+    } else if (pk_u == 4) {
+      if (gather)
+        kv_slots_packed_kernel<true, 4><<<grid, kThreads, 0, s>>>(b, pk_s);
+      else
+        kv_slots_packed_kernel<false, 4><<<grid, kThreads, 0, s>>>(b, pk_s);
+    } else if (tpw == 16) {
       if (gather)
         kv_slots_small_kernel<true, 16><<<grid, kThreads, 0, s>>>(b);
       else

@@ -166,4 +166,74 @@ __global__ __launch_bounds__(kThreads) void kv_slots_small_kernel(SlotArgs a) {
   }
 }
 
+// Rows of 2^s <= 8 vectors (128 B: one e4m3 KV head of 128 dims, one bf16
+// head of 64), packed 64 >> s tokens to a wave instruction: lane = (token
+// sub-slot << s) | vector, so each load and store instruction moves a whole
+// KiB (a token's row is contiguous on both sides), where the kernel above
+// leaves 7/8 of its lanes idle on such rows. Measured on the e4m3 TP8 share
+// (80 layers, 1 KV head, 2 KiB pages), two boxes: 5.2-5.3 / 5.1-5.9 TB/s
+// gather / scatter against 3.6-3.8 / 3.5-3.7. At 16- and 32-vector rows it
+// measured equal or slower than the kernel above (5.1-5.6 vs 5.3-5.7 TB/s
+// gather), which keeps those. Each lane resolves
+// its own token (the 2^s lanes of a token read the same table entries) and
+// uses its own 64-bit global address; U instructions per wave are in flight
+// for K and for V. Invalid tokens' lanes are masked off. Block sizes are
+// powers of two here (vLLM's always are).
+template <bool kGather, int U>
+__global__ __launch_bounds__(kThreads, 4) void kv_slots_packed_kernel(SlotArgs a, int s) {
+  const int tpi = kWave >> s;
+  const int64_t tok_wg = (int64_t)tpi * U * (kThreads / kWave);
+  int64_t unit = blockIdx.x;
+  if (!kGather) {
+    const int64_t nu = ((int64_t)a.n_tokens + tok_wg - 1) / tok_wg * a.n_layers;
+    unit = layer_major_unit(nu, a.n_layers);
+    if (unit < 0) return;
+  }
+  const int64_t tb = unit / a.n_layers;
+  const int l = (int)(unit - tb * a.n_layers);
+  const int wave = (int)threadIdx.x / kWave, lane = (int)threadIdx.x % kWave;
+  const int64_t vo = (int64_t)(lane & ((1 << s) - 1)) << 4;
+  const int64_t t0 = tb * tok_wg + (int64_t)wave * tpi * U + (lane >> s);
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(a.layer_base[l]);
+  const int64_t lofs = (int64_t)(a.layer0 + l) * a.layer_bytes;
+  int64_t slot[U], roff[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {  // every table load first
+    const int64_t t = t0 + (int64_t)k * tpi;
+    const bool live = t < a.n_tokens;
+    slot[k] = live ? a.slot_mapping[t] : -1;
+    roff[k] = live ? a.row_offsets[t] : -1;
+  }
+  const int64_t sv = kGather ? a.kv_stride : a.page_bytes;  // K -> V, source side
+  const int64_t dvs = kGather ? a.page_bytes : a.kv_stride;  // K -> V, destination side
+  const uint8_t* src[U];
+  uint8_t* dst[U];
+  bool ok[U];
+  u32x4 xk[U], xv[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    // power-of-two block sizes only (the launcher checks): a shift and a mask
+    const int64_t blk = slot[k] >> a.block_shift;  // -1 for padding slots
+    const int64_t off = roff[k] + lofs;
+    ok[k] = slot[k] >= 0 && blk < a.num_blocks && roff[k] >= 0 &&
+            off + a.page_bytes + a.row_bytes <= a.staging_bytes;
+    uint8_t* cache = const_cast<uint8_t*>(base) + blk * a.page_stride +
+                     (slot[k] & (a.block_size - 1)) * a.row_bytes + vo;
+    uint8_t* rec = a.staging + off + vo;
+    src[k] = kGather ? cache : rec;
+    dst[k] = kGather ? rec : cache;
+    if (ok[k]) {
+      xk[k] = *reinterpret_cast<const u32x4*>(src[k]);
+      xv[k] = *reinterpret_cast<const u32x4*>(src[k] + sv);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    if (ok[k]) {
+      *reinterpret_cast<u32x4*>(dst[k]) = xk[k];
+      *reinterpret_cast<u32x4*>(dst[k] + dvs) = xv[k];
+    }
+  }
+}
+
 }  // namespace

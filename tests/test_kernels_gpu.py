@@ -427,11 +427,19 @@ def test_rerotate_special_values(gpu, dt):
     KVShape(5, 2, 128, 16, 2),     # 512-byte rows (32 vectors)
     KVShape(4, 4, 128, 16, 2),     # 1 KiB rows: the large-row kernel
     KVShape(5, 1, 128, 16, 1),     # e4m3, 128-byte rows
-], ids=["cfg1", "row128", "row512", "row1k", "e4m3_row128"])
-def test_slots_gather_scatter_match_oracle(gpu, shape):
+    KVShape(3, 1, 32, 32, 2),      # 64-byte rows (4 vectors), block size 32
+    KVShape(3, 1, 16, 8, 1),       # 16-byte rows (1 vector)
+    KVShape(3, 1, 64, 12, 2),      # 128-byte rows, block size 12 (not a power of two)
+], ids=["cfg1", "row128", "row512", "row1k", "e4m3_row128", "row64_bs32", "row16",
+        "row128_bs12"])
+@pytest.mark.parametrize("unroll", ["default", "4"])
+def test_slots_gather_scatter_match_oracle(gpu, monkeypatch, shape, unroll):
     """slot_mapping-driven token gather/scatter with ragged requests, partial
-    last pages and padding tokens, at each row-size class of the kernels."""
-    print(f"case: slots gather/scatter {shape}", flush=True)
+    last pages and padding tokens, at each row-size class of the kernels
+    (rows of <= 8 vectors: the packed kernel, at both unrolls)."""
+    print(f"case: slots gather/scatter {shape} unroll {unroll}", flush=True)
+    if unroll != "default":
+        monkeypatch.setenv("DSR_SLOTS_UNROLL", unroll)
     wl = workloads.config(1) if shape is None else workloads.ragged(
         shape, 8, 100, 2000, seed=3, num_blocks=1024)
     shape = wl.shape
