@@ -404,7 +404,7 @@ class DaserConnector(KVConnectorBase_V1):
             logger.warning("[CONNECTOR] save_kv_layer: unknown layer %s, skipping", layer_name)
             return
         if self._plane.save_mode == "per_layer":
-            self._plane.save_layer(layer_name, self._store_plan, self._store_arena)
+            self._plane.save_layer(layer_name, self._store_plan, self._store_arena, kv_layer)
         self._saved_layers.add(self._plane.layer_idx[layer_name])
 
     def wait_for_save(self) -> None:

@@ -11,11 +11,14 @@ restate the reference's record layout (daser/connector/daser_connector.py:
 
 from __future__ import annotations
 
+import logging
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Optional
 
 import numpy as np
 import torch
+
+logger = logging.getLogger("daser_amd.connector")
 
 if TYPE_CHECKING:  # the request specs live with the connector's metadata
     from daser_amd.connector import ReqLoadSpec, ReqStoreSpec
@@ -174,6 +177,9 @@ class KVDataPlane:
         self._idle_stream: Optional[torch.cuda.Stream] = None
         self._pending_writes: list = []
         self.table = None
+        self._table_geometry: dict = {}
+        self._cache_ptrs: list[int] = []
+        self._warned_layers: set[int] = set()
         self.layer_names: list[str] = []
         self.layer_idx: dict[str, int] = {}
         self.slot_bytes = 0
@@ -191,6 +197,8 @@ class KVDataPlane:
         if caches and caches[0].dim() != 5:  # the shape carries no head geometry
             geo = {k: v for k, v in self.cache_geometry.items() if v is not None}
         self.table = ops.LayerTable(caches, **geo)
+        self._table_geometry = geo
+        self._cache_ptrs = [c.data_ptr() for c in caches]
         lay = self.table.layout
         derived = lay.slot_bytes
         if slot_size and slot_size != derived:
@@ -284,13 +292,36 @@ class KVDataPlane:
         self._side.wait_event(self._save_ev)
         return self._side.cuda_stream
 
-    def save_layer(self, layer_name: str, plan: StorePlan, arena: torch.Tensor) -> None:
+    def save_layer(self, layer_name: str, plan: StorePlan, arena: torch.Tensor,
+                   kv_layer: Optional[torch.Tensor] = None) -> None:
         """Gathers one layer's pages of every store request. With
         save_stream="side" the gather runs on a side stream after the KV
-        writes already enqueued, overlapping the model's later layers."""
+        writes already enqueued, overlapping the model's later layers.
+        ``kv_layer`` is the tensor the hook received; the reference copies
+        from it (daser_connector.py:627-632), so one that is not the
+        registered cache of that layer is gathered from instead (a one-off
+        launch through its own table, with a warning)."""
+        from daser_amd import ops
+
         if plan.gather is None:
             return
-        plan.gather(self.layer_idx[layer_name], 1, self._save_stream(plan))
+        l = self.layer_idx[layer_name]
+        if kv_layer is not None and kv_layer.data_ptr() != self._cache_ptrs[l]:
+            if l not in self._warned_layers:
+                self._warned_layers.add(l)
+                logger.warning("[CONNECTOR] save_kv_layer(%s): the tensor passed is not the "
+                               "registered cache; gathering from the tensor passed",
+                               layer_name)
+            table = ops.LayerTable([kv_layer], **self._table_geometry)
+            if table.layout.layer_bytes != self.table.layout.layer_bytes:
+                raise ValueError(f"save_kv_layer({layer_name}): cache layout differs from the "
+                                 "registered caches")
+            ids, offs = plan.gather.tables
+            stream = self._save_stream(plan)
+            with torch.cuda.stream(torch.cuda.ExternalStream(stream, device=self.device)):
+                ops.gather(table, ids, offs, arena, layer0=l)
+            return
+        plan.gather(l, 1, self._save_stream(plan))
 
     def save_all(self, plan: StorePlan, arena: torch.Tensor) -> None:
         if plan.gather is None:

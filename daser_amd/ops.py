@@ -294,6 +294,7 @@ class PreparedGather:
                  *, layer0: int = 0) -> None:
         args, self._keep = _copy_args(table, page_ids, slot_offsets, staging, layer0, None,
                                       records_written=True)
+        self.tables = self._keep  # (page_ids, slot_offsets) as device tensors
         self._table = table
         self._staging = staging
         self._mid = args[2:12]  # strides, page geometry, tables, staging

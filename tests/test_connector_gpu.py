@@ -583,3 +583,25 @@ def test_flat_caches_save_and_rerotate_load(gpu, tmp_path):
         assert ok, f"layer {l}: {msg}"
     w.shutdown()
     w2.shutdown()
+
+
+def test_save_gathers_from_the_tensor_passed(gpu, tmp_path, caplog):
+    """save_kv_layer copies from the kv_layer it receives, as the reference
+    does (daser_connector.py:627-632): a tensor that is not the registered
+    cache of that layer is gathered from, with one warning."""
+    print("case: connector save from passed tensor", flush=True)
+    w, _ = _worker(tmp_path)
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=36)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    other = rand_caches(SHAPE, 16, "bf16", gpu, seed=37)
+    passed = dict(named)
+    passed["model.layers.1.self_attn.attn"] = other[1]
+    with caplog.at_level("WARNING", logger="daser_amd.connector"):
+        _save(w, passed, _store_reqs())
+    assert "not the registered cache" in caplog.text
+    host = [to_bits_np(c, "bf16") for c in (caches[0], other[1], caches[2])]
+    ref = np.zeros(3 * SHAPE.slot_bytes, dtype=np.uint8)
+    oracle.gather(host, [5, 9, 2], np.arange(3) * SHAPE.slot_bytes, ref, SHAPE.layer_bytes)
+    assert np.array_equal(_file_records(tmp_path / "daser.store", 3, 3), ref)
+    w.shutdown()
