@@ -226,19 +226,22 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
     if (const char* e = getenv("DSR_ROT_GROUPED_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
   }
   const size_t dyn = rot_occupancy_lds(wg);
-  return launch_page_ranges(ra.u, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
+  // units per workgroup of the kernel actually launched: the one-unit
+  // kernels (an override may pick contig where G > 1) take one
+  const int GL = grouped ? G : 1;
+  return launch_page_ranges(ra.u, n_pages, GL, [&](const UnitArgs& b, unsigned grid) {
     RotArgs rb = ra;
     rb.u = b;
     rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
     if (grouped) {
       if (style == DSR_ROPE_NEOX && kx)
-        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX, true><<<grid, kThreads, dyn, s>>>(rb, G);
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX, true><<<grid, kThreads, dyn, s>>>(rb, GL);
       else if (style == DSR_ROPE_NEOX)
-        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX, false><<<grid, kThreads, dyn, s>>>(rb, G);
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX, false><<<grid, kThreads, dyn, s>>>(rb, GL);
       else if (kx)
-        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ, true><<<grid, kThreads, dyn, s>>>(rb, G);
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ, true><<<grid, kThreads, dyn, s>>>(rb, GL);
       else
-        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ, false><<<grid, kThreads, dyn, s>>>(rb, G);
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ, false><<<grid, kThreads, dyn, s>>>(rb, GL);
     } else if (contig) {
       if (style == DSR_ROPE_NEOX && kx)
         kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX, true><<<grid, kThreads, dyn, s>>>(rb);

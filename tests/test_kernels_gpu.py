@@ -846,6 +846,25 @@ def test_random_geometry_slots_parity(gpu, dt, D, H, bs, style, R, L, seed):
         assert np.array_equal(to_bits_np(dst[l], dt), dref[l]), f"layer {l}"
 
 
+@pytest.mark.parametrize("heads,head_dim,dt", [(1, 128, "bf16"), (1, 128, "e4m3"),
+                                              (2, 64, "bf16")])
+def test_rerotate_contig_override_on_small_pages(gpu, monkeypatch, heads, head_dim, dt):
+    """Small pages default to the grouped kernel; DSR_ROT_KERNEL=contig runs
+    the one-unit contig kernel instead, which must then be launched with one
+    unit per workgroup (every page written, same bits as the grouped
+    kernel)."""
+    print(f"case: contig override H{heads} D{head_dim} {dt}", flush=True)
+    shape, dst, dst_ref, page_ids, _ = _rerotate_case(gpu, dt, "neox", head_dim, head_dim,
+                                                      heads=heads, layers=3, seed=8)
+    monkeypatch.setenv("DSR_ROT_KERNEL", "contig")
+    shape2, dst2, _, page_ids2, _ = _rerotate_case(gpu, dt, "neox", head_dim, head_dim,
+                                                   heads=heads, layers=3, seed=8)
+    torch.cuda.synchronize()
+    assert np.array_equal(page_ids, page_ids2)
+    for a, b in zip(dst, dst2):
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+
+
 @pytest.mark.parametrize("heads,head_dim,dt,kernel", [
     (8, 128, "bf16", None),    # grouped kernel, one unit per workgroup
     (1, 128, "bf16", None),    # grouped, several units per workgroup
