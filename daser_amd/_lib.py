@@ -20,7 +20,7 @@ LIB_PATH = os.environ.get("DASER_KV_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so"
 )
 
-DSR_ABI_VERSION = 3
+DSR_ABI_VERSION = 4
 DSR_OK = 0
 DSR_ERR_ARG = -1
 DSR_ERR_ALIGN = -2
@@ -38,6 +38,8 @@ DSR_DTYPE_FP8_E4M3 = 2
 
 DSR_ROPE_NEOX = 0
 DSR_ROPE_GPTJ = 1
+
+DSR_REROTATE_SHARED_RECORDS = 1
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -60,11 +62,11 @@ SIGNATURES = {
     "dsr_ring_last_errno": ([_P], _I),
     "dsr_ring_close": ([_P], _I),
     "dsr_scatter_rerotate": (
-        _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P],
+        _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, ctypes.c_uint, _P],
         _I,
     ),
     "dsr_scatter_rerotate_kx": (
-        _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _P],
+        _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, ctypes.c_uint, _P],
         _I,
     ),
 }

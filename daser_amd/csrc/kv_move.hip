@@ -165,9 +165,11 @@ constexpr int rot_grouped_wg_per_cu() {
 // config 3 7.05 ms at 2-3 per CU, 7.36 at 4-5 (the contig kernel 7.68);
 // config 5 55.1 ms at 2-3, 50.4 at 4-6 (contig 55.4), where the shared
 // source chunks' reads hit the memory-side cache. 3 is taken for the
-// HBM-bound case. e4m3 keeps the contig kernel (24.05 vs 24.22 ms at
-// config 4).
+// HBM-bound case, 4 when the caller flags shared records
+// (DSR_REROTATE_SHARED_RECORDS). e4m3 keeps the contig kernel (24.05 vs
+// 24.22 ms at config 4).
 constexpr int kRotSingleWgPerCu = 3;
+constexpr int kRotSingleSharedWgPerCu = 4;
 // Dynamic LDS that limits the re-rotation kernel to kRotWgPerCu workgroups
 // per CU on the current device (0 if the capacity cannot be read).
 size_t rot_occupancy_lds(int wg_per_cu) {
@@ -182,7 +184,7 @@ size_t rot_occupancy_lds(int wg_per_cu) {
 
 template <int DT>
 int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipStream_t s,
-                    bool kx = false) {
+                    bool kx, unsigned flags) {
   const int h = ra.half_vecs;
   int wg = rot_wg_per_cu<DT>();
   if (const char* e = getenv("DSR_ROT_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
@@ -222,7 +224,9 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
     if (!strcmp(e, "grouped") && (G > 1 || single)) grouped = true;
   }
   if (grouped) {
-    wg = G > 1 ? rot_grouped_wg_per_cu<DT>() : kRotSingleWgPerCu;
+    wg = G > 1 ? rot_grouped_wg_per_cu<DT>()
+         : (flags & DSR_REROTATE_SHARED_RECORDS) ? kRotSingleSharedWgPerCu
+                                                 : kRotSingleWgPerCu;
     if (const char* e = getenv("DSR_ROT_GROUPED_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
   }
   const size_t dyn = rot_occupancy_lds(wg);
@@ -363,7 +367,8 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
                          const int32_t* rope_idx, int n_tables,
                          const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
-                         const float* k_scale, int kx_block, dsr_stream_t stream) {
+                         const float* k_scale, int kx_block, unsigned flags,
+                         dsr_stream_t stream) {
   int rc = check_common(layer_base, n_layers, kv_stride, page_stride, page_bytes,
                         num_blocks, page_ids, slot_offsets, n_pages, staging,
                         staging_bytes, layer_bytes, layer0);
@@ -439,11 +444,11 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
       ra.row_vecs = (int)hv;
       switch (dtype) {
         case DSR_DTYPE_BF16:
-          return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, true, s, true);
+          return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, true, s, true, flags);
         case DSR_DTYPE_FP16:
-          return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, true, s, true);
+          return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, true, s, true, flags);
         default:
-          return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, true, s, true);
+          return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, true, s, true, flags);
       }
     }
     switch (dtype) {
@@ -457,11 +462,11 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
   }
   switch (dtype) {
     case DSR_DTYPE_BF16:
-      return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, vec_ok, s);
+      return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, vec_ok, s, false, flags);
     case DSR_DTYPE_FP16:
-      return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, vec_ok, s);
+      return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, vec_ok, s, false, flags);
     default:
-      return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, vec_ok, s);
+      return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, vec_ok, s, false, flags);
   }
 }
 
@@ -479,12 +484,12 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          const int32_t* rope_idx, int n_tables,
                          const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
-                         const float* k_scale, dsr_stream_t stream) {
+                         const float* k_scale, unsigned flags, dsr_stream_t stream) {
   return scatter_rerotate_any(layer_base, n_layers, kv_stride, page_stride, page_bytes,
                               num_blocks, page_ids, slot_offsets, n_pages, staging,
                               staging_bytes, layer_bytes, layer0, cos_sin, rope_idx, n_tables,
                               layer_group, n_groups, head_dim, rot_dim, rope_style, dtype,
-                              k_scale, 0, stream);
+                              k_scale, 0, flags, stream);
 }
 
 int dsr_scatter_rerotate_kx(const uint64_t* layer_base, int n_layers,
@@ -497,13 +502,14 @@ int dsr_scatter_rerotate_kx(const uint64_t* layer_base, int n_layers,
                             const int32_t* rope_idx, int n_tables,
                             const int32_t* layer_group, int n_groups, int head_dim,
                             int rot_dim, int rope_style, int dtype,
-                            const float* k_scale, int block_size, dsr_stream_t stream) {
+                            const float* k_scale, int block_size, unsigned flags,
+                            dsr_stream_t stream) {
   if (block_size <= 0) return DSR_ERR_ARG;
   return scatter_rerotate_any(layer_base, n_layers, kv_stride, page_stride, page_bytes,
                               num_blocks, page_ids, slot_offsets, n_pages, staging,
                               staging_bytes, layer_bytes, layer0, cos_sin, rope_idx, n_tables,
                               layer_group, n_groups, head_dim, rot_dim, rope_style, dtype,
-                              k_scale, block_size, stream);
+                              k_scale, block_size, flags, stream);
 }
 
 namespace {

@@ -51,6 +51,7 @@ class LoadPlan:
     reads: list[tuple[int, int, int]]  # (arena_off, nbytes, file_off)
     arena_bytes: int
     page_read: np.ndarray = field(default_factory=lambda: np.zeros(0, np.int64))  # read of each page
+    shared_records: bool = False  # some records are scattered to several pages
 
 
 def plan_store(reqs: dict[str, ReqStoreSpec], slot_bytes: int) -> StorePlan:
@@ -74,11 +75,17 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
     """Each segment's records are read once into the arena; page j of a
     segment scatters record j into block_ids[block_offset + j]. A segment
     whose new position differs from its stored one gets a rotation table for
-    delta = new_pos - pos_offset (reference :498-551 for the unrotated part)."""
+    delta = new_pos - pos_offset (reference :498-551 for the unrotated part).
+    A segment whose store slots lie inside a range already read this step
+    (the same cached chunk hit by several requests) reads nothing and
+    scatters from that range; the reference reads it once per request."""
     ids: list[int] = []
-    seg_pages, seg_table, reads = [], [], []
+    src: list[np.ndarray] = []
+    seg_pages, seg_table, seg_read, reads = [], [], [], []
+    read_slots: list[tuple[int, int]] = []  # (start_slot, num_slots) of each read
     table: dict[int, int] = {}
     base = 0
+    shared = False
     for spec in reqs.values():
         blocks = spec.block_ids
         if not blocks:
@@ -89,18 +96,28 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
                 continue
             if seg.block_offset < 0 or seg.block_offset + n > len(blocks):
                 raise ValueError(f"segment of {spec.chunk_key[:8]} exceeds its block list")
-            reads.append((base, n * slot_bytes, seg.start_slot * slot_bytes))
+            hit = next((i for i, (s0, m) in enumerate(read_slots)
+                        if s0 <= seg.start_slot and seg.start_slot + n <= s0 + m), None)
+            if hit is None:
+                hit = len(reads)
+                reads.append((base, n * slot_bytes, seg.start_slot * slot_bytes))
+                read_slots.append((seg.start_slot, n))
+                base += n * slot_bytes
+            else:
+                shared = True
+            first = reads[hit][0] + (seg.start_slot - read_slots[hit][0]) * slot_bytes
+            src.append(first + np.arange(n, dtype=np.int64) * slot_bytes)
             delta = 0 if seg.new_pos is None else int(seg.new_pos) - int(seg.pos_offset)
             seg_table.append(-1 if delta == 0 else table.setdefault(delta, len(table)))
             seg_pages.append(n)
+            seg_read.append(hit)
             ids.extend(blocks[seg.block_offset:seg.block_offset + n])
-            base += n * slot_bytes
-    # segments' records are packed back to back: page k at k * SLOT
     counts = np.asarray(seg_pages, np.int64)
     return LoadPlan(np.asarray(ids, np.int32),
-                    np.arange(len(ids), dtype=np.int64) * slot_bytes,
+                    np.concatenate(src) if src else np.zeros(0, np.int64),
                     np.repeat(np.asarray(seg_table, np.int32), counts), list(table.keys()),
-                    reads, base, np.repeat(np.arange(len(reads), dtype=np.int64), counts))
+                    reads, base, np.repeat(np.asarray(seg_read, np.int64), counts),
+                    shared_records=shared)
 
 
 # ---------------------------------------------------------------------------
@@ -469,7 +486,8 @@ class KVDataPlane:
                 ops.scatter_rerotate(self.table, plan.page_ids[sel], src, buf, tabs,
                                      plan.rope_idx[sel], rot_dim=self.rotary_dim,
                                      style=self.rope_style, k_scale=self.k_scales,
-                                     layer_group=self._layer_group)
+                                     layer_group=self._layer_group,
+                                     shared_records=plan.shared_records)
             if self.device.type == "cuda":
                 done[i] = torch.cuda.Event()
                 done[i].record(torch.cuda.current_stream(self.device))

@@ -342,6 +342,7 @@ def scatter_rerotate(
     layer0: int = 0,
     layers: Optional[tuple[int, int]] = None,
     layer_group=None,
+    shared_records: Optional[bool] = None,
 ) -> None:
     """Scatter with K re-rotated by ``cos_sin[rope_idx[p]]`` (-1 = copy).
 
@@ -351,6 +352,11 @@ def scatter_rerotate(
     (other frequencies, or none), ``cos_sin`` is ``[n_groups, n_tables,
     rot_dim/2, 2]`` and ``layer_group[layer0 + l]`` picks layer l's group
     (-1: no RoPE, K copied).
+
+    ``shared_records``: several pages read the same records (a cached chunk
+    placed in several requests); shapes the launch for cache-served reads.
+    None: inferred from host ``slot_offsets`` (at most half of them
+    distinct), False for device tables. Results do not depend on it.
     """
     lay = table.layout
     if lay.dtype not in _DTYPE_CODES:
@@ -378,6 +384,10 @@ def scatter_rerotate(
                                (lg.size and (lg.min() < -1 or lg.max() >= n_groups))):
             raise IndexError("layer_group needs one group in [-1, n_groups) per layer")
         lg_d = _as_device_table(layer_group, torch.int32, lay.device, "layer_group")
+    if shared_records is None:
+        offs_h = _host_array(slot_offsets, np.int64)
+        shared_records = offs_h is not None and offs_h.size > 1 and \
+            2 * np.unique(offs_h).size <= offs_h.size
     page_ids, slot_offsets, rope_idx = dest_order(page_ids, slot_offsets, rope_idx)
     args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
     ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")
@@ -397,12 +407,13 @@ def scatter_rerotate(
     common = (*args, cos_sin.data_ptr(), ridx_d.data_ptr(), n_tables,
               None if lg_d is None else lg_d.data_ptr(), n_groups if grouped else 0,
               lay.head_dim, rot_dim, ROPE_STYLES[style], _DTYPE_CODES[lay.dtype], ks_ptr)
+    flags = _lib.DSR_REROTATE_SHARED_RECORDS if shared_records else 0
     if lay.k_layout == "kx":
-        rc = _lib.lib().dsr_scatter_rerotate_kx(*common, lay.block_size,
+        rc = _lib.lib().dsr_scatter_rerotate_kx(*common, lay.block_size, flags,
                                                 _stream_handle(lay.device))
         _lib.check("dsr_scatter_rerotate_kx", rc)
     else:
-        rc = _lib.lib().dsr_scatter_rerotate(*common, _stream_handle(lay.device))
+        rc = _lib.lib().dsr_scatter_rerotate(*common, flags, _stream_handle(lay.device))
         _lib.check("dsr_scatter_rerotate", rc)
 
 

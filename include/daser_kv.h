@@ -44,7 +44,7 @@ extern "C" {
 
 typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 
-#define DSR_ABI_VERSION 3
+#define DSR_ABI_VERSION 4
 
 /*
  * Kernel choice and launch shape follow from the geometry; these environment
@@ -74,6 +74,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 /* RoPE pairings. */
 #define DSR_ROPE_NEOX 0 /* rotate-half: pairs (j, j + rot_dim/2)  (Llama) */
 #define DSR_ROPE_GPTJ 1 /* interleaved: pairs (2j, 2j + 1)                */
+
+/* dsr_scatter_rerotate* flags */
+#define DSR_REROTATE_SHARED_RECORDS 1u
 
 /* Returns DSR_ABI_VERSION. */
 int dsr_abi_version(void);
@@ -163,6 +166,11 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
  *   k_scale   [device] per-layer fp32 scales, indexed layer0 + l; required
  *             for fp8, ignored otherwise (may be null). There is no V scale:
  *             V is copied as raw bytes, never decoded.
+ *   flags     0, or DSR_REROTATE_SHARED_RECORDS when several pages of the
+ *             call read the same records (one cached chunk placed in several
+ *             requests): their repeated reads are served by the caches, and
+ *             the launch is shaped for that (more workgroups per CU). A
+ *             performance hint only: results are identical either way.
  */
 int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          int64_t kv_stride, int64_t page_stride,
@@ -174,7 +182,7 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          const int32_t* rope_idx, int n_tables,
                          const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
-                         const float* k_scale, dsr_stream_t stream);
+                         const float* k_scale, unsigned flags, dsr_stream_t stream);
 
 /*
  * dsr_scatter_rerotate for caches whose K page uses the split-x layout of
@@ -203,7 +211,8 @@ int dsr_scatter_rerotate_kx(const uint64_t* layer_base, int n_layers,
                             const int32_t* rope_idx, int n_tables,
                             const int32_t* layer_group, int n_groups, int head_dim,
                             int rot_dim, int rope_style, int dtype,
-                            const float* k_scale, int block_size, dsr_stream_t stream);
+                            const float* k_scale, int block_size, unsigned flags,
+                            dsr_stream_t stream);
 
 /*
  * Token-granular offload gather driven by vLLM's slot_mapping: for every

@@ -99,7 +99,7 @@ int main() {
   rc = dsr_scatter_rerotate(bases + L, L, NB * page, page, page, NB, d_ids, d_offs, n, stg,
                             n * slot, layer_bytes, 0, tab, ridx, 1, nullptr, 0, D, D,
                             DSR_ROPE_NEOX,
-                            DSR_DTYPE_BF16, nullptr, nullptr);
+                            DSR_DTYPE_BF16, nullptr, 0u, nullptr);
   REQUIRE(rc == 0, dsr_error_string(rc));
   std::vector<uint8_t> c3(L * cache_bytes);
   hipMemcpy(c3.data(), cache2, c3.size(), hipMemcpyDeviceToHost);
@@ -108,13 +108,14 @@ int main() {
   hipMemset(cache2, 0, L * cache_bytes);
   rc = dsr_scatter_rerotate_kx(bases + L, L, NB * page, page, page, NB, d_ids, d_offs, n, stg,
                                n * slot, layer_bytes, 0, tab, ridx, 1, nullptr, 0, D, D,
-                               DSR_ROPE_NEOX, DSR_DTYPE_BF16, nullptr, bs, nullptr);
+                               DSR_ROPE_NEOX, DSR_DTYPE_BF16, nullptr, bs,
+                               DSR_REROTATE_SHARED_RECORDS, nullptr);
   REQUIRE(rc == 0, dsr_error_string(rc));
   hipMemcpy(c3.data(), cache2, c3.size(), hipMemcpyDeviceToHost);
   REQUIRE(c3 == c2, "unrotated split-x re-rotate scatter equals plain scatter");
   REQUIRE(dsr_scatter_rerotate_kx(bases + L, L, NB * page, page, page, NB, d_ids, d_offs, n,
                                   stg, n * slot, layer_bytes, 0, tab, ridx, 1, nullptr, 0, D,
-                                  D, DSR_ROPE_NEOX, DSR_DTYPE_BF16, nullptr, 0,
+                                  D, DSR_ROPE_NEOX, DSR_DTYPE_BF16, nullptr, 0, 0u,
                                   nullptr) == DSR_ERR_ARG,
           "split-x without a block size rejected");
 

@@ -67,7 +67,7 @@ def test_rerotate_argument_errors():
     def call(head_dim=128, rot_dim=128, style=0, dtype=0, k_scale=80, n_tables=1,
              layer_group=None, n_groups=0):
         return lib.dsr_scatter_rerotate(*base, 96, 112, n_tables, layer_group, n_groups,
-                                        head_dim, rot_dim, style, dtype, k_scale, None)
+                                        head_dim, rot_dim, style, dtype, k_scale, 0, None)
 
     assert call(style=7) == _lib.DSR_ERR_ARG
     assert call(dtype=9) == _lib.DSR_ERR_ARG
@@ -76,6 +76,11 @@ def test_rerotate_argument_errors():
     assert call(head_dim=100, rot_dim=100) == _lib.DSR_ERR_SHAPE  # page not whole rows
     assert call(dtype=2, k_scale=None) == _lib.DSR_ERR_ARG
     assert call(layer_group=128, n_groups=0) == _lib.DSR_ERR_ARG  # groups without a count
+    # the split-x entry point: a block size is required, and whole-vector widths
+    kx = [*base, 96, 112, 1, None, 0, 128, 128, 0, 0, 80]
+    assert lib.dsr_scatter_rerotate_kx(*kx, 0, 0, None) == _lib.DSR_ERR_ARG
+    kx[19] = 120  # rot_dim 120: half not a whole number of vectors
+    assert lib.dsr_scatter_rerotate_kx(*kx, 16, 0, None) == _lib.DSR_ERR_SHAPE
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -59,11 +59,39 @@ def test_plan_load_positions_and_segments():
     assert p.page_ids.tolist() == [1, 2, 5, 6, 7, 9]
     assert p.deltas == [512]  # 612 - 100 and 512 - 0 share one table
     assert p.rope_idx.tolist() == [0, 0, 0, 0, -1, -1]
+    # r3's slot 0 lies inside r1's read of slots 0-1: no read of its own
     assert p.reads == [(0, 2 * SLOT, 0), (2 * SLOT, 2 * SLOT, 20 * SLOT),
-                       (4 * SLOT, SLOT, 8 * SLOT), (5 * SLOT, SLOT, 0)]
+                       (4 * SLOT, SLOT, 8 * SLOT)]
+    assert p.src_offsets.tolist() == [0, SLOT, 2 * SLOT, 3 * SLOT, 4 * SLOT, 0]
+    assert p.page_read.tolist() == [0, 0, 1, 1, 2, 0] and p.shared_records
     with pytest.raises(ValueError):
         C.plan_load({"x": C.ReqLoadSpec("k", 0, 0, [1], 0, 16, segments=[
             C.LoadSegment(0, 2, 0)])}, SLOT)
+
+
+def test_plan_load_reads_a_shared_chunk_once():
+    """Requests hitting the same cached chunk (or a part of one already read)
+    read it once; each scatters from that read into its own blocks, at its
+    own position."""
+    reqs = {
+        "a": C.ReqLoadSpec("k", 6, 4, [10, 11, 12, 13], 6 * SLOT, 64, pos_offset=0,
+                           new_pos=100),
+        "b": C.ReqLoadSpec("k", 6, 4, [20, 21, 22, 23], 6 * SLOT, 64, pos_offset=0,
+                           new_pos=900),
+        "c": C.ReqLoadSpec("k2", 0, 0, [30, 31], 0, 32, segments=[
+            C.LoadSegment(start_slot=8, num_slots=2, block_offset=0)]),  # inside a's read
+        "d": C.ReqLoadSpec("k3", 9, 2, [40, 41], 9 * SLOT, 32),  # overlaps, not inside
+    }
+    p = C.plan_load(reqs, SLOT)
+    assert p.reads == [(0, 4 * SLOT, 6 * SLOT), (4 * SLOT, 2 * SLOT, 9 * SLOT)]
+    assert p.arena_bytes == 6 * SLOT
+    assert p.page_ids.tolist() == [10, 11, 12, 13, 20, 21, 22, 23, 30, 31, 40, 41]
+    assert p.src_offsets.tolist() == [0, SLOT, 2 * SLOT, 3 * SLOT] * 2 + \
+        [2 * SLOT, 3 * SLOT, 4 * SLOT, 5 * SLOT]
+    assert p.rope_idx.tolist() == [0] * 4 + [1] * 4 + [-1] * 4 and p.deltas == [100, 900]
+    assert p.page_read.tolist() == [0] * 10 + [1, 1] and p.shared_records
+    alone = C.plan_load({"a": reqs["a"], "d": reqs["d"]}, SLOT)
+    assert not alone.shared_records and len(alone.reads) == 2
 
 
 # ---------------------------------------------------------------- scheduler

@@ -846,6 +846,51 @@ def test_random_geometry_slots_parity(gpu, dt, D, H, bs, style, R, L, seed):
         assert np.array_equal(to_bits_np(dst[l], dt), dref[l]), f"layer {l}"
 
 
+@pytest.mark.parametrize("heads,head_dim,dt", [(8, 128, "bf16"), (1, 128, "bf16"),
+                                              (8, 128, "e4m3")])
+def test_shared_records_hint_does_not_change_results(gpu, heads, head_dim, dt):
+    """DSR_REROTATE_SHARED_RECORDS only reshapes the launch: several pages
+    reading the same records give the same bits with and without it (token-
+    major and split-x pages), and match the oracle."""
+    print(f"case: shared-records hint H{heads} D{head_dim} {dt}", flush=True)
+    shape = KVShape(3, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    rng = np.random.default_rng(4)
+    n_src, n = 3, 12
+    nb = n + 4
+    src = rand_caches(shape, nb, dt, gpu, seed=61)
+    recs = torch.zeros(n_src * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(src), [1, 5, 7], np.arange(n_src) * shape.slot_bytes, recs)
+    offs = (np.arange(n) % n_src).astype(np.int64) * shape.slot_bytes  # each record 4 times
+    page_ids = rng.permutation(nb)[:n].astype(np.int32)
+    ridx = (np.arange(n) % 2).astype(np.int32)
+    tabs = position.delta_tables([77, 30001], head_dim, 500000.0, device=gpu)
+    ks = torch.full((3,), 0.05, dtype=torch.float32, device=gpu) if dt == "e4m3" else None
+    outs = []
+    for flat in (False, True):
+        for hint in (False, True):
+            dst = rand_caches(shape, nb, dt, gpu, seed=62)
+            caches = [c.reshape(2, nb, -1) for c in dst] if flat else dst
+            geo = dict(block_size=16, head_dim=head_dim) if flat else {}
+            ops.scatter_rerotate(ops.LayerTable(caches, **geo), page_ids, offs, recs, tabs, ridx,
+                                 k_scale=ks, shared_records=hint)
+            outs.append([to_bits_np(c, dt) for c in dst])
+    torch.cuda.synchronize()
+    for l in range(3):
+        assert np.array_equal(outs[0][l], outs[1][l]), f"layer {l}: token-major"
+        assert np.array_equal(outs[2][l], outs[3][l]), f"layer {l}: split-x"
+    ref = [to_bits_np(c, dt) for c in rand_caches(shape, nb, dt, gpu, seed=62)]
+    delta = np.where(ridx == 0, 77, 30001)
+    oracle.scatter_rerotate(ref, page_ids, offs, recs.cpu().numpy(), shape.layer_bytes,
+                            dtype=ORC_DT[dt], rot_dim=head_dim, style=0,
+                            stored_pos=np.zeros(n, np.int64), new_pos=delta,
+                            rotate=np.ones(n, bool), theta=500000.0,
+                            k_scale=None if ks is None else np.full(3, 0.05, np.float32))
+    for l in range(3):
+        assert np.array_equal(outs[0][l][1], ref[l][1])
+        ok, msg = rotation_within_tolerance(outs[0][l][0][page_ids], ref[l][0][page_ids], dt)
+        assert ok, f"layer {l}: {msg}"
+
+
 @pytest.mark.parametrize("heads,head_dim,dt", [(1, 128, "bf16"), (1, 128, "e4m3"),
                                               (2, 64, "bf16")])
 def test_rerotate_contig_override_on_small_pages(gpu, monkeypatch, heads, head_dim, dt):
