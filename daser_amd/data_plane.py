@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import logging
 from dataclasses import dataclass, field
+from itertools import repeat
 from typing import TYPE_CHECKING, Optional
 
 import numpy as np
@@ -83,6 +84,7 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
     src: list[np.ndarray] = []
     seg_pages, seg_table, seg_read, reads = [], [], [], []
     read_slots: list[tuple[int, int]] = []  # (start_slot, num_slots) of each read
+    slot_read: dict[int, int] = {}  # store slot -> a read covering it
     table: dict[int, int] = {}
     base = 0
     shared = False
@@ -96,12 +98,13 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
                 continue
             if seg.block_offset < 0 or seg.block_offset + n > len(blocks):
                 raise ValueError(f"segment of {spec.chunk_key[:8]} exceeds its block list")
-            hit = next((i for i, (s0, m) in enumerate(read_slots)
-                        if s0 <= seg.start_slot and seg.start_slot + n <= s0 + m), None)
-            if hit is None:
+            # reads are contiguous slot ranges: one covering both ends covers all
+            hit = slot_read.get(seg.start_slot)
+            if hit is None or slot_read.get(seg.start_slot + n - 1) != hit:
                 hit = len(reads)
                 reads.append((base, n * slot_bytes, seg.start_slot * slot_bytes))
                 read_slots.append((seg.start_slot, n))
+                slot_read.update(zip(range(seg.start_slot, seg.start_slot + n), repeat(hit)))
                 base += n * slot_bytes
             else:
                 shared = True
