@@ -118,3 +118,42 @@ def test_rerotate_full_size_properties(gpu, cfg):
         assert ((zf - xf).abs() <= 2 ** -7 * rowmax).all(), f"layer {l}: inverse"
         assert (yf != xf).float().mean() > 0.5, f"layer {l}: K was not rotated"
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("cfg", [3, 6])
+def test_split_x_rerotate_equals_token_major_full_size(gpu, cfg):
+    """At full size, re-rotating split-x pages (vLLM's PagedAttention K
+    layout) gives exactly the bits of re-rotating the same data in token-major
+    pages, after the layout permutation: the two entry points run the same
+    arithmetic per element (the token-major path is pinned to the oracle)."""
+    print(f"case: full-size split-x re-rotate cfg{cfg}", flush=True)
+    wl = workloads.config(cfg)
+    shape = wl.shape
+    L, bs, H, D = shape.num_layers, shape.block_size, shape.num_heads, shape.head_dim
+    X = 16 // shape.elem_bytes
+    src_full, src_caches, _ = bench.fill_caches(torch, shape, wl.num_blocks, "bf16", gpu, seed=62)
+    n = wl.n_pages
+    st = torch.empty(n * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(src_caches), wl.page_ids, wl.slot_offsets, st)
+    del src_caches, src_full
+    ridx, uniq = position.page_rope_index(wl.chunk_pages, wl.chunk_delta)
+    fwd = position.delta_tables(uniq, D, 500000.0, device=gpu)
+    ids = torch.from_numpy(wl.page_ids.astype(np.int64)).to(gpu)
+
+    nhd_full = torch.zeros((L, 2, wl.num_blocks, bs, H, D), dtype=torch.bfloat16, device=gpu)
+    ops.scatter_rerotate(ops.LayerTable([nhd_full[l] for l in range(L)]), wl.page_ids,
+                         wl.slot_offsets, st, fwd, ridx)
+    # the same records with every page in split-x order
+    st_kx = (st.view(torch.bfloat16).view(n, L, 2, bs, H, D // X, X)
+             .permute(0, 1, 2, 4, 5, 3, 6).contiguous().view(-1).view(torch.uint8))
+    del st
+    kx_full = torch.zeros((L, 2, wl.num_blocks, bs * H * D), dtype=torch.bfloat16, device=gpu)
+    ops.scatter_rerotate(ops.LayerTable([kx_full[l] for l in range(L)], block_size=bs,
+                                        head_dim=D),
+                         wl.page_ids, wl.slot_offsets, st_kx, fwd, ridx)
+    for l in range(L):
+        a = nhd_full[l][:, ids]
+        b = (kx_full[l][:, ids].view(2, n, H, D // X, bs, X)
+             .permute(0, 1, 4, 2, 3, 5).reshape(2, n, bs, H, D))
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"layer {l}"
+    torch.cuda.synchronize()
