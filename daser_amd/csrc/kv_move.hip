@@ -172,13 +172,17 @@ constexpr int kRotSingleWgPerCu = 3;
 constexpr int kRotSingleSharedWgPerCu = 4;
 // Dynamic LDS that limits the re-rotation kernel to kRotWgPerCu workgroups
 // per CU on the current device (0 if the capacity cannot be read).
+constexpr int64_t kLdsGranule = 512;
 size_t rot_occupancy_lds(int wg_per_cu) {
   int dev = 0, lds = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
                             dev) != hipSuccess || lds <= 0)
     return 0;
-  const int64_t want = (int64_t)lds / wg_per_cu - (int64_t)sizeof(float2) * kMaxRotHalf;
+  // a workgroup's LDS (the static table plus this) is allocated in 512-byte
+  // granules: round its share down so that wg_per_cu of them fit
+  const int64_t share = (int64_t)lds / wg_per_cu / kLdsGranule * kLdsGranule;
+  const int64_t want = share - (int64_t)sizeof(float2) * kMaxRotHalf;
   return want > 0 ? (size_t)want : 0;
 }
 
