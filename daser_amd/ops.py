@@ -101,7 +101,10 @@ class PagedKVLayout:
         expect = 1
         for dim in range(t0.dim() - 1, 1, -1):  # a page kv[0, b] is C-contiguous
             if t0.shape[dim] != 1 and s[dim] != expect:
-                raise ValueError("a KV page kv[0, b] must be contiguous")
+                raise ValueError(
+                    "a KV page kv[0, b] must be C-contiguous (records hold its bytes in "
+                    "index order); head-major caches (vLLM's HND layout, heads before "
+                    "tokens in memory) are not supported: use the NHD layout")
             expect *= t0.shape[dim]
         page_elems = expect
         e = t0.element_size()
