@@ -807,6 +807,25 @@ def test_random_geometry_parity(gpu, dt, D, H, bs, style, R, L, seed):
         assert np.array_equal(got[1], rref[l][1]), f"V layer {l}"
         ok, msg = rotation_within_tolerance(got[0], rref[l][0], dt)
         assert ok, f"K layer {l}: {msg}"
+    # the same data as split-x pages (3-D caches), where the geometry allows:
+    # bit-identical to the token-major result after the layout permutation
+    e = shape.elem_bytes
+    X = 16 // e
+    ve = X
+    whole = ((R // 2) % ve == 0 if style == "neox" else R % ve == 0) and ((D - R) * e) % 16 == 0
+    if whole and D % X == 0:
+        tdt = rot[0].dtype
+        st_kx = (st.view(tdt).view(n, L, 2, bs, H, D // X, X).permute(0, 1, 2, 4, 5, 3, 6)
+                 .contiguous().view(-1).view(torch.uint8))
+        kx = [torch.zeros((2, nb, bs * H * D), dtype=tdt, device=gpu) for _ in range(L)]
+        ops.scatter_rerotate(ops.LayerTable(kx, block_size=bs, head_dim=D), dst_ids, offs, st_kx,
+                             tabs, ridx, rot_dim=R, style=style, k_scale=ks)
+        torch.cuda.synchronize()
+        for l in range(L):
+            back = kx[l].view(2, nb, H, D // X, bs, X).permute(0, 1, 4, 2, 3, 5).reshape(
+                2, nb, bs, H, D)
+            assert torch.equal(back.view(torch.uint8), rot[l].view(torch.uint8)), \
+                f"split-x layer {l}"
 
 
 @pytest.mark.parametrize("dt,D,H,bs,style,R,L,seed", _random_cases(max(1, _N_RANDOM // 2), 77))
