@@ -44,6 +44,9 @@ extern "C" {
 
 typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 
+/* Bumped whenever an entry point's signature changes or one is added:
+ * 2 layer_group on the re-rotation, 3 dsr_scatter_rerotate_kx, 4 the
+ * re-rotations' flags. Callers check dsr_abi_version() against it. */
 #define DSR_ABI_VERSION 4
 
 /*
