@@ -20,7 +20,7 @@ LIB_PATH = os.environ.get("DASER_KV_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so"
 )
 
-DSR_ABI_VERSION = 4
+DSR_ABI_VERSION = 5
 DSR_OK = 0
 DSR_ERR_ARG = -1
 DSR_ERR_ALIGN = -2
@@ -66,6 +66,12 @@ SIGNATURES = {
         _I,
     ),
     "dsr_scatter_rerotate_kx": (
+        _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, ctypes.c_uint, _P],
+        _I,
+    ),
+    "dsr_gather_hnd": (_COPY_ARGS[:-1] + [_I, _I, _P], _I),
+    "dsr_scatter_hnd": (_COPY_ARGS[:-1] + [_I, _I, _P], _I),
+    "dsr_scatter_rerotate_hnd": (
         _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, ctypes.c_uint, _P],
         _I,
     ),

@@ -19,6 +19,7 @@ constexpr int kMaxGroup = 64;     // units per workgroup of the grouped copy ker
 constexpr int kGatherUnroll = 16;  // 16-byte vectors per lane per half per round
 constexpr int kScatterUnroll = 16;
 constexpr int kRotCopyUnroll = 8;  // copy of unrotated pages inside the re-rotation kernels
+constexpr int kHndUnroll = 8;      // head-major page copies
 constexpr int kRotUnroll = 4;      // rotation tasks per lane per round (pair-task kernel)
 constexpr int kMaxRotHalf = 512;   // LDS table capacity: rot_dim <= 1024
 constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-robin
@@ -46,6 +47,12 @@ struct UnitArgs {
   int64_t n_units;
   int32_t n_layers;
   int32_t layer0;
+  // Head-major cache pages ([H][block_size][row] in memory while records
+  // hold [block_size][H][row]): rows of hnd_row_vecs vectors; 0 = pages in
+  // record order.
+  int32_t hnd_heads = 0;
+  int32_t hnd_block = 0;
+  int32_t hnd_row_vecs = 0;
 };
 
 // Workgroup -> unit. Hardware deals consecutive workgroup ids round-robin
@@ -110,6 +117,14 @@ __device__ __forceinline__ void bstore(rsrc_t r, int off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kStorePolicy);
 }
 
+// Head-major pages: record vector i (row r = t * H + h of token t, head h)
+// is cache vector (h * block_size + t) * row_vecs + its column.
+__device__ __forceinline__ int hnd_vec(const UnitArgs& a, int i) {
+  const int r = i / a.hnd_row_vecs, v = i - r * a.hnd_row_vecs;
+  const int t = r / a.hnd_heads, h = r - t * a.hnd_heads;
+  return (h * a.hnd_block + t) * a.hnd_row_vecs + v;
+}
+
 // Copies the two page_bytes runs src_k -> dst_k and src_v -> dst_v, issuing
 // all 2*U loads of a round before its stores.
 template <int U>
@@ -136,6 +151,37 @@ __device__ __forceinline__ void copy_halves(const uint8_t* src_k, const uint8_t*
         bstore(dk, i << 4, rk[k]);
         bstore(dv, i << 4, rv[k]);
       }
+    }
+  }
+}
+
+// copy_halves between a head-major cache page and its record: the record
+// side is walked lane-consecutively, the cache side through hnd_vec (whole
+// rows stay contiguous, so a row's lanes still coalesce). Vectors past the
+// page go to offset page_bytes, outside the descriptors: loads read 0 and
+// stores are dropped.
+template <int U, bool kGather>
+__device__ __forceinline__ void copy_halves_hnd(const UnitArgs& a, uint8_t* cache,
+                                                uint8_t* rec) {
+  const int64_t pb = a.page_bytes;
+  const rsrc_t ck = make_rsrc(cache, pb), cv = make_rsrc(cache + a.kv_stride, pb);
+  const rsrc_t rk = make_rsrc(rec, pb), rv = make_rsrc(rec + pb, pb);
+  const int nvec = (int)(pb >> 4);
+  for (int base = threadIdx.x; base < nvec; base += kThreads * U) {
+    u32x4 xk[U], xv[U];
+    int ro[U], co[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * kThreads;
+      ro[k] = i < nvec ? i << 4 : (int)pb;
+      co[k] = i < nvec ? hnd_vec(a, i) << 4 : (int)pb;
+      xk[k] = bload(kGather ? ck : rk, kGather ? co[k] : ro[k]);
+      xv[k] = bload(kGather ? cv : rv, kGather ? co[k] : ro[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      bstore(kGather ? rk : ck, kGather ? ro[k] : co[k], xk[k]);
+      bstore(kGather ? rv : cv, kGather ? ro[k] : co[k], xv[k]);
     }
   }
 }

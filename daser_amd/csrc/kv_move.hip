@@ -267,6 +267,22 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
   });
 }
 
+// Head-major cache pages: the contig kernel with the HND store mapping, one
+// unit per workgroup, at the one-unit kernels' occupancy.
+template <int DT>
+int launch_rerotate_hnd(const RotArgs& ra, int n_pages, int style, hipStream_t s) {
+  const size_t dyn = rot_occupancy_lds(rot_wg_per_cu<DT>());
+  return launch_page_ranges(ra.u, n_pages, 1, [&](const UnitArgs& b, unsigned grid) {
+    RotArgs rb = ra;
+    rb.u = b;
+    rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
+    if (style == DSR_ROPE_NEOX)
+      kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX, false, true><<<grid, kThreads, dyn, s>>>(rb);
+    else
+      kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ, false, true><<<grid, kThreads, dyn, s>>>(rb);
+  });
+}
+
 // The pair-task kernel alone: the split-x K layout, whose rotation partners
 // are a whole block of vectors apart.
 template <int DT>
@@ -359,8 +375,10 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
 
 namespace {
 
-// Both K layouts: kx_block = 0 for token-major K rows (block_size x H x D),
-// kx_block = block_size for the split-x K layout (H x D/X x block_size x X).
+// All K layouts: kx_block = 0 for token-major K rows (block_size x H x D),
+// kx_block = block_size for the split-x K layout (H x D/X x block_size x X);
+// hnd_block = block_size for head-major cache pages (H x block_size x D,
+// records token-major).
 int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
                          int64_t kv_stride, int64_t page_stride,
                          int64_t page_bytes, int64_t num_blocks,
@@ -371,7 +389,7 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
                          const int32_t* rope_idx, int n_tables,
                          const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
-                         const float* k_scale, int kx_block, unsigned flags,
+                         const float* k_scale, int kx_block, int hnd_block, unsigned flags,
                          dsr_stream_t stream) {
   int rc = check_common(layer_base, n_layers, kv_stride, page_stride, page_bytes,
                         num_blocks, page_ids, slot_offsets, n_pages, staging,
@@ -433,6 +451,27 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
   ra.half_vecs = rope_style == DSR_ROPE_NEOX && vec_ok ? rot_dim / 2 * esize / 16 : 0;
   ra.k_scale = k_scale;
   hipStream_t s = (hipStream_t)stream;
+  if (hnd_block > 0) {
+    // head-major pages: the contig kernel only (rows and partners stay whole
+    // in record order; the cache side goes through hnd_vec)
+    const int h = ra.half_vecs;
+    const bool contig = vec_ok && (rope_style == DSR_ROPE_GPTJ ||
+                                   (h > 0 && h <= 32 && (h & (h - 1)) == 0 &&
+                                    ra.row_vecs % (2 * h) == 0));
+    const int64_t rows = page_bytes / row_bytes;
+    if (!contig || kx_block > 0 || rows % hnd_block) return DSR_ERR_SHAPE;
+    ra.u.hnd_heads = (int)(rows / hnd_block);
+    ra.u.hnd_block = hnd_block;
+    ra.u.hnd_row_vecs = ra.row_vecs;
+    switch (dtype) {
+      case DSR_DTYPE_BF16:
+        return launch_rerotate_hnd<DSR_DTYPE_BF16>(ra, n_pages, rope_style, s);
+      case DSR_DTYPE_FP16:
+        return launch_rerotate_hnd<DSR_DTYPE_FP16>(ra, n_pages, rope_style, s);
+      default:
+        return launch_rerotate_hnd<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, s);
+    }
+  }
   if (kx_block > 0) {
     // vector kernels when the head block is a power-of-two number of
     // vectors (>= one wave), block_size a power of two and the neox partner
@@ -493,7 +532,7 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                               num_blocks, page_ids, slot_offsets, n_pages, staging,
                               staging_bytes, layer_bytes, layer0, cos_sin, rope_idx, n_tables,
                               layer_group, n_groups, head_dim, rot_dim, rope_style, dtype,
-                              k_scale, 0, flags, stream);
+                              k_scale, 0, 0, flags, stream);
 }
 
 int dsr_scatter_rerotate_kx(const uint64_t* layer_base, int n_layers,
@@ -513,7 +552,83 @@ int dsr_scatter_rerotate_kx(const uint64_t* layer_base, int n_layers,
                               num_blocks, page_ids, slot_offsets, n_pages, staging,
                               staging_bytes, layer_bytes, layer0, cos_sin, rope_idx, n_tables,
                               layer_group, n_groups, head_dim, rot_dim, rope_style, dtype,
-                              k_scale, block_size, flags, stream);
+                              k_scale, block_size, 0, flags, stream);
+}
+
+int dsr_scatter_rerotate_hnd(const uint64_t* layer_base, int n_layers,
+                             int64_t kv_stride, int64_t page_stride,
+                             int64_t page_bytes, int64_t num_blocks,
+                             const int32_t* page_ids, const int64_t* slot_offsets,
+                             int n_pages, const void* staging,
+                             int64_t staging_bytes, int64_t layer_bytes,
+                             int layer0, const float* cos_sin,
+                             const int32_t* rope_idx, int n_tables,
+                             const int32_t* layer_group, int n_groups, int head_dim,
+                             int rot_dim, int rope_style, int dtype,
+                             const float* k_scale, int block_size, unsigned flags,
+                             dsr_stream_t stream) {
+  if (block_size <= 0) return DSR_ERR_ARG;
+  return scatter_rerotate_any(layer_base, n_layers, kv_stride, page_stride, page_bytes,
+                              num_blocks, page_ids, slot_offsets, n_pages, staging,
+                              staging_bytes, layer_bytes, layer0, cos_sin, rope_idx, n_tables,
+                              layer_group, n_groups, head_dim, rot_dim, rope_style, dtype,
+                              k_scale, 0, block_size, flags, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Head-major copies: the unit geometry, then one unit per workgroup.
+int copy_hnd(bool gather, const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+             int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+             const int32_t* page_ids, const int64_t* slot_offsets, int n_pages,
+             const void* staging, int64_t staging_bytes, int64_t layer_bytes, int layer0,
+             int block_size, int num_heads, dsr_stream_t stream) {
+  if (block_size <= 0 || num_heads <= 0) return DSR_ERR_ARG;
+  int rc = check_common(layer_base, n_layers, kv_stride, page_stride, page_bytes,
+                        num_blocks, page_ids, slot_offsets, n_pages, staging,
+                        staging_bytes, layer_bytes, layer0);
+  if (rc != DSR_OK) return rc;
+  const int64_t rows = (int64_t)block_size * num_heads;
+  if (page_bytes % (rows * 16)) return DSR_ERR_SHAPE;
+  if (n_pages == 0 || n_layers == 0) return DSR_OK;
+  UnitArgs a = make_unit(layer_base, n_layers, kv_stride, page_stride, page_bytes,
+                         num_blocks, page_ids, slot_offsets, n_pages, staging,
+                         staging_bytes, layer_bytes, layer0);
+  a.hnd_heads = num_heads;
+  a.hnd_block = block_size;
+  a.hnd_row_vecs = (int)(page_bytes / rows / 16);
+  return launch_page_ranges(a, n_pages, 1, [&](const UnitArgs& b, unsigned grid) {
+    if (gather)
+      kv_copy_hnd_kernel<true><<<grid, kThreads, 0, (hipStream_t)stream>>>(b);
+    else
+      kv_copy_hnd_kernel<false><<<grid, kThreads, 0, (hipStream_t)stream>>>(b);
+  });
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsr_gather_hnd(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                   int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                   const int32_t* page_ids, const int64_t* slot_offsets, int n_pages,
+                   void* staging, int64_t staging_bytes, int64_t layer_bytes, int layer0,
+                   int block_size, int num_heads, dsr_stream_t stream) {
+  return copy_hnd(true, layer_base, n_layers, kv_stride, page_stride, page_bytes, num_blocks,
+                  page_ids, slot_offsets, n_pages, staging, staging_bytes, layer_bytes, layer0,
+                  block_size, num_heads, stream);
+}
+
+int dsr_scatter_hnd(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                    int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                    const int32_t* page_ids, const int64_t* slot_offsets, int n_pages,
+                    const void* staging, int64_t staging_bytes, int64_t layer_bytes,
+                    int layer0, int block_size, int num_heads, dsr_stream_t stream) {
+  return copy_hnd(false, layer_base, n_layers, kv_stride, page_stride, page_bytes,
+                  num_blocks, page_ids, slot_offsets, n_pages, staging, staging_bytes,
+                  layer_bytes, layer0, block_size, num_heads, stream);
 }
 
 namespace {

@@ -30,6 +30,17 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_kernel(UnitArgs a) {
                               a.page_bytes);
 }
 
+// Gather and scatter of head-major cache pages (records in token-major
+// order), one unit per workgroup, in the unit orders above.
+template <bool kGather>
+__global__ __launch_bounds__(kThreads) void kv_copy_hnd_kernel(UnitArgs a) {
+  uint8_t *cache, *rec;
+  int l;
+  const int64_t u = kGather ? xcd_unit(a.n_units) : layer_major_unit(a.n_units, a.n_layers);
+  if (u < 0 || !unit_addresses(a, u, &cache, &rec, &l)) return;
+  copy_halves_hnd<kHndUnroll, kGather>(a, cache, rec);
+}
+
 // ---------------------------------------------------------------------------
 // Small pages: several units per workgroup.
 //

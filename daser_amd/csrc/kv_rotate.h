@@ -290,6 +290,14 @@ struct VRound {
       if (i < nvec) bstore(rd, i << 4, r[k]);
     }
   }
+  // head-major cache page: vector i of the round goes to cache vector hnd_vec(i)
+  __device__ __forceinline__ void store_hnd(const UnitArgs& a, rsrc_t rd, int base, int nvec) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int i = base + k * kThreads;
+      if (i < nvec) bstore(rd, hnd_vec(a, i) << 4, r[k]);
+    }
+  }
   // K of a split-x page: vector i of the round is physical vector kx_phys(i)
   __device__ __forceinline__ void load_kx(const RotArgs& ra, rsrc_t rs, int base, int nvec) {
 #pragma unroll
@@ -403,7 +411,7 @@ __device__ __forceinline__ u32x4 rotate_vec(const RotArgs& ra, u32x4 own, u32x4 
 // shuffle. Valid when half_vecs is a power of two <= 32 dividing the row
 // evenly (rows then start on 2*half_vecs lane boundaries), and always for
 // gptj, whose pairs sit inside one vector.
-template <int DT, int STYLE, int U, bool KX>
+template <int DT, int STYLE, int U, bool KX, bool HND = false>
 __device__ __forceinline__ void rotate_contig_round(const RotArgs& ra, VRound<U>& kk,
                                                     int base, int nvec, rsrc_t kd,
                                                     const float2* tab, float scale,
@@ -418,9 +426,11 @@ __device__ __forceinline__ void rotate_contig_round(const RotArgs& ra, VRound<U>
       for (int w = 0; w < 4; ++w) q[w] = (unsigned)__shfl_xor((int)kk.r[k][w], dist);
     }
     if (i >= nvec) continue;
+    // split-x: both sides move vector kx_phys(i); head-major: the record
+    // row order is token-major (the table column follows i), the cache's not
     const int p = KX ? kx_phys(ra, i) : i;
-    bstore(kd, p << 4, rotate_vec<DT, STYLE>(ra, kk.r[k], q, k_column<KX>(ra, p), tab, scale,
-                                             inv_scale));
+    bstore(kd, (HND ? hnd_vec(ra.u, i) : p) << 4,
+           rotate_vec<DT, STYLE>(ra, kk.r[k], q, k_column<KX>(ra, p), tab, scale, inv_scale));
   }
 }
 
@@ -431,7 +441,7 @@ constexpr int rot_contig_unroll() {
   return DT == DSR_DTYPE_FP8_E4M3 ? 4 : 8;
 }
 
-template <int DT, int STYLE, bool KX>
+template <int DT, int STYLE, bool KX, bool HND = false>
 __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(RotArgs ra) {
   __shared__ float2 tab[kMaxRotHalf];
   uint8_t *cache, *rec;
@@ -442,7 +452,10 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
   const int ti = rope_table(ra, p, l);
   const int64_t pb = ra.u.page_bytes;
   if (ti < 0) {
-    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    if (HND)
+      copy_halves_hnd<kRotCopyUnroll, false>(ra.u, cache, rec);
+    else
+      copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
     return;
   }
   constexpr int U = rot_contig_unroll<DT>();
@@ -473,8 +486,11 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
       else
         kk.load(ks, base, nvec);
     }
-    v.store(vd, base, nvec);
-    rotate_contig_round<DT, STYLE, U, KX>(ra, kk, base, nvec, kd, tab, scale, inv_scale);
+    if (HND)
+      v.store_hnd(ra.u, vd, base, nvec);
+    else
+      v.store(vd, base, nvec);
+    rotate_contig_round<DT, STYLE, U, KX, HND>(ra, kk, base, nvec, kd, tab, scale, inv_scale);
   }
 }
 

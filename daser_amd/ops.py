@@ -49,7 +49,11 @@ class PagedKVLayout:
       ``(2, NB, block_size, H, D)`` of vLLM's FlashAttention-style backends;
     * ``"kx"``: ``[H][D / X][block_size][X]`` with X = 16 / element bytes,
       the 3-D caches ``(2, NB, block_size * H * D)`` of vLLM's
-      PagedAttention kernels (its ROCm paged-attention backend).
+      PagedAttention kernels (its ROCm paged-attention backend);
+    * ``"hnd"``: 5-D caches whose pages are stored head-major,
+      ``[H][block_size][D]`` (vLLM's HND layout). Their records still hold
+      the page in index order ``[block_size][H][D]``, as the reference's
+      ``reshape(-1)`` of ``kv[:, b]`` does, so the copies permute rows.
 
     A cache that is not 5-D carries no head geometry in its shape: pass
     ``block_size`` and ``head_dim`` (``num_heads`` follows from the page
@@ -98,24 +102,30 @@ class PagedKVLayout:
                 raise ValueError("all layer caches must live on one device")
         nb = t0.shape[1]
         s = t0.stride()
-        expect = 1
-        for dim in range(t0.dim() - 1, 1, -1):  # a page kv[0, b] is C-contiguous
+        expect, c_order = 1, True
+        for dim in range(t0.dim() - 1, 1, -1):  # is a page kv[0, b] C-contiguous?
             if t0.shape[dim] != 1 and s[dim] != expect:
-                raise ValueError(
-                    "a KV page kv[0, b] must be C-contiguous (records hold its bytes in "
-                    "index order); head-major caches (vLLM's HND layout, heads before "
-                    "tokens in memory) are not supported: use the NHD layout")
+                c_order = False
             expect *= t0.shape[dim]
         page_elems = expect
         e = t0.element_size()
+        head_major = False
+        if not c_order:
+            # vLLM's HND layout: logical (2, NB, bs, H, D), page stored [H][bs][D]
+            head_major = (t0.dim() == 5 and s[4] == 1 and s[2] == t0.shape[4] and
+                          s[3] == t0.shape[2] * t0.shape[4])
+            if not head_major:
+                raise ValueError("a KV page kv[0, b] must be contiguous in memory, in "
+                                 "(block_size, heads, head_dim) order or head-major")
         if t0.dim() == 5:
-            if k_layout not in (None, "nhd"):
-                raise ValueError("a 5-D cache (2, NB, block_size, H, D) has the 'nhd' K layout")
+            want = "hnd" if head_major else "nhd"
+            if k_layout not in (None, want):
+                raise ValueError(f"this 5-D cache's pages have the {want!r} layout")
             _, _, bs, h, d = t0.shape
             if (block_size not in (None, bs)) or (head_dim not in (None, d)):
                 raise ValueError(f"cache shape {tuple(t0.shape)} disagrees with "
                                  f"block_size={block_size}, head_dim={head_dim}")
-            layout = "nhd"
+            layout = want
         else:
             layout = k_layout or ("kx" if t0.dim() == 3 else "nhd")
             if layout not in ("nhd", "kx"):
@@ -282,8 +292,18 @@ def gather(
     """
     args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers,
                             records_written=True)
-    rc = _lib.lib().dsr_gather(*args, _stream_handle(table.layout.device))
-    _lib.check("dsr_gather", rc)
+    fn, name, extra = _copy_entry(table.layout, "dsr_gather")
+    rc = fn(*args, *extra, _stream_handle(table.layout.device))
+    _lib.check(name, rc)
+
+
+def _copy_entry(lay: PagedKVLayout, base: str):
+    """The copy entry point for the layout's pages and its extra arguments:
+    head-major pages go through the row-permuting ``*_hnd`` variant."""
+    if lay.k_layout == "hnd":
+        return getattr(_lib.lib(), base + "_hnd"), base + "_hnd", (lay.block_size,
+                                                                   lay.num_heads)
+    return getattr(_lib.lib(), base), base, ()
 
 
 class PreparedGather:
@@ -303,16 +323,17 @@ class PreparedGather:
         self._mid = args[2:12]  # strides, page geometry, tables, staging
         self._layer0 = layer0
         self._n_layers = table.layout.num_layers
-        self._fn = _lib.lib().dsr_gather
+        self._fn, self._name, self._extra = _copy_entry(table.layout, "dsr_gather")
 
     def __call__(self, first: int, count: int, stream: int) -> None:
         """Gathers table layers [first, first + count) on ``stream`` (a HIP
         stream handle, e.g. ``torch.cuda.current_stream().cuda_stream``)."""
         if first < 0 or count < 0 or first + count > self._n_layers:
             raise IndexError("layer range outside the registered caches")
-        rc = self._fn(self._table.ptr(first), count, *self._mid, self._layer0 + first, stream)
+        rc = self._fn(self._table.ptr(first), count, *self._mid, self._layer0 + first,
+                      *self._extra, stream)
         if rc:
-            _lib.check("dsr_gather", rc)
+            _lib.check(self._name, rc)
 
 
 def scatter(
@@ -327,8 +348,9 @@ def scatter(
     """Unpacks slot records into pages (reference load loop, :536-551)."""
     page_ids, slot_offsets, _ = dest_order(page_ids, slot_offsets)
     args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
-    rc = _lib.lib().dsr_scatter(*args, _stream_handle(table.layout.device))
-    _lib.check("dsr_scatter", rc)
+    fn, name, extra = _copy_entry(table.layout, "dsr_scatter")
+    rc = fn(*args, *extra, _stream_handle(table.layout.device))
+    _lib.check(name, rc)
 
 
 def scatter_rerotate(
@@ -411,10 +433,11 @@ def scatter_rerotate(
               None if lg_d is None else lg_d.data_ptr(), n_groups if grouped else 0,
               lay.head_dim, rot_dim, ROPE_STYLES[style], _DTYPE_CODES[lay.dtype], ks_ptr)
     flags = _lib.DSR_REROTATE_SHARED_RECORDS if shared_records else 0
-    if lay.k_layout == "kx":
-        rc = _lib.lib().dsr_scatter_rerotate_kx(*common, lay.block_size, flags,
-                                                _stream_handle(lay.device))
-        _lib.check("dsr_scatter_rerotate_kx", rc)
+    if lay.k_layout in ("kx", "hnd"):
+        name = "dsr_scatter_rerotate_" + lay.k_layout
+        rc = getattr(_lib.lib(), name)(*common, lay.block_size, flags,
+                                       _stream_handle(lay.device))
+        _lib.check(name, rc)
     else:
         rc = _lib.lib().dsr_scatter_rerotate(*common, flags, _stream_handle(lay.device))
         _lib.check("dsr_scatter_rerotate", rc)

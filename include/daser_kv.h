@@ -46,8 +46,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 
 /* Bumped whenever an entry point's signature changes or one is added:
  * 2 layer_group on the re-rotation, 3 dsr_scatter_rerotate_kx, 4 the
- * re-rotations' flags. Callers check dsr_abi_version() against it. */
-#define DSR_ABI_VERSION 4
+ * re-rotations' flags, 5 the head-major (_hnd) entry points. Callers check
+ * dsr_abi_version() against it. */
+#define DSR_ABI_VERSION 5
 
 /*
  * Kernel choice and launch shape follow from the geometry; these environment
@@ -216,6 +217,47 @@ int dsr_scatter_rerotate_kx(const uint64_t* layer_base, int n_layers,
                             int rot_dim, int rope_style, int dtype,
                             const float* k_scale, int block_size, unsigned flags,
                             dsr_stream_t stream);
+
+/*
+ * Head-major cache pages: vLLM's optional HND KV layout keeps the caches'
+ * logical shape (2, num_blocks, block_size, H, D) but stores a page with its
+ * heads outermost, [H][block_size][D]. The record of a page is still
+ * bytes(kv_l[:, b]) in logical, token-major order [block_size][H][D] (the
+ * reference's reshape(-1), daser/connector/daser_connector.py:625-632, and
+ * its copy_ back, :545-550), so these entry points permute whole rows of D
+ * elements between the two orders: row (t, h) of the record is row
+ * h * block_size + t of the cache page. Same arguments and contracts as
+ * dsr_gather / dsr_scatter / dsr_scatter_rerotate, plus the page geometry:
+ * block_size and num_heads with page_bytes a multiple of block_size *
+ * num_heads * 16 (the copies); block_size, with page_bytes a multiple of
+ * block_size * head_dim * elem_bytes (the re-rotation, whose rotary widths
+ * must be whole 16-byte vectors with a power-of-two neox partner distance
+ * of at most 32 vectors, or gptj; other shapes return DSR_ERR_SHAPE).
+ */
+int dsr_gather_hnd(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                   int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                   const int32_t* page_ids, const int64_t* slot_offsets, int n_pages,
+                   void* staging, int64_t staging_bytes, int64_t layer_bytes, int layer0,
+                   int block_size, int num_heads, dsr_stream_t stream);
+
+int dsr_scatter_hnd(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                    int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                    const int32_t* page_ids, const int64_t* slot_offsets, int n_pages,
+                    const void* staging, int64_t staging_bytes, int64_t layer_bytes,
+                    int layer0, int block_size, int num_heads, dsr_stream_t stream);
+
+int dsr_scatter_rerotate_hnd(const uint64_t* layer_base, int n_layers,
+                             int64_t kv_stride, int64_t page_stride,
+                             int64_t page_bytes, int64_t num_blocks,
+                             const int32_t* page_ids, const int64_t* slot_offsets,
+                             int n_pages, const void* staging,
+                             int64_t staging_bytes, int64_t layer_bytes,
+                             int layer0, const float* cos_sin,
+                             const int32_t* rope_idx, int n_tables,
+                             const int32_t* layer_group, int n_groups, int head_dim,
+                             int rot_dim, int rope_style, int dtype,
+                             const float* k_scale, int block_size, unsigned flags,
+                             dsr_stream_t stream);
 
 /*
  * Token-granular offload gather driven by vLLM's slot_mapping: for every

@@ -605,3 +605,48 @@ def test_save_gathers_from_the_tensor_passed(gpu, tmp_path, caplog):
     oracle.gather(host, [5, 9, 2], np.arange(3) * SHAPE.slot_bytes, ref, SHAPE.layer_bytes)
     assert np.array_equal(_file_records(tmp_path / "daser.store", 3, 3), ref)
     w.shutdown()
+
+
+def test_head_major_caches_save_reference_records_and_load(gpu, tmp_path):
+    """vLLM's HND layout (pages stored heads-first): the store file holds the
+    same records as for token-major caches of the same values, and a load
+    with a new position puts the same logical values back."""
+    print("case: connector head-major caches", flush=True)
+
+    def hnd(caches):
+        out = []
+        for c in caches:
+            m = torch.empty((2, 16, SHAPE.num_heads, SHAPE.block_size, SHAPE.head_dim),
+                            dtype=c.dtype, device=gpu)
+            v = m.permute(0, 1, 3, 2, 4)
+            v.copy_(c)
+            out.append(v)
+        return out
+
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=38)
+    w, _ = _worker(tmp_path, rope_theta=500000.0)
+    named = _named(hnd(caches))
+    w.register_kv_caches(named)
+    assert w._plane.table.layout.k_layout == "hnd"
+    _save(w, named, _store_reqs())
+    host = [to_bits_np(c, "bf16") for c in caches]
+    ref = np.zeros(3 * SHAPE.slot_bytes, dtype=np.uint8)
+    oracle.gather(host, [5, 9, 2], np.arange(3) * SHAPE.slot_bytes, ref, SHAPE.layer_bytes)
+    assert np.array_equal(_file_records(tmp_path / "daser.store", 3, 3), ref)
+
+    slot = SHAPE.slot_bytes
+    meta = C.DaserConnectorMeta(reqs_to_load={
+        "x": C.ReqLoadSpec("ka", 3, 3, [1, 12, 4], 3 * slot, 40, pos_offset=100, new_pos=4196)})
+    outs = []
+    for layout in (hnd, lambda cs: cs):
+        fresh = layout([torch.zeros_like(c) for c in caches])
+        w2, _ = _worker(tmp_path, rope_theta=500000.0)
+        w2.register_kv_caches(_named(fresh))
+        w2.bind_connector_metadata(meta)
+        w2.start_load_kv(None)
+        torch.cuda.synchronize()
+        outs.append([f.contiguous() for f in fresh])
+        w2.shutdown()
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    w.shutdown()

@@ -1129,3 +1129,108 @@ def test_rerotate_kx_layout_matches_oracle(gpu, monkeypatch, dt, style, heads, h
         assert ok, f"layer {l}: {msg}"
         still = page_ids[page_delta == 0]
         assert np.array_equal(got[0][still], ref[l][0][still]), f"layer {l}: delta 0 copy"
+
+
+# ---------------------------------------------------------------------------
+# head-major (HND) cache pages: records in token-major order
+
+
+def _hnd_caches(shape, nb, dt, gpu, seed, scale=1.0):
+    """(2, NB, bs, H, D) views of head-major memory (2, NB, H, bs, D), holding
+    the same logical values as rand_caches with the same seed."""
+    out = []
+    for c in rand_caches(shape, nb, dt, gpu, seed, scale):
+        m = torch.empty((2, nb, shape.num_heads, shape.block_size, shape.head_dim),
+                        dtype=c.dtype, device=gpu)
+        v = m.permute(0, 1, 3, 2, 4)
+        v.copy_(c)
+        out.append(v)
+    return out
+
+
+@pytest.mark.parametrize("heads,head_dim,bs,dt", [
+    (8, 128, 16, "bf16"), (2, 64, 16, "bf16"), (4, 128, 32, "e4m3"), (3, 96, 16, "bf16"),
+])
+def test_hnd_copies_match_oracle(gpu, heads, head_dim, bs, dt):
+    """Gather from head-major pages writes the records of the logical page
+    (the reference's reshape(-1) of kv[:, b]); scatter writes them back."""
+    print(f"case: hnd copies H{heads} D{head_dim} bs{bs} {dt}", flush=True)
+    shape = KVShape(3, heads, head_dim, bs, 1 if dt == "e4m3" else 2)
+    wl = workloads.ragged(shape, 4, 1, 200, seed=5, pool_slack=1.5)
+    caches = _hnd_caches(shape, wl.num_blocks, dt, gpu, seed=70)
+    table = ops.LayerTable(caches)
+    assert table.layout.k_layout == "hnd"
+    st = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(table, wl.page_ids, wl.slot_offsets, st)
+    ref = np.zeros(wl.staging_bytes, dtype=np.uint8)
+    host = [np.ascontiguousarray(to_bits_np(c, dt)) for c in caches]
+    oracle.gather(host, wl.page_ids, wl.slot_offsets, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    assert np.array_equal(st.cpu().numpy(), ref)
+    dst = _hnd_caches(shape, wl.num_blocks, dt, gpu, seed=71)
+    before = [to_bits_np(c, dt) for c in dst]
+    ops.scatter(ops.LayerTable(dst), wl.page_ids, wl.slot_offsets, st)
+    dref = [np.ascontiguousarray(b) for b in before]
+    oracle.scatter(dref, wl.page_ids, wl.slot_offsets, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    for l in range(3):
+        assert np.array_equal(to_bits_np(dst[l], dt), dref[l]), f"layer {l}"
+    # the per-layer prepared gather of the connector takes the same route
+    st2 = torch.zeros_like(st)
+    pg = ops.PreparedGather(table, torch.from_numpy(wl.page_ids).to(gpu),
+                            torch.from_numpy(wl.slot_offsets).to(gpu), st2)
+    for l in range(3):
+        pg(l, 1, torch.cuda.current_stream(gpu).cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(st, st2)
+    with pytest.raises(ValueError):  # the token form needs token-major pages
+        ops.gather_slots(table, [0], [0], st)
+
+
+@pytest.mark.parametrize("heads,head_dim,rot,dt,style", [
+    (8, 128, 128, "bf16", "neox"), (2, 64, 64, "bf16", "neox"), (4, 128, 128, "e4m3", "neox"),
+    (2, 128, 128, "bf16", "gptj"), (4, 128, 64, "bf16", "neox"),
+])
+def test_hnd_rerotate_equals_token_major(gpu, heads, head_dim, rot, dt, style):
+    """Re-rotation into head-major pages gives, per logical element, exactly
+    the bits of the token-major kernel on the same records, and matches the
+    oracle."""
+    print(f"case: hnd rerotate H{heads} D{head_dim} R{rot} {dt} {style}", flush=True)
+    shape, dst, dst_ref, page_ids, deltas = _rerotate_case(gpu, dt, style, head_dim, rot,
+                                                           heads=heads, layers=3, seed=9)
+    # the same call on head-major caches holding the same initial values
+    rng = np.random.default_rng(9)
+    chunk_pages = [int(x) for x in rng.integers(1, 4, size=5)]
+    n = sum(chunk_pages)
+    nb = n + 5
+    src_caches = rand_caches(shape, nb, dt, gpu, seed=10)
+    staging = torch.zeros(n * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    offs = np.arange(n, dtype=np.int64) * shape.slot_bytes
+    ops.gather(ops.LayerTable(src_caches), rng.permutation(nb)[:n].astype(np.int32), offs,
+               staging)
+    hnd = _hnd_caches(shape, nb, dt, gpu, seed=11)
+    ids = rng.permutation(nb)[:n].astype(np.int32)
+    assert np.array_equal(ids, page_ids)
+    ridx, uniq = position.page_rope_index(chunk_pages, (0, 1, 517, 32767, 123))
+    tabs = position.delta_tables(uniq, rot, 500000.0, device=gpu)
+    ks = None
+    if dt == "e4m3":
+        ks = torch.from_numpy(rng.random(3).astype(np.float32) * 0.5 + 0.01).to(gpu)
+    ops.scatter_rerotate(ops.LayerTable(hnd), ids, offs, staging, tabs, ridx, rot_dim=rot,
+                         style=style, k_scale=ks)
+    torch.cuda.synchronize()
+    for l in range(3):
+        assert torch.equal(hnd[l].contiguous().view(torch.uint8), dst[l].view(torch.uint8)), \
+            f"layer {l}"
+        got = to_bits_np(dst[l], dt)
+        ok, msg = rotation_within_tolerance(got[0][page_ids], dst_ref[l][0][page_ids], dt)
+        assert ok, f"layer {l}: {msg}"
+
+
+def test_hnd_rerotate_unsupported_width_refused(gpu):
+    shape = KVShape(2, 2, 96, 16, 2)
+    caches = _hnd_caches(shape, 4, "bf16", gpu, seed=12)
+    st = torch.zeros(shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    tabs = position.delta_tables([5], 96, device=gpu)
+    with pytest.raises(DaserKVError):  # 96-dim neox rows: partners 6 vectors apart
+        ops.scatter_rerotate(ops.LayerTable(caches), [1], [0], st, tabs, [0])

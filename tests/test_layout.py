@@ -27,12 +27,19 @@ def test_block_major_allocation_viewed_kv_first():
     assert lay.kv_stride == 16 * 8 * 128 * 2 and lay.page_stride == 2 * lay.kv_stride
 
 
-def test_head_major_pages_rejected_with_a_reason():
-    with pytest.raises(ValueError, match="HND"):
-        PagedKVLayout.from_caches([_hnd(10, 16, 8, 128)])
+def test_head_major_pages():
+    lay = PagedKVLayout.from_caches([_hnd(10, 16, 8, 128)])
+    assert (lay.k_layout, lay.block_size, lay.num_heads, lay.head_dim) == ("hnd", 16, 8, 128)
+    assert lay.page_bytes == 16 * 8 * 128 * 2
+    with pytest.raises(ValueError):
+        PagedKVLayout.from_caches([_hnd(10, 16, 8, 128)], k_layout="nhd")
     # one KV head: head-major and token-major memory coincide
     lay = PagedKVLayout.from_caches([_hnd(10, 16, 1, 128)])
-    assert lay.page_bytes == 16 * 128 * 2
+    assert lay.k_layout == "nhd" and lay.page_bytes == 16 * 128 * 2
+    # a page that is not contiguous in memory at all
+    sliced = torch.zeros((2, 10, 16, 8, 256), dtype=torch.bfloat16)[..., :128]
+    with pytest.raises(ValueError, match="contiguous"):
+        PagedKVLayout.from_caches([sliced])
 
 
 def test_flat_paged_attention_caches():
