@@ -60,6 +60,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
  *   DSR_ROT_KERNEL=contig|grouped|pairs   re-rotation kernel where several apply
  *   DSR_ROT_WG_PER_CU=n, DSR_ROT_GROUPED_WG_PER_CU=n   re-rotation occupancy
  *   DSR_SLOTS_TPW=4|8|16         tokens per wave of the small-row token kernels
+ *   DSR_SLOTS_KERNEL=small       rows of <= 8 vectors: the small-row kernel
+ *                                instead of the packed one
+ *   DSR_SLOTS_UNROLL=4|8         instructions per wave of the packed kernel
  */
 
 #define DSR_OK 0
