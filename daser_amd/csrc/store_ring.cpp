@@ -12,9 +12,11 @@
 //   F + k * slot_bytes; a slot is refilled only after its write completed.
 //   Copies of later pieces run on the GPU's DMA engine while earlier pieces
 //   are being written.
-// Read: io_uring READs fill free slots; each completed read is copied
-//   pinned slot -> device on the side stream (event e_k); a slot is reused
-//   after its copy event; the consumer stream waits on the last copy.
+// Read: the side stream waits for the consumer stream (earlier work may
+//   still use the destination); io_uring READs fill free slots; each
+//   completed read is copied pinned slot -> device on the side stream (event
+//   e_k); a slot is reused after its copy event; the consumer stream waits
+//   on the last copy.
 //
 // Without io_uring (ENOSYS/EPERM, or an op the kernel rejects) the same
 // loop runs with pwrite/pread. Host mode (DSR_RING_HOST) uses plain memory
@@ -399,6 +401,10 @@ int dsr_ring_read(dsr_ring* r, void* dst, int64_t nbytes, int64_t file_offset,
   std::vector<int64_t> piece_of(S, -1);
   int err = 0;
   int64_t inflight = 0, submitted = 0, landed = 0;
+  if (!r->host) {  // copies into dst wait for the consumer's earlier work on it
+    err = hip_rc(hipEventRecord(r->ready, (hipStream_t)consumer));
+    if (!err) err = hip_rc(hipStreamWaitEvent(r->stream, r->ready, 0));
+  }
   auto land = [&](int s) -> int {  // a read is in slot s: copy it to the device
     const Piece& pc = pieces[(size_t)piece_of[s]];
     uint8_t* to = (uint8_t*)dst + pc.dev_off;

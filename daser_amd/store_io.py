@@ -189,13 +189,18 @@ class PinnedRingIO:
 
     def read_into_device(self, dst: torch.Tensor, file_offset: int,
                          consumer: Optional[torch.cuda.Stream] = None) -> int:
-        """Reads ``dst.nbytes`` bytes at ``file_offset`` into ``dst``. On
-        return the host reads are done and ``consumer`` (default: the current
-        stream) is ordered after the last copy into ``dst``."""
+        """Reads ``dst.nbytes`` bytes at ``file_offset`` into ``dst``. Work
+        enqueued on ``consumer`` (default: the current stream) before the call
+        is complete before the first copy into ``dst``; on return the host
+        reads are done and ``consumer`` is ordered after the last copy."""
         self._check()
         flat = dst.reshape(-1).view(torch.uint8)
         n = flat.numel()
         with self._lock:
+            if self._gpu:  # earlier work on the consumer may still use dst
+                before = torch.cuda.Event()
+                before.record(consumer or torch.cuda.current_stream(self.device))
+                self._stream.wait_event(before)
             try:
                 # keep up to len(slots) reads in flight ahead of the copies
                 pending = []

@@ -338,9 +338,10 @@ int dsr_ring_open(const char* path, int64_t slot_bytes, int n_slots, int flags,
 int dsr_ring_write(dsr_ring* ring, const void* src, int64_t nbytes, int64_t file_offset,
                    dsr_stream_t producer);
 
-/* Reads nbytes at file_offset into `dst`. On return the file reads are done
- * and `consumer` is ordered after the last copy into dst. A read past the end
- * of the file is DSR_ERR_IO. */
+/* Reads nbytes at file_offset into `dst`. Work enqueued on `consumer` before
+ * the call (which may still use dst) is complete before the first copy into
+ * dst; on return the file reads are done and `consumer` is ordered after the
+ * last copy. A read past the end of the file is DSR_ERR_IO. */
 int dsr_ring_read(dsr_ring* ring, void* dst, int64_t nbytes, int64_t file_offset,
                   dsr_stream_t consumer);
 

@@ -3,7 +3,8 @@
 // checks the records against a host memcpy of the same layout, scatters them
 // into a second cache with dsr_scatter and checks the pages, then re-rotates
 // with a zero table (rope_idx -1) through both K layouts' entry points and
-// checks a bit-exact copy; gathers the
+// checks a bit-exact copy; gathers the page list from the cache read as
+// head-major pages and checks the row permutation; gathers the
 // same records token by token with dsr_gather_slots; writes them to a store
 // file through the staging ring and reads them back. Exit code 0 on success;
 // prints the failing check otherwise.
@@ -122,6 +123,33 @@ int main() {
   REQUIRE(dsr_gather(bases, L, 4100, page, page, NB, d_ids, d_offs, n, stg, n * slot,
                      layer_bytes, 0, nullptr) == DSR_ERR_ALIGN,
           "misaligned stride rejected");
+
+  // the same cache memory read as head-major pages ([H][bs][D]): records
+  // hold each page's rows in token-major order, row (t, h) <- (h * bs + t)
+  {
+    const int64_t row = (int64_t)D * 2;
+    uint8_t* stg3;
+    REQUIRE(hipMalloc(&stg3, n * slot) == hipSuccess, "hipMalloc");
+    rc = dsr_gather_hnd(bases, L, NB * page, page, page, NB, d_ids, d_offs, n, stg3, n * slot,
+                        layer_bytes, 0, bs, H, nullptr);
+    REQUIRE(rc == 0, dsr_error_string(rc));
+    std::vector<uint8_t> got3(n * slot), want3(n * slot);
+    hipMemcpy(got3.data(), stg3, got3.size(), hipMemcpyDeviceToHost);
+    for (int p = 0; p < n; ++p)
+      for (int l = 0; l < L; ++l)
+        for (int kv = 0; kv < 2; ++kv) {
+          const uint8_t* pg = host.data() + l * cache_bytes + kv * NB * page + ids[p] * page;
+          uint8_t* rec = want3.data() + offs[p] + l * layer_bytes + kv * page;
+          for (int t = 0; t < bs; ++t)
+            for (int h = 0; h < H; ++h)
+              memcpy(rec + (t * H + h) * row, pg + (h * bs + t) * row, row);
+        }
+    REQUIRE(got3 == want3, "head-major gather records");
+    REQUIRE(dsr_gather_hnd(bases, L, NB * page, page, page, NB, d_ids, d_offs, n, stg3,
+                           n * slot, layer_bytes, 0, 0, H, nullptr) == DSR_ERR_ARG,
+            "head-major gather without a block size rejected");
+    hipFree(stg3);
+  }
 
   // token form: slot_mapping of the same pages, full pages -> the same records
   const int64_t row = (int64_t)H * D * 2;

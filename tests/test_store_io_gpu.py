@@ -80,3 +80,23 @@ def test_missing_file_raises(gpu, tmp_path, ring):
     print(f"case: ring missing file {ring}", flush=True)
     with pytest.raises(FileNotFoundError):
         RINGS[ring](str(tmp_path / "nonexistent.store"), gpu)
+
+
+@pytest.mark.parametrize("ring", RINGS)
+def test_read_waits_for_earlier_work_on_the_destination(gpu, store_file, ring):
+    """A read into a buffer that earlier work on the consumer stream still
+    writes (here a delayed fill) lands after that work: the ring's copies
+    wait for the consumer stream, so the file's bytes are what remains."""
+    print(f"case: ring read ordering {ring}", flush=True)
+    nbytes = 2 * 1024 * 1024
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=gpu)
+    io = RINGS[ring](store_file, gpu, slot_bytes=256 * 1024, n_slots=4)
+    io.write_from_device(src, 0)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(100_000_000)  # keeps the fill below pending while the file is read
+    dst.fill_(7)
+    io.read_into_device(dst, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
+    io.close()
