@@ -15,8 +15,14 @@ Per-kernel durations come from HIP events recorded on the launch stream
 around every timed launch. cpu_baseline times the C oracle (one thread) on a
 bounded sample of the same shape on the host.
 
+Re-rotations are also timed on the same memory viewed as vLLM's 3-D
+PagedAttention caches (split-x K pages). --io adds the PCIe- and
+file-inclusive save/load of the connector's data plane, --serving the host
+cost of the connector's worker hooks on serving-shaped steps; neither is
+`value`.
+
 Usage: python bench.py [--steps K] [--warmup W] [--configs 2,3,4,5,6] [--no-cpu]
-                       [--no-ref-loop] [--io] [--calibrate]
+                       [--no-ref-loop] [--io] [--serving] [--calibrate]
 """
 
 from __future__ import annotations
