@@ -234,7 +234,7 @@ def test_missing_layer_saves_are_completed(gpu, tmp_path):
 def test_batched_load_matches_single_batch(gpu, tmp_path):
     """Scattering per batch while later batches are read, with one reader
     ring or several in parallel, gives the same caches as one scatter after
-    all reads."""
+    all reads, also when requests share a cached chunk (read once)."""
     print("case: batched load", flush=True)
     w, _ = _worker(tmp_path, rope_theta=500000.0)
     caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=35)
@@ -245,7 +245,13 @@ def test_batched_load_matches_single_batch(gpu, tmp_path):
     reqs = {
         "x": C.ReqLoadSpec("ka", 3, 3, [1, 12, 4], 3 * slot, 40, pos_offset=0, new_pos=300),
         "y": C.ReqLoadSpec("kb", 10, 1, [0], 10 * slot, 16),
+        # the same cached chunk again (read once, scattered twice), elsewhere
+        "z": C.ReqLoadSpec("ka", 3, 3, [5, 6, 8], 3 * slot, 40, pos_offset=0, new_pos=9000),
+        # part of it, as stored
+        "w": C.ReqLoadSpec("ka", 0, 0, [9], 0, 16, segments=[C.LoadSegment(4, 1, 0)]),
     }
+    plan = C.plan_load(reqs, slot)
+    assert len(plan.reads) == 2 and plan.shared_records
     outs = []
     for batch, readers in ((1, 1), (1 << 30, 1), (1, 4), (1 << 30, 3)):
         fresh = [torch.zeros_like(c) for c in caches]
@@ -259,7 +265,14 @@ def test_batched_load_matches_single_batch(gpu, tmp_path):
     for other in outs[1:]:
         for a, b in zip(outs[0], other):
             assert torch.equal(a, b)
-    assert torch.equal(outs[0][0][:, 0], caches[0][:, 7])
+    for l in range(SHAPE.num_layers):
+        got = outs[0][l]
+        assert torch.equal(got[:, 0], caches[l][:, 7])  # as stored
+        assert torch.equal(got[:, 9], caches[l][:, 9])  # stored slot 4 = block 9
+        # V of the shared chunk lands unchanged in both requests' blocks
+        assert torch.equal(got[1][[1, 12, 4]], caches[l][1][[5, 9, 2]])
+        assert torch.equal(got[1][[5, 6, 8]], caches[l][1][[5, 9, 2]])
+        assert not torch.equal(got[0][[1, 12, 4]], got[0][[5, 6, 8]])  # two positions
     w.shutdown()
 
 
