@@ -112,3 +112,49 @@ def test_direct_io_round_trip_and_alignment(store, uring):
     with pytest.raises(DaserKVError) as e:
         NativeRingIO(store, "cpu", slot_bytes=5000, direct=True)
     assert e.value.code == DSR_ERR_ALIGN
+
+
+@pytest.mark.parametrize("uring", [True, False])
+def test_randomized_transfers_from_several_threads(tmp_path, uring):
+    """Random sizes and offsets (pieces shorter and longer than a slot, odd
+    lengths) from four threads, each with its own ring on one file over
+    disjoint regions, and a shared ring used by two threads at once (its
+    calls serialise): the file and every read back equal a host model."""
+    import threading
+
+    path = str(tmp_path / "daser.store")
+    size = 8 << 20
+    preallocate_store(path, size)
+    model = np.zeros(size, np.uint8)
+    shared = NativeRingIO(path, "cpu", slot_bytes=8192, n_slots=3, use_io_uring=uring)
+    errors = []
+
+    def worker(t: int, ring) -> None:
+        try:
+            rng = np.random.default_rng(100 + t)
+            lo = t * (size // 6)
+            for _ in range(40):
+                n = int(rng.integers(1, 60_000))
+                off = lo + int(rng.integers(0, size // 6 - n))
+                data = rng.integers(0, 256, n, dtype=np.uint8)
+                ring.write_from_device(torch.from_numpy(data), off)
+                model[off:off + n] = data
+                back = torch.zeros(n, dtype=torch.uint8)
+                ring.read_into_device(back, off)
+                assert np.array_equal(back.numpy(), data), f"thread {t}"
+        except BaseException as e:  # reported on the main thread
+            errors.append(e)
+
+    own = [NativeRingIO(path, "cpu", slot_bytes=int(s), n_slots=int(k), use_io_uring=uring)
+           for s, k in ((4096, 1), (16384, 2), (65536, 4), (5000 * 16, 3))]
+    threads = [threading.Thread(target=worker, args=(t, r)) for t, r in enumerate(own)]
+    threads += [threading.Thread(target=worker, args=(4 + t, shared)) for t in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    for r in own + [shared]:
+        r.close()
+    assert not errors, errors[0]
+    with open(path, "rb") as f:
+        assert np.array_equal(np.frombuffer(f.read(), np.uint8), model)
