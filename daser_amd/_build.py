@@ -21,6 +21,8 @@ PROBE_SRC = os.path.join(HERE, "csrc", "hbm_probe.hip")
 PROBE_OUT = os.path.join(HERE, "hbm_probe")
 ABI_TEST_SRC = os.path.join(ROOT, "tests", "c", "abi_roundtrip.cpp")
 ABI_TEST_OUT = os.path.join(ROOT, "tests", "c", "abi_roundtrip")
+RING_SAN_SRC = os.path.join(ROOT, "tests", "c", "ring_sanitize.cpp")
+RING_SAN_OUT = os.path.join(ROOT, "tests", "c", "ring_sanitize")
 
 ARCH = "gfx950"
 
@@ -74,7 +76,28 @@ def build(verbose: bool = False) -> str:
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
     os.replace(ABI_TEST_OUT + ".tmp", ABI_TEST_OUT)
+    build_ring_sanitize(verbose)
     return OUT
+
+
+def build_ring_sanitize(verbose: bool = False) -> None:
+    """Best effort: the staging ring's host-mode driver under ASan and UBSan
+    (ROCm's clang, host code only), run by a CPU test. Skipped with a note
+    where the sanitizer runtimes are missing."""
+    clang = "/opt/rocm/llvm/bin/clang++"
+    if not os.path.exists(clang):
+        return
+    cmd = [clang, "-O1", "-g", "-fsanitize=address,undefined", "-fno-omit-frame-pointer",
+           "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", f"-I{INCLUDE}",
+           SRCS[1], RING_SAN_SRC, "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib",
+           "-o", RING_SAN_OUT + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        print(f"note: ring sanitizer driver not built ({proc.stderr.strip()[:200]})", flush=True)
+        return
+    os.replace(RING_SAN_OUT + ".tmp", RING_SAN_OUT)
 
 
 if __name__ == "__main__":

@@ -158,3 +158,15 @@ def test_randomized_transfers_from_several_threads(tmp_path, uring):
     assert not errors, errors[0]
     with open(path, "rb") as f:
         assert np.array_equal(np.frombuffer(f.read(), np.uint8), model)
+
+
+def test_ring_host_code_under_sanitizers():
+    """The C++ ring's host path under ASan + UBSan (tests/c/ring_sanitize.cpp,
+    built by the package build where the sanitizer runtimes exist)."""
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c", "ring_sanitize")
+    if not os.path.exists(exe):
+        pytest.skip("ring sanitizer driver not built (no sanitizer runtimes)")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "ring sanitize ok" in r.stdout, r.stdout + r.stderr
