@@ -158,8 +158,8 @@ __device__ __forceinline__ void copy_halves(const uint8_t* src_k, const uint8_t*
 // copy_halves between a head-major cache page and its record: the record
 // side is walked lane-consecutively, the cache side through hnd_vec (whole
 // rows stay contiguous, so a row's lanes still coalesce). Vectors past the
-// page go to offset page_bytes, outside the descriptors: loads read 0 and
-// stores are dropped.
+// page are skipped, as in copy_halves (issuing them against an empty range
+// cost 40% at 4 KiB pages).
 template <int U, bool kGather>
 __device__ __forceinline__ void copy_halves_hnd(const UnitArgs& a, uint8_t* cache,
                                                 uint8_t* rec) {
@@ -173,15 +173,20 @@ __device__ __forceinline__ void copy_halves_hnd(const UnitArgs& a, uint8_t* cach
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int i = base + k * kThreads;
-      ro[k] = i < nvec ? i << 4 : (int)pb;
-      co[k] = i < nvec ? hnd_vec(a, i) << 4 : (int)pb;
-      xk[k] = bload(kGather ? ck : rk, kGather ? co[k] : ro[k]);
-      xv[k] = bload(kGather ? cv : rv, kGather ? co[k] : ro[k]);
+      if (i < nvec) {
+        ro[k] = i << 4;
+        co[k] = hnd_vec(a, i) << 4;
+        xk[k] = bload(kGather ? ck : rk, kGather ? co[k] : ro[k]);
+        xv[k] = bload(kGather ? cv : rv, kGather ? co[k] : ro[k]);
+      }
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      bstore(kGather ? rk : ck, kGather ? ro[k] : co[k], xk[k]);
-      bstore(kGather ? rv : cv, kGather ? ro[k] : co[k], xv[k]);
+      const int i = base + k * kThreads;
+      if (i < nvec) {
+        bstore(kGather ? rk : ck, kGather ? ro[k] : co[k], xk[k]);
+        bstore(kGather ? rv : cv, kGather ? ro[k] : co[k], xv[k]);
+      }
     }
   }
 }

@@ -188,7 +188,7 @@ size_t rot_occupancy_lds(int wg_per_cu) {
 
 template <int DT>
 int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipStream_t s,
-                    bool kx, unsigned flags) {
+                    bool kx, unsigned flags, bool hnd = false) {
   const int h = ra.half_vecs;
   int wg = rot_wg_per_cu<DT>();
   if (const char* e = getenv("DSR_ROT_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
@@ -205,7 +205,7 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
   }
   // split-x K (kx): the caller checked the kx_phys conditions, which make
   // every neox partner lane ^ 32
-  const bool contig = kx || style == DSR_ROPE_GPTJ ||
+  const bool contig = kx || hnd || style == DSR_ROPE_GPTJ ||
                       (h > 0 && h <= 32 && (h & (h - 1)) == 0 && ra.row_vecs % (2 * h) == 0);
   const int G = contig ? units_per_group(ra.u.page_bytes, rot_contig_unroll<DT>(),
                                          kMaxRotHalf / ra.rot_half)
@@ -242,7 +242,11 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
     rb.u = b;
     rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
     if (grouped) {
-      if (style == DSR_ROPE_NEOX && kx)
+      if (hnd && style == DSR_ROPE_NEOX)
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX, false, true><<<grid, kThreads, dyn, s>>>(rb, GL);
+      else if (hnd)
+        kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ, false, true><<<grid, kThreads, dyn, s>>>(rb, GL);
+      else if (style == DSR_ROPE_NEOX && kx)
         kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX, true><<<grid, kThreads, dyn, s>>>(rb, GL);
       else if (style == DSR_ROPE_NEOX)
         kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_NEOX, false><<<grid, kThreads, dyn, s>>>(rb, GL);
@@ -251,7 +255,11 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
       else
         kv_scatter_rerotate_grouped_kernel<DT, DSR_ROPE_GPTJ, false><<<grid, kThreads, dyn, s>>>(rb, GL);
     } else if (contig) {
-      if (style == DSR_ROPE_NEOX && kx)
+      if (hnd && style == DSR_ROPE_NEOX)
+        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX, false, true><<<grid, kThreads, dyn, s>>>(rb);
+      else if (hnd)
+        kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ, false, true><<<grid, kThreads, dyn, s>>>(rb);
+      else if (style == DSR_ROPE_NEOX && kx)
         kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX, true><<<grid, kThreads, dyn, s>>>(rb);
       else if (style == DSR_ROPE_NEOX)
         kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX, false><<<grid, kThreads, dyn, s>>>(rb);
@@ -264,22 +272,6 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
     } else {
       kv_scatter_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(rb);
     }
-  });
-}
-
-// Head-major cache pages: the contig kernel with the HND store mapping, one
-// unit per workgroup, at the one-unit kernels' occupancy.
-template <int DT>
-int launch_rerotate_hnd(const RotArgs& ra, int n_pages, int style, hipStream_t s) {
-  const size_t dyn = rot_occupancy_lds(rot_wg_per_cu<DT>());
-  return launch_page_ranges(ra.u, n_pages, 1, [&](const UnitArgs& b, unsigned grid) {
-    RotArgs rb = ra;
-    rb.u = b;
-    rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
-    if (style == DSR_ROPE_NEOX)
-      kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_NEOX, false, true><<<grid, kThreads, dyn, s>>>(rb);
-    else
-      kv_scatter_rerotate_contig_kernel<DT, DSR_ROPE_GPTJ, false, true><<<grid, kThreads, dyn, s>>>(rb);
   });
 }
 
@@ -452,8 +444,8 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
   ra.k_scale = k_scale;
   hipStream_t s = (hipStream_t)stream;
   if (hnd_block > 0) {
-    // head-major pages: the contig kernel only (rows and partners stay whole
-    // in record order; the cache side goes through hnd_vec)
+    // head-major pages: the contig or grouped kernels (rows and partners
+    // stay whole in record order; the cache side goes through hnd_vec)
     const int h = ra.half_vecs;
     const bool contig = vec_ok && (rope_style == DSR_ROPE_GPTJ ||
                                    (h > 0 && h <= 32 && (h & (h - 1)) == 0 &&
@@ -465,11 +457,14 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
     ra.u.hnd_row_vecs = ra.row_vecs;
     switch (dtype) {
       case DSR_DTYPE_BF16:
-        return launch_rerotate_hnd<DSR_DTYPE_BF16>(ra, n_pages, rope_style, s);
+        return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, true, s, false, flags,
+                                               true);
       case DSR_DTYPE_FP16:
-        return launch_rerotate_hnd<DSR_DTYPE_FP16>(ra, n_pages, rope_style, s);
+        return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, true, s, false, flags,
+                                               true);
       default:
-        return launch_rerotate_hnd<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, s);
+        return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, true, s, false,
+                                                   flags, true);
     }
   }
   if (kx_block > 0) {
@@ -599,11 +594,21 @@ int copy_hnd(bool gather, const uint64_t* layer_base, int n_layers, int64_t kv_s
   a.hnd_heads = num_heads;
   a.hnd_block = block_size;
   a.hnd_row_vecs = (int)(page_bytes / rows / 16);
-  return launch_page_ranges(a, n_pages, 1, [&](const UnitArgs& b, unsigned grid) {
-    if (gather)
-      kv_copy_hnd_kernel<true><<<grid, kThreads, 0, (hipStream_t)stream>>>(b);
+  // units per workgroup as for token-major pages (dsr_gather / dsr_scatter)
+  const int G = gather ? (page_bytes < kThreads * 16
+                              ? units_per_group(page_bytes, kGatherUnroll, kMaxGroup) : 1)
+                       : (page_bytes <= kThreads * 16
+                              ? units_per_group(page_bytes, kScatterUnroll, kMaxGroup) : 1);
+  hipStream_t s = (hipStream_t)stream;
+  return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
+    if (G > 1 && gather)
+      kv_copy_grouped_kernel<true, kGatherUnroll, true><<<grid, kThreads, 0, s>>>(b, G);
+    else if (G > 1)
+      kv_copy_grouped_kernel<false, kScatterUnroll, true><<<grid, kThreads, 0, s>>>(b, G);
+    else if (gather)
+      kv_copy_hnd_kernel<true><<<grid, kThreads, 0, s>>>(b);
     else
-      kv_copy_hnd_kernel<false><<<grid, kThreads, 0, (hipStream_t)stream>>>(b);
+      kv_copy_hnd_kernel<false><<<grid, kThreads, 0, s>>>(b);
   });
 }
 

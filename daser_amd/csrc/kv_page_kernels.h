@@ -151,8 +151,9 @@ __device__ __forceinline__ int64_t group_start(const UnitArgs& a, int64_t g, int
 }
 
 // Gather (kGather: page-major, cache -> records) or scatter (layer-major,
-// records -> cache) over G units per workgroup.
-template <bool kGather, int U>
+// records -> cache) over G units per workgroup. HND: head-major cache pages
+// (the cache side of each vector goes through hnd_vec).
+template <bool kGather, int U, bool HND = false>
 __global__ __launch_bounds__(kThreads) void kv_copy_grouped_kernel(UnitArgs a, int G) {
   const int64_t g = xcd_unit((a.n_units + G - 1) / G);
   if (g < 0) return;
@@ -165,26 +166,28 @@ __global__ __launch_bounds__(kThreads) void kv_copy_grouped_kernel(UnitArgs a, i
   const int lane = (int)threadIdx.x % kWave;
   u32x4 rk[U], rv[U];
   rsrc_t dk[U], dv[U];
-  int off[U];
+  int off[U], doff[U];
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const int fw = k * kThreads + wave * kWave;  // first flat vector of this wave
     const int j = fw / nvec;
     off[k] = (fw - j * nvec + lane) << 4;
+    const int coff = HND ? hnd_vec(a, off[k] >> 4) << 4 : off[k];  // cache side
     const UnitRsrc u = unit_rsrc<kGather>(a, n_pages, p0, l0, j, n_here);
     const uint8_t* src = kGather ? u.cache : u.rec;
     const uint8_t* src_v = kGather ? u.cache + a.kv_stride : u.rec + a.page_bytes;
     const uint8_t* dst = kGather ? u.rec : u.cache;
     const uint8_t* dst_v = kGather ? u.rec + a.page_bytes : u.cache + a.kv_stride;
-    rk[k] = bload(make_rsrc(src, u.n), off[k]);
-    rv[k] = bload(make_rsrc(src_v, u.n), off[k]);
+    rk[k] = bload(make_rsrc(src, u.n), kGather ? coff : off[k]);
+    rv[k] = bload(make_rsrc(src_v, u.n), kGather ? coff : off[k]);
     dk[k] = make_rsrc(dst, u.n);
     dv[k] = make_rsrc(dst_v, u.n);
+    doff[k] = kGather ? off[k] : coff;
   }
 #pragma unroll
   for (int k = 0; k < U; ++k) {
-    bstore(dk[k], off[k], rk[k]);
-    bstore(dv[k], off[k], rv[k]);
+    bstore(dk[k], doff[k], rk[k]);
+    bstore(dv[k], doff[k], rv[k]);
   }
 }
 

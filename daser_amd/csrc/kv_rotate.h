@@ -673,7 +673,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_lds_kernel(RotAr
 // kernel). The group's (cos, sin) tables are staged in LDS, one rot_half
 // stretch per unit; G * rot_half <= kMaxRotHalf. K of an un-rotated unit is
 // stored as loaded.
-template <int DT, int STYLE, bool KX>
+template <int DT, int STYLE, bool KX, bool HND = false>
 __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(RotArgs ra,
                                                                                int G) {
   constexpr int U = rot_contig_unroll<DT>();
@@ -694,12 +694,14 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
   float sc[U];  // its layer's K scale (e4m3)
   int off[U];
   int koff[U];  // K: split-x pages move vector kx_phys(i) in lane slot i
+  int coff[U];  // cache-side offset of record vector i (head-major: hnd_vec)
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const int fw = k * kThreads + wave * kWave;
     const int j = fw / nvec;
     off[k] = (fw - j * nvec + lane) << 4;
     koff[k] = KX ? kx_phys(ra, off[k] >> 4) << 4 : off[k];
+    coff[k] = HND ? hnd_vec(a, off[k] >> 4) << 4 : koff[k];
     const UnitRsrc u = unit_rsrc<false>(a, n_pages, p0, l0, j, n_here);
     rk[k] = bload(make_rsrc(u.rec, u.n), koff[k]);
     rv[k] = bload(make_rsrc(u.rec + a.page_bytes, u.n), off[k]);
@@ -718,7 +720,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
     if (ti >= 0) tab[e] = ra.cos_sin[(int64_t)ti * ra.rot_half + (e - jj * ra.rot_half)];
   }
 #pragma unroll
-  for (int k = 0; k < U; ++k) bstore(vd[k], off[k], rv[k]);
+  for (int k = 0; k < U; ++k) bstore(vd[k], HND ? coff[k] : off[k], rv[k]);
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < U; ++k) {
@@ -731,7 +733,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
     const int t = tj[k] < 0 ? 0 : tj[k];
     const u32x4 r = rotate_vec<DT, STYLE>(ra, rk[k], q, k_column<KX>(ra, koff[k] >> 4),
                                           tab + t * ra.rot_half, sc[k], 1.0f / sc[k]);
-    bstore(kd[k], koff[k], tj[k] < 0 ? rk[k] : r);
+    bstore(kd[k], coff[k], tj[k] < 0 ? rk[k] : r);
   }
 }
 

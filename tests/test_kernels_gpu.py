@@ -1150,6 +1150,8 @@ def _hnd_caches(shape, nb, dt, gpu, seed, scale=1.0):
 
 @pytest.mark.parametrize("heads,head_dim,bs,dt", [
     (8, 128, 16, "bf16"), (2, 64, 16, "bf16"), (4, 128, 32, "e4m3"), (3, 96, 16, "bf16"),
+    (2, 32, 16, "bf16"),   # 2 KiB pages: the grouped copies
+    (4, 64, 16, "e4m3"),   # 4 KiB e4m3: grouped scatter, one-unit gather
 ])
 def test_hnd_copies_match_oracle(gpu, heads, head_dim, bs, dt):
     """Gather from head-major pages writes the records of the logical page
@@ -1190,6 +1192,9 @@ def test_hnd_copies_match_oracle(gpu, heads, head_dim, bs, dt):
 @pytest.mark.parametrize("heads,head_dim,rot,dt,style", [
     (8, 128, 128, "bf16", "neox"), (2, 64, 64, "bf16", "neox"), (4, 128, 128, "e4m3", "neox"),
     (2, 128, 128, "bf16", "gptj"), (4, 128, 64, "bf16", "neox"),
+    (2, 128, 128, "e4m3", "neox"),  # 4 KiB e4m3 pages: grouped
+    (2, 32, 32, "bf16", "neox"),    # 2 KiB pages: grouped, 16 units per workgroup
+    (16, 128, 128, "bf16", "neox"),  # 64 KiB pages: contig in rounds
 ])
 def test_hnd_rerotate_equals_token_major(gpu, heads, head_dim, rot, dt, style):
     """Re-rotation into head-major pages gives, per logical element, exactly
