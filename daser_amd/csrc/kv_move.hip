@@ -33,6 +33,9 @@
 //     rows of <= 32 vectors, kv_slots_kernel above.
 //   split-x K pages (dsr_scatter_rerotate_kx): the contig and grouped
 //     kernels with the KX flag, or the pair-task kernel.
+//   head-major cache pages (dsr_*_hnd): the same kernels as token-major
+//     pages of that size with the HND flag (kv_copy_hnd_kernel for one unit
+//     per workgroup), whose cache-side offsets go through hnd_vec.
 // Calls too large for one launch run as several over page (token) ranges.
 //
 // Reference being replaced: the Python per-(request, block, layer) torch
