@@ -826,6 +826,32 @@ def test_random_geometry_parity(gpu, dt, D, H, bs, style, R, L, seed):
                 2, nb, bs, H, D)
             assert torch.equal(back.view(torch.uint8), rot[l].view(torch.uint8)), \
                 f"split-x layer {l}"
+    # head-major (HND) pages holding the same values: the same records, and
+    # (where the contig / grouped kernels apply) the same re-rotated bits
+    if H > 1 and bs > 1:
+        def hnd_like(cs):
+            out = []
+            for c in cs:
+                m = torch.empty((2, nb, H, bs, D), dtype=c.dtype, device=gpu)
+                v = m.permute(0, 1, 3, 2, 4)
+                v.copy_(c)
+                out.append(v)
+            return out
+        st_h = torch.zeros_like(st)
+        ops.gather(ops.LayerTable(hnd_like(src)), ids, offs, st_h)
+        torch.cuda.synchronize()
+        assert torch.equal(st_h, st), "head-major gather"
+        hv = (R // 2) * e // 16 if style == "neox" else 0
+        row_vecs = D * e // 16
+        if whole and (style == "gptj" or (0 < hv <= 32 and hv & (hv - 1) == 0
+                                          and row_vecs % (2 * hv) == 0)):
+            hr = hnd_like([torch.zeros_like(c) for c in src])
+            ops.scatter_rerotate(ops.LayerTable(hr), dst_ids, offs, st, tabs, ridx, rot_dim=R,
+                                 style=style, k_scale=ks)
+            torch.cuda.synchronize()
+            for l in range(L):
+                assert torch.equal(hr[l].contiguous().view(torch.uint8),
+                                   rot[l].view(torch.uint8)), f"head-major layer {l}"
 
 
 @pytest.mark.parametrize("dt,D,H,bs,style,R,L,seed", _random_cases(max(1, _N_RANDOM // 2), 77))
