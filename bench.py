@@ -12,8 +12,11 @@ configs 3 (RAG reuse), 4 (e4m3), 5 (70B share) and 6 (one TP8 rank of 70B:
 one KV head, 4 KiB pages) are reported beside it.
 
 Per-kernel durations come from HIP events recorded on the launch stream
-around every timed launch. cpu_baseline times the C oracle (one thread) on a
-bounded sample of the same shape on the host.
+around every timed launch. cpu_baseline times the reference's own copy loops
+(per page and layer torch copy_, daser_connector.py:536-551, 625-632),
+restated on host tensors with torch on every host core of the process's
+affinity, on a bounded sample of the same shape; cpu_port is the C oracle on
+one thread, cpu_rerotate an fp32 torch rotate-half on all cores.
 
 Re-rotations are also timed on the same memory viewed as vLLM's 3-D
 PagedAttention caches (split-x K pages). --io adds the PCIe- and
@@ -524,6 +527,17 @@ def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int 
     return out
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def reference_loop(torch, dev, budget_s: float = 6.0) -> dict:
     """The reference's own copy path, timed on `dev` (the GPU, or "cpu"):
     save = for each page, for each layer,
@@ -593,7 +607,7 @@ def pmc_traffic(kernel: str, config: int, pages: int):
     return None
 
 
-def cpu_baseline(budget_s: float = 12.0) -> dict:
+def cpu_port(budget_s: float = 8.0) -> dict:
     """C oracle (single thread) gather+scatter on a sample of config 2's
     shape: 256 pages of a 1024-block host pool, repeated to ~budget_s."""
     from daser_amd import workloads
@@ -802,14 +816,19 @@ def main() -> int:
         log("[bench] reference copy loop on the GPU")
         out["reference_loop_gpu"] = reference_loop(torch, dev)
     if not args.no_cpu:
-        log("[bench] cpu baseline (C oracle, one thread)")
-        out["cpu_baseline"] = cpu_baseline()
         ncpu = len(os.sched_getaffinity(0))
         torch.set_num_threads(ncpu)
-        log(f"[bench] reference copy loop on the CPU ({ncpu} threads)")
-        r = reference_loop(torch, torch.device("cpu"), budget_s=10.0)
-        r["threads"] = ncpu
-        out["cpu_reference_loop"] = r
+        log(f"[bench] cpu baseline: the reference's copy loops in torch on the CPU "
+            f"({ncpu} threads)")
+        r = reference_loop(torch, torch.device("cpu"), budget_s=12.0)
+        out["cpu_baseline"] = {
+            "value": r["GBps"], "unit": "GB/s", "cores": ncpu, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": "torch restatement of daser_connector.py:625-632 (save: reshape + copy_ "
+                      "per page and layer) and :536-551 (load: copy_ per page and layer) on "
+                      f"host tensors, {torch.get_num_threads()} torch threads; {r['sample']}"}
+        log("[bench] C oracle gather+scatter on the CPU (one thread)")
+        out["cpu_port"] = cpu_port()
         log(f"[bench] fp32 torch re-rotation on the CPU ({ncpu} threads)")
         out["cpu_rerotate"] = cpu_rerotate(torch)
     print(json.dumps(out), flush=True)

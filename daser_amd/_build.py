@@ -17,8 +17,6 @@ ROOT = os.path.dirname(HERE)
 SRCS = [os.path.join(HERE, "csrc", "kv_move.hip"), os.path.join(HERE, "csrc", "store_ring.cpp")]
 INCLUDE = os.path.join(ROOT, "include")
 OUT = os.path.join(HERE, "libdaser_kv.so")
-PROBE_SRC = os.path.join(HERE, "csrc", "hbm_probe.hip")
-PROBE_OUT = os.path.join(HERE, "hbm_probe")
 ABI_TEST_SRC = os.path.join(ROOT, "tests", "c", "abi_roundtrip.cpp")
 ABI_TEST_OUT = os.path.join(ROOT, "tests", "c", "abi_roundtrip")
 RING_SAN_SRC = os.path.join(ROOT, "tests", "c", "ring_sanitize.cpp")
@@ -58,15 +56,6 @@ def build(verbose: bool = False) -> str:
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
     os.replace(tmp, OUT)
-    # the HBM ceiling probe (a stand-alone executable, not part of the library)
-    flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
-    cmd = [hipcc(), *flags, PROBE_SRC, "-o", PROBE_OUT + ".tmp"]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
-    os.replace(PROBE_OUT + ".tmp", PROBE_OUT)
     # a C++ caller of the C ABI (no Python, no torch), run by the GPU tests
     cmd = [hipcc(), "-O2", "-std=c++17", f"-I{INCLUDE}", ABI_TEST_SRC, "-o", ABI_TEST_OUT + ".tmp",
            f"-L{HERE}", "-ldaser_kv", "-Wl,-rpath,$ORIGIN/../../daser_amd"]

@@ -20,7 +20,7 @@ LIB_PATH = os.environ.get("DASER_KV_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so"
 )
 
-DSR_ABI_VERSION = 5
+DSR_ABI_VERSION = 6
 DSR_OK = 0
 DSR_ERR_ARG = -1
 DSR_ERR_ALIGN = -2
@@ -41,6 +41,11 @@ DSR_ROPE_GPTJ = 1
 
 DSR_REROTATE_SHARED_RECORDS = 1
 
+# dsr_set_tuning knobs (measurements and tests only)
+TUNE = {"units_per_group": 0, "max_wg_per_launch": 1, "rot_kernel": 2, "rot_wg_per_cu": 3,
+        "rot_grouped_wg_per_cu": 4, "slots_tpw": 5, "slots_kernel": 6, "slots_unroll": 7}
+ROT_KERNEL_CODES = {"auto": 0, "pairs": 1, "contig": 2, "grouped": 3}
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
@@ -51,6 +56,7 @@ _SLOT_ARGS = [_P, _I, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _I, _P, _I64, _I
 SIGNATURES = {
     "dsr_abi_version": ([], _I),
     "dsr_error_string": ([_I], ctypes.c_char_p),
+    "dsr_set_tuning": ([_I, _I64], _I),
     "dsr_gather": (_COPY_ARGS, _I),
     "dsr_scatter": (_COPY_ARGS, _I),
     "dsr_gather_slots": (_SLOT_ARGS, _I),
@@ -117,3 +123,14 @@ def check(fn: str, code: int) -> None:
     if code != DSR_OK:
         text = lib().dsr_error_string(code).decode()
         raise DaserKVError(fn, code, text)
+
+
+def set_tuning(knob: str, value) -> None:
+    """Launch-shape override for measurements and tests (``TUNE`` names;
+    ``rot_kernel`` also takes "auto" / "pairs" / "contig" / "grouped",
+    ``slots_kernel`` "small"); 0 or "auto" restores the default."""
+    if knob == "rot_kernel" and isinstance(value, str):
+        value = ROT_KERNEL_CODES[value]
+    elif knob == "slots_kernel" and isinstance(value, str):
+        value = 1 if value == "small" else 0
+    check("dsr_set_tuning", lib().dsr_set_tuning(TUNE[knob], int(value)))

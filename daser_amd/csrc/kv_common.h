@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "daser_kv.h"
 
 namespace {
@@ -30,6 +32,17 @@ constexpr int kXcds = 8;           // MI355X: 8 XCDs, workgroups dealt round-rob
 // default-policy stores at the Llama-3-8B shape).
 constexpr int kLoadPolicy = 2;
 constexpr int kStorePolicy = 17;
+// Launch-shape overrides for measurements and tests, set through
+// dsr_set_tuning() (0 = the geometry's own choice). Nothing reads the
+// environment: a serving process gets the defaults unless its code asks.
+// Relaxed atomics, read once per call.
+enum RotKernelOverride { kRotAuto = 0, kRotPairs = 1, kRotContig = 2, kRotGrouped = 3 };
+struct TuningKnobs {
+  std::atomic<int64_t> v[DSR_TUNE_COUNT_];
+};
+TuningKnobs g_tuning{};
+inline int64_t tune(int knob) { return g_tuning.v[knob].load(std::memory_order_relaxed); }
+
 // Buffer descriptor word 3 for raw (untyped) dword access on CDNA3/4.
 constexpr int kRsrcWord3 = 0x00020000;
 

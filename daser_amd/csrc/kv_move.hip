@@ -101,12 +101,12 @@ UnitArgs make_unit(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
 }
 
 // Largest workgroup count of one launch: HIP caps gridDim.x * blockDim.x at
-// 2^32 - 1 threads (16.7 M workgroups of 256). Env DSR_MAX_WG_PER_LAUNCH
-// lowers it, so that tests can exercise the split.
+// 2^32 - 1 threads (16.7 M workgroups of 256). The DSR_TUNE_MAX_WG_PER_LAUNCH
+// override lowers it, so that tests can exercise the split.
 int64_t max_wg_per_launch() {
   int64_t m = 0xffffffffLL / kThreads / kXcds * kXcds;
-  if (const char* e = getenv("DSR_MAX_WG_PER_LAUNCH")) {
-    const int64_t v = atoll(e) / kXcds * kXcds;
+  if (const int64_t t = tune(DSR_TUNE_MAX_WG_PER_LAUNCH)) {
+    const int64_t v = t / kXcds * kXcds;
     if (v >= 2 * kXcds && v < m) m = v;
   }
   return m;
@@ -145,7 +145,7 @@ int launch_page_ranges(const UnitArgs& a, int n_pages, int G, F launch) {
 }
 
 // Workgroups per CU for the re-rotation kernel, applied with dynamic LDS
-// sized from the CU's LDS capacity (env DSR_ROT_WG_PER_CU overrides, for
+// sized from the CU's LDS capacity (the DSR_TUNE_ROT_WG_PER_CU override changes it, for
 // tuning). Measured in-process at the Llama-3-8B shapes: 16-bit K (64 KiB
 // per unit) runs best at 2-3 per CU (7.67 ms vs 7.87 ms at 4-8 and 11.0 ms
 // at 1); e4m3 (32 KiB per unit) at 4 per CU (24.17 ms; 24.4-24.5 ms at 6-12,
@@ -194,7 +194,8 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
                     bool kx, unsigned flags, bool hnd = false) {
   const int h = ra.half_vecs;
   int wg = rot_wg_per_cu<DT>();
-  if (const char* e = getenv("DSR_ROT_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
+  if (const int64_t t = tune(DSR_TUNE_ROT_WG_PER_CU)) wg = t > 0 ? (int)t : wg;
+  const int64_t rot_kernel = tune(DSR_TUNE_ROT_KERNEL);
   if (!vec_ok) {  // rotary width not in whole vectors: the LDS kernel
     return launch_page_ranges(ra.u, n_pages, 1, [&](const UnitArgs& b, unsigned grid) {
       RotArgs rb = ra;
@@ -214,27 +215,24 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
                                          kMaxRotHalf / ra.rot_half)
                        : 1;
   // neox rows of <= 64 vectors whatever the partner distance: the row-aligned
-  // kernel (env DSR_ROT_KERNEL=pairs keeps the pair-task kernel).
+  // kernel (the DSR_TUNE_ROT_KERNEL override "pairs" keeps the pair-task kernel).
   bool rows_ok = !contig && style == DSR_ROPE_NEOX && ra.row_vecs <= kWave && h > 0 &&
                  2 * h <= ra.row_vecs;
-  if (const char* e = getenv("DSR_ROT_KERNEL"))
-    if (!strcmp(e, "pairs")) rows_ok = false;
+  if (rot_kernel == kRotPairs) rows_ok = false;
   // The grouped kernel also serves pages of exactly U vectors per lane
-  // (G = 1), for 16-bit K. Env DSR_ROT_KERNEL=contig|grouped overrides the
+  // (G = 1), for 16-bit K. The DSR_TUNE_ROT_KERNEL override (contig, grouped) changes the
   // choice where both apply, for in-process comparisons.
   const int64_t nvec = ra.u.page_bytes >> 4;
   const bool single = contig && nvec % kThreads == 0 &&
                       nvec == (int64_t)rot_contig_unroll<DT>() * kThreads;
   bool grouped = G > 1 || (single && DT != DSR_DTYPE_FP8_E4M3);
-  if (const char* e = getenv("DSR_ROT_KERNEL")) {
-    if (!strcmp(e, "contig") && contig) grouped = false;
-    if (!strcmp(e, "grouped") && (G > 1 || single)) grouped = true;
-  }
+  if (rot_kernel == kRotContig && contig) grouped = false;
+  if (rot_kernel == kRotGrouped && (G > 1 || single)) grouped = true;
   if (grouped) {
     wg = G > 1 ? rot_grouped_wg_per_cu<DT>()
          : (flags & DSR_REROTATE_SHARED_RECORDS) ? kRotSingleSharedWgPerCu
                                                  : kRotSingleWgPerCu;
-    if (const char* e = getenv("DSR_ROT_GROUPED_WG_PER_CU")) wg = atoi(e) > 0 ? atoi(e) : wg;
+    if (const int64_t t = tune(DSR_TUNE_ROT_GROUPED_WG_PER_CU)) wg = t > 0 ? (int)t : wg;
   }
   const size_t dyn = rot_occupancy_lds(wg);
   // units per workgroup of the kernel actually launched: the one-unit
@@ -299,6 +297,12 @@ int launch_rerotate_pairs(const RotArgs& ra, int n_pages, int style, hipStream_t
 extern "C" {
 
 int dsr_abi_version(void) { return DSR_ABI_VERSION; }
+
+int dsr_set_tuning(int knob, int64_t value) {
+  if (knob < 0 || knob >= DSR_TUNE_COUNT_ || value < 0) return DSR_ERR_ARG;
+  g_tuning.v[knob].store(value, std::memory_order_relaxed);
+  return DSR_OK;
+}
 
 const char* dsr_error_string(int code) {
   switch (code) {
@@ -478,7 +482,7 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
     const int dist = rope_style == DSR_ROPE_NEOX ? task_vecs * kx_block : 0;
     const bool pow2 = (hv & (hv - 1)) == 0 && (kx_block & (kx_block - 1)) == 0;
     if (pow2 && hv >= kWave && dist % 32 == 0 && page_bytes % 1024 == 0 &&
-        !(getenv("DSR_ROT_KERNEL") && !strcmp(getenv("DSR_ROT_KERNEL"), "pairs"))) {
+        tune(DSR_TUNE_ROT_KERNEL) != kRotPairs) {
       ra.kx_row_shift = __builtin_ctzll((unsigned long long)hv);
       ra.kx_bs_shift = __builtin_ctz((unsigned)kx_block);
       ra.kx_dist = dist;
@@ -662,15 +666,14 @@ int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t 
   // 80 layers): 8 at 16-vector rows (4.34 ms gather vs 4.39 at 4 and 16),
   // 4 at 32-vector rows (8.19 ms vs 8.35-8.45). 0: the large-row kernel.
   int tpw = vpr <= 16 ? 8 : vpr <= 32 ? 4 : 0;
-  if (const char* e = getenv("DSR_SLOTS_TPW"))  // tuning override for small rows
-    if (tpw && (atoi(e) == 4 || atoi(e) == 8 || atoi(e) == 16)) tpw = atoi(e);
+  if (const int64_t t = tune(DSR_TUNE_SLOTS_TPW))  // override for small rows
+    if (tpw && (t == 4 || t == 8 || t == 16)) tpw = (int)t;
   // power-of-two rows of <= 8 vectors: the packed kernel, U instructions
   // per wave (4 and 8 measured alike; 16 spills)
   int pk_u = vpr <= 8 && (vpr & (vpr - 1)) == 0 && (block_size & (block_size - 1)) == 0 ? 8 : 0;
-  if (const char* e = getenv("DSR_SLOTS_KERNEL"))
-    if (!strcmp(e, "small")) pk_u = 0;
-  if (const char* e = getenv("DSR_SLOTS_UNROLL"))
-    if (pk_u && (atoi(e) == 4 || atoi(e) == 8)) pk_u = atoi(e);
+  if (tune(DSR_TUNE_SLOTS_KERNEL) == 1) pk_u = 0;
+  if (const int64_t t = tune(DSR_TUNE_SLOTS_UNROLL))
+    if (pk_u && (t == 4 || t == 8)) pk_u = (int)t;
   const int pk_s = pk_u ? __builtin_ctzll((unsigned long long)vpr) : 0;
   const int tok_wg = pk_u ? (kWave >> pk_s) * pk_u * (kThreads / kWave)
                      : tpw ? tpw * (kThreads / kWave) : kTokPerWg;

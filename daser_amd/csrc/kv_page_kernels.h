@@ -64,12 +64,11 @@ __global__ __launch_bounds__(kThreads) void kv_copy_hnd_kernel(UnitArgs a) {
 
 // Units per workgroup for the grouped kernels, 1 when the page does not
 // qualify or one unit already fills the budget of U vectors per lane. Env
-// DSR_UNITS_PER_GROUP caps G (1 turns the grouped kernels off), for
+// The DSR_TUNE_UNITS_PER_GROUP override caps G (1 turns the grouped kernels off), for
 // in-process comparisons.
 int units_per_group(int64_t page_bytes, int u_budget, int cap) {
-  if (const char* e = getenv("DSR_UNITS_PER_GROUP")) {
-    const int c = atoi(e);
-    if (c > 0 && c < cap) cap = c;
+  if (const int64_t c = tune(DSR_TUNE_UNITS_PER_GROUP)) {
+    if (c > 0 && c < cap) cap = (int)c;
   }
   const int64_t nvec = page_bytes >> 4;
   if (nvec % kWave) return 1;

@@ -46,24 +46,38 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 
 /* Bumped whenever an entry point's signature changes or one is added:
  * 2 layer_group on the re-rotation, 3 dsr_scatter_rerotate_kx, 4 the
- * re-rotations' flags, 5 the head-major (_hnd) entry points. Callers check
+ * re-rotations' flags, 5 the head-major (_hnd) entry points, 6
+ * dsr_set_tuning. Callers check
  * dsr_abi_version() against it. */
-#define DSR_ABI_VERSION 5
+#define DSR_ABI_VERSION 6
 
 /*
- * Kernel choice and launch shape follow from the geometry; these environment
- * variables, read at every call, override them for measurements and tests
- * only (results are the same bytes; leave them unset in production):
- *   DSR_UNITS_PER_GROUP=n        cap the (page, layer) units per workgroup
- *                                of the small-page kernels (1: off)
- *   DSR_MAX_WG_PER_LAUNCH=n      split calls into launches of <= n workgroups
- *   DSR_ROT_KERNEL=contig|grouped|pairs   re-rotation kernel where several apply
- *   DSR_ROT_WG_PER_CU=n, DSR_ROT_GROUPED_WG_PER_CU=n   re-rotation occupancy
- *   DSR_SLOTS_TPW=4|8|16         tokens per wave of the small-row token kernels
- *   DSR_SLOTS_KERNEL=small       rows of <= 8 vectors: the small-row kernel
- *                                instead of the packed one
- *   DSR_SLOTS_UNROLL=4|8         instructions per wave of the packed kernel
+ * Kernel choice and launch shape follow from the geometry. dsr_set_tuning()
+ * overrides them for measurements and tests only (results are the same
+ * bytes); the library reads no environment variables. Knobs (value 0 = the
+ * geometry's own choice):
+ *   DSR_TUNE_UNITS_PER_GROUP      cap the (page, layer) units per workgroup
+ *                                 of the small-page kernels (1: off)
+ *   DSR_TUNE_MAX_WG_PER_LAUNCH    split calls into launches of <= n workgroups
+ *   DSR_TUNE_ROT_KERNEL           re-rotation kernel where several apply:
+ *                                 1 pairs, 2 contig, 3 grouped
+ *   DSR_TUNE_ROT_WG_PER_CU, DSR_TUNE_ROT_GROUPED_WG_PER_CU
+ *                                 re-rotation occupancy
+ *   DSR_TUNE_SLOTS_TPW            4|8|16 tokens per wave of the small-row
+ *                                 token kernels
+ *   DSR_TUNE_SLOTS_KERNEL         1: rows of <= 8 vectors take the small-row
+ *                                 kernel instead of the packed one
+ *   DSR_TUNE_SLOTS_UNROLL         4|8 instructions per wave of the packed kernel
  */
+#define DSR_TUNE_UNITS_PER_GROUP 0
+#define DSR_TUNE_MAX_WG_PER_LAUNCH 1
+#define DSR_TUNE_ROT_KERNEL 2
+#define DSR_TUNE_ROT_WG_PER_CU 3
+#define DSR_TUNE_ROT_GROUPED_WG_PER_CU 4
+#define DSR_TUNE_SLOTS_TPW 5
+#define DSR_TUNE_SLOTS_KERNEL 6
+#define DSR_TUNE_SLOTS_UNROLL 7
+#define DSR_TUNE_COUNT_ 8
 
 #define DSR_OK 0
 #define DSR_ERR_ARG (-1)   /* null pointer, negative count, bad enum     */
@@ -90,6 +104,12 @@ int dsr_abi_version(void);
 
 /* Human-readable text for a return code of this library. */
 const char* dsr_error_string(int code);
+
+/* Sets a launch-shape override (DSR_TUNE_*; 0 restores the default) for
+ * every later call in this process. No counterpart in the reference: a
+ * measurement and test hook, replacing per-call environment reads. Returns
+ * DSR_ERR_ARG for an unknown knob or a negative value. */
+int dsr_set_tuning(int knob, int64_t value);
 
 /*
  * Offload gather: for every page p in [0, n_pages) and layer l in

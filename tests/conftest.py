@@ -25,3 +25,20 @@ def gpu():
     import torch
 
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def tuning():
+    """Sets libdaser_kv launch-shape overrides (dsr_set_tuning) for one
+    test and restores every knob it touched to the default afterwards."""
+    from daser_amd import _lib
+
+    touched = set()
+
+    def set_knob(knob, value):
+        touched.add(knob)
+        _lib.set_tuning(knob, value)
+
+    yield set_knob
+    for knob in touched:
+        _lib.set_tuning(knob, 0)

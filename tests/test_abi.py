@@ -92,3 +92,19 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
         assert "no CPU fallback" in str(e)
     else:
         raise AssertionError("expected a RuntimeError")
+
+
+def test_set_tuning_checks_and_no_environment_reads():
+    """Launch-shape overrides come only through dsr_set_tuning: unknown
+    knobs and negative values are rejected, and no library source reads the
+    environment."""
+    lib = _lib.lib()
+    assert lib.dsr_set_tuning(-1, 0) == _lib.DSR_ERR_ARG
+    assert lib.dsr_set_tuning(len(_lib.TUNE), 0) == _lib.DSR_ERR_ARG
+    assert lib.dsr_set_tuning(_lib.TUNE["rot_kernel"], -2) == _lib.DSR_ERR_ARG
+    for knob in _lib.TUNE:
+        assert lib.dsr_set_tuning(_lib.TUNE[knob], 0) == _lib.DSR_OK
+    csrc = os.path.join(ROOT, "daser_amd", "csrc")
+    for name in os.listdir(csrc):
+        with open(os.path.join(csrc, name)) as f:
+            assert "getenv" not in f.read(), name

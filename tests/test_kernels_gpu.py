@@ -304,11 +304,11 @@ def test_rerotate_matches_oracle(gpu, dt, style, head_dim, rot_dim):
 
 
 @pytest.mark.parametrize("dt,head_dim", [("bf16", 80), ("fp16", 96), ("e4m3", 192)])
-def test_rerotate_pair_task_kernel_matches_oracle(gpu, monkeypatch, dt, head_dim):
+def test_rerotate_pair_task_kernel_matches_oracle(gpu, tuning, dt, head_dim):
     """The pair-task kernel (kept for rows of more than 64 vectors), forced
     on the shapes the row-aligned kernel serves by default."""
     print(f"case: rerotate pair-task {dt} D{head_dim}", flush=True)
-    monkeypatch.setenv("DSR_ROT_KERNEL", "pairs")
+    tuning("rot_kernel", "pairs")
     shape, dst, dst_ref, page_ids, page_delta = _rerotate_case(
         gpu, dt, "neox", head_dim, head_dim, scale=40.0 if dt == "e4m3" else 1.0)
     for l in range(shape.num_layers):
@@ -433,13 +433,13 @@ def test_rerotate_special_values(gpu, dt):
 ], ids=["cfg1", "row128", "row512", "row1k", "e4m3_row128", "row64_bs32", "row16",
         "row128_bs12"])
 @pytest.mark.parametrize("unroll", ["default", "4"])
-def test_slots_gather_scatter_match_oracle(gpu, monkeypatch, shape, unroll):
+def test_slots_gather_scatter_match_oracle(gpu, tuning, shape, unroll):
     """slot_mapping-driven token gather/scatter with ragged requests, partial
     last pages and padding tokens, at each row-size class of the kernels
     (rows of <= 8 vectors: the packed kernel, at both unrolls)."""
     print(f"case: slots gather/scatter {shape} unroll {unroll}", flush=True)
     if unroll != "default":
-        monkeypatch.setenv("DSR_SLOTS_UNROLL", unroll)
+        tuning("slots_unroll", int(unroll))
     wl = workloads.config(1) if shape is None else workloads.ragged(
         shape, 8, 100, 2000, seed=3, num_blocks=1024)
     shape = wl.shape
@@ -532,15 +532,15 @@ def test_large_page_geometry(gpu):
     (3, 1, 64, "e4m3"),    # 1 KiB: one unit per wave
 ])
 @pytest.mark.parametrize("group_cap", ["1", "2", "3", ""])
-def test_grouped_units_match_oracle(gpu, monkeypatch, layers, heads, head_dim, dt, group_cap):
+def test_grouped_units_match_oracle(gpu, tuning, layers, heads, head_dim, dt, group_cap):
     """Groups span layer boundaries (3 pages, fewer than a group) and end
     part-way; every grouping (1 = the one-unit kernels) gives the oracle's
     bytes for gather, scatter and re-rotation."""
     print(f"case: grouped L{layers} H{heads} D{head_dim} {dt} cap={group_cap!r}", flush=True)
     if group_cap:
-        monkeypatch.setenv("DSR_UNITS_PER_GROUP", group_cap)
+        tuning("units_per_group", int(group_cap))
     else:
-        monkeypatch.delenv("DSR_UNITS_PER_GROUP", raising=False)
+        tuning("units_per_group", 0)
     shape = KVShape(layers, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
     nb = 9
     src = rand_caches(shape, nb, dt, gpu, seed=60, scale=40.0 if dt == "e4m3" else 1.0)
@@ -589,14 +589,14 @@ def test_grouped_units_match_oracle(gpu, monkeypatch, layers, heads, head_dim, d
 
 
 @pytest.mark.parametrize("group_cap", ["1", ""])
-def test_grouped_units_skip_out_of_range(gpu, monkeypatch, group_cap):
+def test_grouped_units_skip_out_of_range(gpu, tuning, group_cap):
     """Device tables with an out-of-range block inside a group: that unit is
     skipped in every layer, its neighbours in the group still move."""
     print(f"case: grouped skip cap={group_cap!r}", flush=True)
     if group_cap:
-        monkeypatch.setenv("DSR_UNITS_PER_GROUP", group_cap)
+        tuning("units_per_group", int(group_cap))
     else:
-        monkeypatch.delenv("DSR_UNITS_PER_GROUP", raising=False)
+        tuning("units_per_group", 0)
     shape = KVShape(5, 1, 128, 16, 2)
     src = rand_caches(shape, 8, "bf16", gpu, seed=61)
     staging = torch.zeros(3 * shape.slot_bytes, dtype=torch.uint8, device=gpu)
@@ -632,7 +632,7 @@ def test_grouped_units_skip_out_of_range(gpu, monkeypatch, group_cap):
     (7, 1, 128, "bf16"),    # grouped (4 KiB pages)
     (5, 1, 128, "e4m3"),    # grouped (2 KiB pages)
 ])
-def test_launch_split_matches_single_launch(gpu, monkeypatch, layers, heads, head_dim, dt):
+def test_launch_split_matches_single_launch(gpu, tuning, layers, heads, head_dim, dt):
     """Calls whose workgroups exceed one launch's limit run as several
     launches over page (token) ranges; forced here with a limit of 16
     workgroups, every entry point writes the same bytes as one launch."""
@@ -672,9 +672,9 @@ def test_launch_split_matches_single_launch(gpu, monkeypatch, layers, heads, hea
         torch.cuda.synchronize()
         return outs
 
-    monkeypatch.delenv("DSR_MAX_WG_PER_LAUNCH", raising=False)
+    tuning("max_wg_per_launch", 0)
     one = run()
-    monkeypatch.setenv("DSR_MAX_WG_PER_LAUNCH", "16")
+    tuning("max_wg_per_launch", 16)
     split = run()
     for i, (a, b) in enumerate(zip(one, split)):
         assert torch.equal(a, b), f"output {i}"
@@ -938,15 +938,15 @@ def test_shared_records_hint_does_not_change_results(gpu, heads, head_dim, dt):
 
 @pytest.mark.parametrize("heads,head_dim,dt", [(1, 128, "bf16"), (1, 128, "e4m3"),
                                               (2, 64, "bf16")])
-def test_rerotate_contig_override_on_small_pages(gpu, monkeypatch, heads, head_dim, dt):
-    """Small pages default to the grouped kernel; DSR_ROT_KERNEL=contig runs
+def test_rerotate_contig_override_on_small_pages(gpu, tuning, heads, head_dim, dt):
+    """Small pages default to the grouped kernel; the "contig" rot_kernel override runs
     the one-unit contig kernel instead, which must then be launched with one
     unit per workgroup (every page written, same bits as the grouped
     kernel)."""
     print(f"case: contig override H{heads} D{head_dim} {dt}", flush=True)
     shape, dst, dst_ref, page_ids, _ = _rerotate_case(gpu, dt, "neox", head_dim, head_dim,
                                                       heads=heads, layers=3, seed=8)
-    monkeypatch.setenv("DSR_ROT_KERNEL", "contig")
+    tuning("rot_kernel", "contig")
     shape2, dst2, _, page_ids2, _ = _rerotate_case(gpu, dt, "neox", head_dim, head_dim,
                                                    heads=heads, layers=3, seed=8)
     torch.cuda.synchronize()
@@ -964,7 +964,7 @@ def test_rerotate_contig_override_on_small_pages(gpu, monkeypatch, heads, head_d
     (16, 128, "bf16", None),   # 64 KiB pages: contig kernel in rounds
     (4, 96, "bf16", "lds24"),  # rotary width 24 of 96: the LDS kernel
 ])
-def test_rerotate_per_layer_groups(gpu, monkeypatch, heads, head_dim, dt, kernel):
+def test_rerotate_per_layer_groups(gpu, tuning, heads, head_dim, dt, kernel):
     """Layers with different RoPE bases (local / global attention) and layers
     without RoPE: layer_group picks each layer's table block; group -1
     copies K. Each layer matches the oracle run with its own base."""
@@ -973,7 +973,7 @@ def test_rerotate_per_layer_groups(gpu, monkeypatch, heads, head_dim, dt, kernel
     if kernel == "lds24":
         rot = 24
     elif kernel:
-        monkeypatch.setenv("DSR_ROT_KERNEL", kernel)
+        tuning("rot_kernel", kernel)
     L = 6
     groups = np.array([0, 1, -1, 0, 1, -1], np.int32)
     thetas = [10000.0, 1000000.0]
@@ -1097,7 +1097,7 @@ def test_flat_cache_copies_bit_exact(gpu):
     ("bf16", "neox", 3, 96, 96),     # 12-vector columns: the pair-task kernel
 ])
 @pytest.mark.parametrize("kernel", ["auto", "pairs"])
-def test_rerotate_kx_layout_matches_oracle(gpu, monkeypatch, dt, style, heads, head_dim,
+def test_rerotate_kx_layout_matches_oracle(gpu, tuning, dt, style, heads, head_dim,
                                            rot_dim, kernel):
     """Split-x K pages (vLLM PagedAttention layout) re-rotated by the kernel
     equal the oracle's token-major re-rotation of the same pages moved into
@@ -1106,7 +1106,7 @@ def test_rerotate_kx_layout_matches_oracle(gpu, monkeypatch, dt, style, heads, h
     print(f"case: kx re-rotate {dt} {style} H{heads} D{head_dim} R{rot_dim} {kernel}",
           flush=True)
     if kernel == "pairs":
-        monkeypatch.setenv("DSR_ROT_KERNEL", "pairs")
+        tuning("rot_kernel", "pairs")
     bs, L = 16, 3
     shape = KVShape(L, heads, head_dim, bs, 1 if dt == "e4m3" else 2)
     rng = np.random.default_rng(17)
