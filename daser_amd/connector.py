@@ -54,7 +54,6 @@ from __future__ import annotations
 import array
 import asyncio
 import logging
-import math
 import threading
 from dataclasses import dataclass, field
 from typing import Any, Optional
@@ -82,8 +81,8 @@ from daser_amd.data_plane import (  # noqa: E402
 )
 
 __all__ = ["DaserConnector", "DaserConnectorMeta", "KVDataPlane", "LoadPlan", "LoadSegment",
-           "ReqLoadSpec", "ReqStoreSpec", "StorePlan", "hash_tokens", "plan_load",
-           "plan_store"]
+           "ReqLoadSpec", "ReqStoreSpec", "StorePlan", "hash_tokens", "load_spec",
+           "place_chunks", "plan_load", "plan_store"]
 
 
 def hash_tokens(tokens: list[int]) -> str:
@@ -144,6 +143,63 @@ class ReqStoreSpec:
 class DaserConnectorMeta(KVConnectorMetadata):
     reqs_to_load: dict[str, ReqLoadSpec] = field(default_factory=dict)
     reqs_to_store: dict[str, ReqStoreSpec] = field(default_factory=dict)
+
+
+# ---------------------------------------------------------------------------
+# placing looked-up chunks in the prompt (scheduler side)
+
+
+def place_chunks(tokens: list[int], chunks: list[dict],
+                 block_tokens: int) -> list[tuple[int, dict]]:
+    """(first token position, chunk) of each chunk of a lookup reply that the
+    prompt can use, in prompt order.
+
+    The first chunk goes at position 0, as the reference loads its single
+    prefix hit (daser_connector.py:240-258, daser/retrieval/prefix.py:49-72).
+    Each further chunk goes where the previous one ends, if that is a block
+    boundary and its key is the hash of exactly the prompt tokens it would
+    cover: a reply that lists alternatives rather than consecutive pieces
+    stops after the first.
+    Positions here are prompt positions; a chunk's stored position is its
+    ``pos_offset``."""
+    placed: list[tuple[int, dict]] = []
+    pos = 0
+    for i, ch in enumerate(chunks):
+        n = int(ch.get("token_count", 0))
+        if n <= 0 or pos + n > len(tokens) and i > 0:
+            break
+        if i > 0 and (pos % block_tokens or
+                      hash_tokens(tokens[pos:pos + n]) != ch.get("chunk_key")):
+            break
+        placed.append((pos, ch))
+        pos += n
+    return placed
+
+
+def load_spec(placed: list[tuple[int, dict]], block_ids: list[int],
+              block_tokens: int) -> Optional[ReqLoadSpec]:
+    """The worker's load of placed chunks into the request's first blocks:
+    chunk i's records go to the blocks from ``position_i / block_size``, as
+    far as the blocks reach, each with ``new_pos`` = its position. A single
+    chunk keeps the reference's flat fields; several become segments."""
+    segs = []
+    for pos, ch in placed:
+        first = pos // block_tokens
+        n = min(int(ch["num_slots"]), len(block_ids) - first)
+        if n <= 0:
+            break
+        segs.append(LoadSegment(start_slot=int(ch["start_slot"]), num_slots=n, block_offset=first,
+                                pos_offset=int(ch.get("pos_offset", 0)), new_pos=pos))
+    if not segs:
+        return None
+    head = placed[0][1]
+    used = block_ids[:segs[-1].block_offset + segs[-1].num_slots]
+    return ReqLoadSpec(
+        chunk_key=head["chunk_key"], start_slot=segs[0].start_slot, num_slots=segs[0].num_slots,
+        block_ids=used, file_offset=int(head["file_offset"]),
+        token_count=placed[len(segs) - 1][0] + int(placed[len(segs) - 1][1]["token_count"]),
+        pos_offset=segs[0].pos_offset, new_pos=segs[0].new_pos,
+        segments=segs if len(segs) > 1 else [])
 
 
 # ---------------------------------------------------------------------------
@@ -251,71 +307,75 @@ class DaserConnector(KVConnectorBase_V1):
 
     # ------------------------------------------------------------ scheduler
     def get_num_new_matched_tokens(self, request: Any, num_computed_tokens: int):
-        """Reference :194-258 (match_and_alloc in one RPC), unchanged."""
+        """Asks the server for cached chunks of the prompt (one
+        ``match_and_alloc`` RPC, as the reference does at :194-258: the
+        block-aligned part of the prompt to look up, and the key under which
+        a miss stores the whole aligned prompt) and places the chunks it
+        returns (:func:`place_chunks`). Returns the tokens the placed chunks
+        add beyond those vLLM already computed. A failed RPC is a miss."""
+        rid = request.request_id
         tokens = list(request.prompt_token_ids)
-        self._req_tokens[request.request_id] = tokens
-        available = len(tokens) - num_computed_tokens
-        if available < self._block_tokens:
+        self._req_tokens[rid] = tokens
+        bs = self._block_tokens
+        lookup_len = num_computed_tokens + (len(tokens) - num_computed_tokens) // bs * bs
+        if lookup_len - num_computed_tokens <= 0:
             return 0, False
-        aligned = (available // self._block_tokens) * self._block_tokens
-        prefix = tokens[: num_computed_tokens + aligned]
-        full_aligned = (len(tokens) // self._block_tokens) * self._block_tokens
-        store_key = hash_tokens(tokens[:full_aligned]) if full_aligned > 0 else ""
+        whole = len(tokens) // bs * bs
         try:
-            resp = self._ipc_sync.match_and_alloc(prefix, store_key, self._model_id)
+            reply = self._ipc_sync.match_and_alloc(
+                tokens[:lookup_len], hash_tokens(tokens[:whole]) if whole else "",
+                self._model_id)
         except Exception as exc:  # a failed lookup degrades to a miss
             logger.warning("[CONNECTOR] match_and_alloc failed: %s", exc)
             return 0, False
-        chunks = resp.get("chunks", [])
-        alloc = resp.get("alloc")
-        if alloc is not None:
-            self._pending_alloc[request.request_id] = alloc
-        if not chunks:
+        if reply.get("alloc") is not None:
+            self._pending_alloc[rid] = reply["alloc"]
+        placed = place_chunks(tokens[:lookup_len], reply.get("chunks") or [], bs)
+        if not placed:
             return 0, False
-        best = chunks[0]
-        extra_tokens = best["token_count"] - num_computed_tokens
-        if extra_tokens <= 0:
+        new_tokens = placed[-1][0] + int(placed[-1][1]["token_count"]) - num_computed_tokens
+        if new_tokens <= 0:
             return 0, False
-        self._pending_loads[request.request_id] = best
-        return extra_tokens, False
+        self._pending_loads[rid] = {"placed": placed}
+        return new_tokens, False
 
     def update_state_after_alloc(self, request: Any, blocks: Any, num_external_tokens: int) -> None:
-        """Reference :260-298."""
-        req_id = request.request_id
+        """Records the blocks vLLM gave the request: the first
+        ceil(num_external_tokens / block_size) receive a load (reference
+        :260-298), or those of the aligned prompt receive its store."""
+        rid = request.request_id
         block_ids = [blk.block_id for blk in blocks.blocks[0]]
-        if num_external_tokens > 0 and req_id in self._pending_loads:
-            chunk = self._pending_loads[req_id]
-            chunk["block_ids"] = block_ids[: math.ceil(num_external_tokens / self._block_tokens)]
-        else:
-            alloc = self._pending_alloc.pop(req_id, None)
-            if alloc is None:
-                return
-            alloc["block_ids"] = block_ids[: math.ceil(alloc["token_count"] / self._block_tokens)]
-            self._pending_stores[req_id] = alloc
+        bs = self._block_tokens
+        pending = self._pending_loads.get(rid)
+        if num_external_tokens > 0 and pending is not None:
+            pending["block_ids"] = block_ids[:-(-num_external_tokens // bs)]
+            return
+        alloc = self._pending_alloc.pop(rid, None)
+        if alloc is not None:
+            alloc["block_ids"] = block_ids[:-(-int(alloc["token_count"]) // bs)]
+            self._pending_stores[rid] = alloc
 
     def build_connector_meta(self, scheduler_output: Any) -> DaserConnectorMeta:
-        """Reference :300-357; also forwards the chunk's stored position
-        (``pos_offset`` of the lookup reply) and, when the reply names one, the
-        position to place it at (``new_pos``) and its segments."""
+        """Turns the scheduled requests' pending loads and stores into the
+        worker's metadata (reference :300-357). Every load names the position
+        its records go to: segment i lands at the token where chunk i was
+        placed, so a chunk stored at ``pos_offset`` is re-rotated when that
+        differs, including the reference's single prefix chunk (placed at 0)."""
         meta = DaserConnectorMeta()
-        scheduled = set(scheduler_output.num_scheduled_tokens.keys())
-        for req_id, chunk in list(self._pending_loads.items()):
-            if req_id in scheduled and "block_ids" in chunk:
-                segs = [LoadSegment(**s) for s in chunk.get("segments", [])]
-                meta.reqs_to_load[req_id] = ReqLoadSpec(
-                    chunk_key=chunk["chunk_key"], start_slot=chunk["start_slot"],
-                    num_slots=chunk["num_slots"], block_ids=chunk["block_ids"],
-                    file_offset=chunk["file_offset"], token_count=chunk["token_count"],
-                    pos_offset=int(chunk.get("pos_offset", 0)), new_pos=chunk.get("new_pos"),
-                    segments=segs)
-                del self._pending_loads[req_id]
-        for req_id, alloc in list(self._pending_stores.items()):
-            if req_id in scheduled and "block_ids" in alloc:
-                meta.reqs_to_store[req_id] = ReqStoreSpec(
-                    chunk_key=alloc["chunk_key"], start_slot=alloc["start_slot"],
-                    num_slots=alloc["num_slots"], block_ids=alloc["block_ids"],
-                    file_offset=alloc["file_offset"], token_count=alloc["token_count"])
-                del self._pending_stores[req_id]
+        scheduled = scheduler_output.num_scheduled_tokens
+        for rid in [r for r, p in self._pending_loads.items()
+                    if r in scheduled and "block_ids" in p]:
+            pending = self._pending_loads.pop(rid)
+            spec = load_spec(pending["placed"], pending["block_ids"], self._block_tokens)
+            if spec is not None:
+                meta.reqs_to_load[rid] = spec
+        for rid in [r for r, a in self._pending_stores.items()
+                    if r in scheduled and "block_ids" in a]:
+            a = self._pending_stores.pop(rid)
+            meta.reqs_to_store[rid] = ReqStoreSpec(
+                chunk_key=a["chunk_key"], start_slot=a["start_slot"], num_slots=a["num_slots"],
+                block_ids=a["block_ids"], file_offset=a["file_offset"],
+                token_count=a["token_count"])
         return meta
 
     def request_finished(self, request: Any, block_ids: list[int]):

@@ -7,11 +7,12 @@ from scratch, longest first (daser/retrieval/prefix.py:49-72): O(n^2 / bs)
 bytes hashed per lookup, a cold-path cost its own notes list as open. The
 xxh3 streaming state gives the digest of each prefix as the tokens are fed
 once, so all n / bs keys cost one pass, and they are the same keys.
+daser_amd.retrieval builds its lookups on them.
 """
 
 from __future__ import annotations
 
-from typing import Iterable, Mapping, Optional
+from typing import Iterable
 
 import numpy as np
 
@@ -23,7 +24,8 @@ def prefix_keys(tokens: Iterable[int], block_tokens: int) -> list[str]:
 
     if block_tokens <= 0:
         raise ValueError("block_tokens must be positive")
-    buf = np.ascontiguousarray(np.asarray(list(tokens), dtype=np.int32)).tobytes()
+    arr = tokens if isinstance(tokens, np.ndarray) else np.asarray(list(tokens))
+    buf = np.ascontiguousarray(arr, dtype=np.int32).tobytes()
     step = 4 * block_tokens
     h = xxhash.xxh3_128()
     keys = []
@@ -31,16 +33,3 @@ def prefix_keys(tokens: Iterable[int], block_tokens: int) -> list[str]:
         h.update(buf[off:off + step])
         keys.append(h.hexdigest())
     return keys
-
-
-def longest_prefix(index: Mapping[str, object], tokens: Iterable[int], block_tokens: int,
-                   accept=None) -> tuple[int, Optional[object]]:
-    """(matched tokens, entry) of the longest block-aligned prefix present in
-    ``index`` (and accepted by ``accept(entry)``, e.g. a model_id check),
-    else (0, None); the result of the reference's longest-first scan."""
-    keys = prefix_keys(tokens, block_tokens)
-    for i in range(len(keys) - 1, -1, -1):
-        entry = index.get(keys[i])
-        if entry is not None and (accept is None or accept(entry)):
-            return (i + 1) * block_tokens, entry
-    return 0, None

@@ -396,15 +396,17 @@ class _FakeServer:
     (scheduler, sync) and commit_chunk (worker, async) over shared state, with
     the reply shapes the reference's IPC server uses."""
 
-    def __init__(self, slot_bytes, block_tokens=16, new_pos=None):
-        self.slot, self.bs, self.new_pos = slot_bytes, block_tokens, new_pos
+    def __init__(self, slot_bytes, block_tokens=16, stored_pos=None):
+        # stored_pos: report committed chunks as stored at this position
+        # (a position encoder that records where a chunk was prefilled)
+        self.slot, self.bs, self.stored_pos = slot_bytes, block_tokens, stored_pos
         self.next_slot, self.pending, self.committed = 1, {}, {}
 
     def match_and_alloc(self, prefix, store_key, model_id):
         if store_key in self.committed:
             meta = dict(self.committed[store_key])
-            if self.new_pos is not None:
-                meta["new_pos"] = self.new_pos
+            if self.stored_pos is not None:
+                meta["pos_offset"] = self.stored_pos
             return {"chunks": [meta], "alloc": None}
         n = len(prefix) // self.bs
         meta = {"chunk_key": store_key, "start_slot": self.next_slot, "num_slots": n,
@@ -423,8 +425,8 @@ def test_cold_then_warm_request_end_to_end(gpu, tmp_path):
     """The reference's integration check (tests/integration/test_vllm_e2e.py:
     177-181, cold == warm) at the connector level: a cold request is missed,
     allocated and saved by the worker; the same prompt later hits and its
-    KV is loaded into other blocks bit-exactly; placed at a new position it
-    is re-rotated."""
+    KV is loaded into other blocks bit-exactly; reported as stored at
+    another position than the one it is placed at (0), it is re-rotated."""
     print("case: connector cold/warm end to end", flush=True)
     server = _FakeServer(SHAPE.slot_bytes)
     extra = dict(store_path=str(tmp_path / "daser.store"), io_slot_mb=0.03125, io_slots=3,
@@ -467,8 +469,9 @@ def test_cold_then_warm_request_end_to_end(gpu, tmp_path):
         assert torch.equal(fresh[l][:, [1, 12, 4]], caches[l][:, [5, 9, 2]]), f"layer {l}"
         assert not fresh[l][:, 7].view(torch.int16).any()  # the uncached tail block
 
-    # the same chunk placed at position 700: K re-rotated by +700, V as stored
-    server.new_pos = 700
+    # the same chunk reported as stored at position 700 and hit at 0: K
+    # re-rotated by -700, V as stored
+    server.stored_pos = 700
     moved = SimpleNamespace(request_id="moved", prompt_token_ids=list(prompt.prompt_token_ids))
     assert sched.get_num_new_matched_tokens(moved, 0) == (48, False)
     rot = [torch.zeros_like(c) for c in caches]
@@ -480,7 +483,7 @@ def test_cold_then_warm_request_end_to_end(gpu, tmp_path):
     ref = [np.zeros_like(to_bits_np(c, "bf16")) for c in caches]
     oracle.scatter_rerotate(ref, [3, 6, 8], np.arange(3) * SHAPE.slot_bytes, recs,
                             SHAPE.layer_bytes, dtype=oracle.BF16, rot_dim=64, style=oracle.NEOX,
-                            stored_pos=np.zeros(3, np.int64), new_pos=np.full(3, 700),
+                            stored_pos=np.full(3, 700), new_pos=np.zeros(3, np.int64),
                             rotate=np.ones(3), theta=500000.0)
     for l in range(SHAPE.num_layers):
         got = to_bits_np(rot[l], "bf16")

@@ -121,8 +121,11 @@ def _blocks(ids):
 
 
 def test_scheduler_hit_carries_positions():
+    """The reference's prefix hit (one chunk, matching the prompt from token
+    0) is placed at position 0, so a chunk stored at another position
+    (pos_offset 3000) is re-rotated back to 0 on load."""
     chunk = {"chunk_key": "ck", "start_slot": 5, "num_slots": 3, "file_offset": 5 * SLOT,
-             "token_count": 40, "pos_offset": 0, "new_pos": 1000}
+             "token_count": 40, "pos_offset": 3000}
     ipc = FakeIPC(chunks=[chunk])
     conn = C.DaserConnector(_cfg(block_tokens=16), C.KVConnectorRole.SCHEDULER, ipc_client=ipc)
     n, is_async = conn.get_num_new_matched_tokens(_req("r", 50), 0)
@@ -132,8 +135,11 @@ def test_scheduler_hit_carries_positions():
     meta = conn.build_connector_meta(SimpleNamespace(num_scheduled_tokens={"r": 50}))
     spec = meta.reqs_to_load["r"]
     assert spec.block_ids == [8, 1, 4]  # ceil(40 / 16)
-    assert (spec.pos_offset, spec.new_pos) == (0, 1000)
+    assert (spec.pos_offset, spec.new_pos) == (3000, 0)
+    assert spec.segments == [] and spec.num_slots == 3 and spec.start_slot == 5
     assert meta.reqs_to_store == {}
+    plan = C.plan_load(meta.reqs_to_load, SLOT)
+    assert plan.deltas == [-3000] and plan.rope_idx.tolist() == [0, 0, 0]
 
 
 def test_scheduler_miss_allocates_store():

@@ -1,8 +1,15 @@
-"""Full-size checks at the benchmark configurations, through properties that
-do not need the CPU oracle: round trips (scatter . gather = identity on the
-touched pages, untouched pages unchanged), token form = page form, zero
-delta = bit-exact copy, R(-d) R(d) = identity within rounding, pair norms
-preserved, V untouched. Comparisons run on the GPU, one layer at a time."""
+"""Full-size checks at the benchmark configurations (2-6, the sizes bench.py
+times), two ways:
+
+* oracle samples: after each full-size launch, 64 seeded pages (every
+  layer) are copied to the host and compared with the CPU oracle run on the
+  same pages' inputs: bit-exact for gather/scatter bytes and V, within the
+  re-rotation tolerance for K (oracle.rotation_within_tolerance);
+* properties over every page: round trips (scatter . gather = identity on
+  the touched pages, untouched pages unchanged), token form = page form,
+  zero delta = bit-exact copy, R(-d) R(d) = identity within rounding, pair
+  norms preserved, V untouched. Comparisons run on the GPU, one layer at a
+  time."""
 
 from __future__ import annotations
 
@@ -12,8 +19,91 @@ import torch
 
 import bench
 from daser_amd import ops, position, workloads
+from oracle import oracle
 
 pytestmark = pytest.mark.gpu
+
+N_SAMPLE = 64
+THETA = 500000.0
+
+
+def _sample(n_pages: int, seed: int) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    return np.sort(rng.choice(n_pages, size=min(N_SAMPLE, n_pages), replace=False))
+
+
+def _host_bits(t: torch.Tensor) -> np.ndarray:
+    """Raw element bits of a device tensor on the host (uint16 or uint8)."""
+    if t.element_size() == 2:
+        return t.cpu().view(torch.int16).numpy().view(np.uint16)
+    return t.cpu().view(torch.uint8).numpy()
+
+
+def _records(staging: torch.Tensor, offsets, slot_bytes: int) -> np.ndarray:
+    """The slot records at ``offsets``, back to back, on the host."""
+    return torch.cat([staging[int(o):int(o) + slot_bytes] for o in offsets]).cpu().numpy()
+
+
+def _cache_pages(caches, blocks) -> list[np.ndarray]:
+    """Per layer, the (2, n, bs, H, D) pages of ``blocks`` on the host."""
+    ids = torch.from_numpy(np.asarray(blocks, np.int64)).to(caches[0].device)
+    return [np.ascontiguousarray(_host_bits(c[:, ids])) for c in caches]
+
+
+def check_gather_sample(wl, caches, staging, seed):
+    """The kernel's records of sampled pages = oracle.gather of those pages."""
+    sh = wl.shape
+    sel = _sample(wl.n_pages, seed)
+    pages = _cache_pages(caches, wl.page_ids[sel])
+    want = np.zeros(sel.size * sh.slot_bytes, np.uint8)
+    oracle.gather(pages, np.arange(sel.size), np.arange(sel.size) * sh.slot_bytes, want,
+                  sh.layer_bytes)
+    got = _records(staging, wl.slot_offsets[sel], sh.slot_bytes)
+    assert np.array_equal(got, want), "gather records differ from the oracle"
+
+
+def check_scatter_sample(wl, caches, staging, src_offsets, seed):
+    """The kernel's cache pages of sampled pages = oracle.scatter of their records."""
+    sh = wl.shape
+    sel = _sample(wl.n_pages, seed)
+    recs = _records(staging, src_offsets[sel], sh.slot_bytes)
+    dt = np.uint16 if sh.elem_bytes == 2 else np.uint8
+    want = [np.zeros((2, sel.size, sh.block_size, sh.num_heads, sh.head_dim), dt)
+            for _ in range(sh.num_layers)]
+    oracle.scatter(want, np.arange(sel.size), np.arange(sel.size) * sh.slot_bytes, recs,
+                   sh.layer_bytes)
+    got = _cache_pages(caches, wl.page_ids[sel])
+    for l in range(sh.num_layers):
+        assert np.array_equal(got[l], want[l]), f"layer {l}: scatter differs from the oracle"
+
+
+def check_rerotate_sample(wl, caches, staging, src_offsets, page_delta, dtype, seed,
+                          k_scale=None):
+    """Sampled pages of a full-size re-rotating scatter against
+    oracle.scatter_rerotate on the same records: V bit-exact, K within 1 ulp
+    of the float64 rotation (cancellation-aware)."""
+    sh = wl.shape
+    sel = _sample(wl.n_pages, seed)
+    recs = _records(staging, src_offsets[sel], sh.slot_bytes)
+    dt = np.uint16 if sh.elem_bytes == 2 else np.uint8
+    want = [np.zeros((2, sel.size, sh.block_size, sh.num_heads, sh.head_dim), dt)
+            for _ in range(sh.num_layers)]
+    ks = None if k_scale is None else k_scale.detach().cpu().numpy().astype(np.float32)
+    oracle.scatter_rerotate(want, np.arange(sel.size), np.arange(sel.size) * sh.slot_bytes,
+                            recs, sh.layer_bytes, dtype=dtype, rot_dim=sh.head_dim,
+                            style=oracle.NEOX, stored_pos=np.zeros(sel.size, np.int64),
+                            new_pos=np.asarray(page_delta, np.int64)[sel],
+                            rotate=np.ones(sel.size, np.int8), theta=THETA, k_scale=ks)
+    got = _cache_pages(caches, wl.page_ids[sel])
+    stored = recs.view(dt).reshape(sel.size, sh.num_layers, 2, sh.block_size, sh.num_heads,
+                                   sh.head_dim)
+    moved = 0
+    for l in range(sh.num_layers):
+        assert np.array_equal(got[l][1], want[l][1]), f"layer {l}: V differs from the oracle"
+        ok, msg = oracle.rotation_within_tolerance(got[l][0], want[l][0], dtype)
+        assert ok, f"layer {l}: K outside tolerance: {msg}"
+        moved += int((got[l][0] != stored[:, l, 0]).sum())
+    assert moved > 0, "no K element was rotated"
 
 
 def _block_tables(wl):
@@ -32,9 +122,11 @@ def test_round_trip_full_size(gpu, cfg, dtype):
     st = torch.empty(wl.staging_bytes, dtype=torch.uint8, device=gpu)
     ids = torch.from_numpy(wl.page_ids.astype(np.int64)).to(gpu)
     ops.gather(ops.LayerTable(caches), wl.page_ids, wl.slot_offsets, st)
+    check_gather_sample(wl, caches, st, seed=cfg)
     dst_full = torch.zeros_like(full)
     dst = [dst_full[l] for l in range(wl.shape.num_layers)]
     ops.scatter(ops.LayerTable(dst), wl.page_ids, wl.slot_offsets, st)
+    check_scatter_sample(wl, dst, st, wl.slot_offsets, seed=cfg + 100)
     untouched = torch.ones(wl.num_blocks, dtype=torch.bool, device=gpu)
     untouched[ids] = False
     for l in range(wl.shape.num_layers):
@@ -67,6 +159,64 @@ def test_round_trip_full_size(gpu, cfg, dtype):
         assert torch.equal(a[mask], b[mask])
         assert not b[~mask].any()
     torch.cuda.synchronize()
+    del full, caches, dst_full, dst, st
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("cfg", [3, 5, 6])
+def test_rerotate_full_size_oracle_sample(gpu, cfg):
+    """The benchmark's re-rotating scatter at full size (config 5: 80 layers,
+    171.8 GB of destination caches, 64 shared source chunks read by many
+    pages with the shared-records launch), sampled against the oracle."""
+    print(f"case: full-size rerotate oracle sample cfg{cfg}", flush=True)
+    wl = workloads.config(cfg)
+    sh = wl.shape
+    src_bytes = wl.meta["src_staging_bytes"]
+    src = torch.empty(src_bytes, dtype=torch.uint8, device=gpu)
+    g = torch.Generator(device=gpu).manual_seed(70 + cfg)
+    for i in range(0, src_bytes, 1 << 30):
+        src[i:i + min(1 << 30, src_bytes - i)].view(torch.bfloat16).normal_(generator=g)
+    full = torch.empty((sh.num_layers, 2, wl.num_blocks, sh.block_size, sh.num_heads,
+                        sh.head_dim), dtype=torch.bfloat16, device=gpu)
+    caches = [full[l] for l in range(sh.num_layers)]
+    ridx, uniq = position.page_rope_index(wl.chunk_pages, wl.chunk_delta)
+    tabs = position.delta_tables(uniq, sh.head_dim, THETA, device=gpu)
+    shared = bool(2 * np.unique(wl.src_offsets).size <= wl.src_offsets.size)
+    assert shared == (cfg != 3)
+    ops.scatter_rerotate(ops.LayerTable(caches), wl.page_ids, wl.src_offsets, src, tabs, ridx)
+    torch.cuda.synchronize()
+    check_rerotate_sample(wl, caches, src, wl.src_offsets, wl.page_delta, oracle.BF16,
+                          seed=200 + cfg)
+    del full, caches, src
+    torch.cuda.empty_cache()
+
+
+def test_fp8_rerotate_full_size_oracle_sample(gpu):
+    """Config 4's e4m3 re-rotation at full size (128 requests, 1.09 M tokens,
+    per-layer fp32 K scales, every request moved by its own delta), sampled
+    against the oracle's dequantise -> rotate -> requantise."""
+    print("case: full-size fp8 rerotate oracle sample cfg4", flush=True)
+    wl = workloads.config(4)
+    sh = wl.shape
+    full, caches, k_scale = bench.fill_caches(torch, sh, wl.num_blocks, "fp8", gpu, seed=64)
+    st = torch.empty(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(caches), wl.page_ids, wl.slot_offsets, st)
+    del full, caches
+    rng = np.random.default_rng(7)
+    deltas = rng.integers(1, 32768, size=len(wl.req_pages)).tolist()
+    ridx, uniq = position.page_rope_index(wl.req_pages, deltas)
+    tabs = position.delta_tables(uniq, sh.head_dim, THETA, device=gpu)
+    dst_full = torch.empty((sh.num_layers, 2, wl.num_blocks, sh.block_size, sh.num_heads,
+                            sh.head_dim), dtype=torch.float8_e4m3fn, device=gpu)
+    dst = [dst_full[l] for l in range(sh.num_layers)]
+    ops.scatter_rerotate(ops.LayerTable(dst), wl.page_ids, wl.slot_offsets, st, tabs, ridx,
+                         k_scale=k_scale)
+    torch.cuda.synchronize()
+    page_delta = np.repeat(np.asarray(deltas, np.int64), wl.req_pages)
+    check_rerotate_sample(wl, dst, st, wl.slot_offsets, page_delta, oracle.E4M3, seed=204,
+                          k_scale=k_scale)
+    del dst_full, dst, st
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("cfg", [3, 6])  # 6: one KV head, 4 KiB pages (grouped kernels)

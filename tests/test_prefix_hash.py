@@ -3,7 +3,7 @@
 import numpy as np
 
 from daser_amd.connector import hash_tokens
-from daser_amd.prefix_hash import longest_prefix, prefix_keys
+from daser_amd.prefix_hash import prefix_keys
 
 
 def test_keys_equal_per_prefix_hashes():
@@ -21,13 +21,6 @@ def test_short_and_negative_tokens():
     assert prefix_keys(toks, 4)[-1] == hash_tokens(toks)
 
 
-def test_longest_prefix_matches_reference_scan():
-    rng = np.random.default_rng(1)
-    toks = rng.integers(0, 1000, size=200).tolist()
-    index = {hash_tokens(toks[:48]): ("m", 48), hash_tokens(toks[:112]): ("other", 112),
-             hash_tokens(toks[:16]): ("m", 16)}
-    n, e = longest_prefix(index, toks, 16, accept=lambda m: m[0] == "m")
-    assert (n, e) == (48, ("m", 48))
-    n, e = longest_prefix(index, toks, 16)
-    assert n == 112
-    assert longest_prefix({}, toks, 16) == (0, None)
+def test_numpy_input_equals_list_input():
+    toks = np.arange(-50, 270, dtype=np.int64)
+    assert prefix_keys(toks, 16) == prefix_keys(toks.tolist(), 16)
