@@ -173,20 +173,45 @@ constexpr int rot_grouped_wg_per_cu() {
 // 24.22 ms at config 4).
 constexpr int kRotSingleWgPerCu = 3;
 constexpr int kRotSingleSharedWgPerCu = 4;
-// Dynamic LDS that limits the re-rotation kernel to kRotWgPerCu workgroups
-// per CU on the current device (0 if the capacity cannot be read).
+// Dynamic LDS that limits a kernel with `static_lds` bytes of static LDS to
+// wg_per_cu workgroups per CU on the current device (0 if the capacity cannot
+// be read). The capacity is read once per device.
 constexpr int64_t kLdsGranule = 512;
-size_t rot_occupancy_lds(int wg_per_cu) {
-  int dev = 0, lds = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
-                            dev) != hipSuccess || lds <= 0)
-    return 0;
-  // a workgroup's LDS (the static table plus this) is allocated in 512-byte
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_lds_per_cu[kMaxDevices];
+size_t occupancy_lds(int wg_per_cu, int64_t static_lds) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || wg_per_cu <= 0) return 0;
+  int lds = dev < kMaxDevices ? g_lds_per_cu[dev].load(std::memory_order_relaxed) : 0;
+  if (lds <= 0) {
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                              dev) != hipSuccess || lds <= 0)
+      return 0;
+    if (dev < kMaxDevices) g_lds_per_cu[dev].store(lds, std::memory_order_relaxed);
+  }
+  // a workgroup's LDS (static plus dynamic) is allocated in 512-byte
   // granules: round its share down so that wg_per_cu of them fit
   const int64_t share = (int64_t)lds / wg_per_cu / kLdsGranule * kLdsGranule;
-  const int64_t want = share - (int64_t)sizeof(float2) * kMaxRotHalf;
+  const int64_t want = share - static_lds;
   return want > 0 ? (size_t)want : 0;
+}
+size_t rot_occupancy_lds(int wg_per_cu) {
+  return occupancy_lds(wg_per_cu, (int64_t)sizeof(float2) * kMaxRotHalf);
+}
+
+// Workgroups per CU for the one-unit page copies (0: no limit; the copy
+// kernels' registers allow 3). Units in flight per CU are limited to about
+// 64 KiB of pages (K + V): one workgroup per CU at 32 KiB pages, two at 16
+// KiB. Measured in-process (ms, 3 per CU -> this policy): Llama-3-8B bf16
+// (32 KiB pages) scatter 12.08 -> 11.97 (stream kernel), gather 11.75 ->
+// 11.60, on three boxes alike; e4m3 (16 KiB pages) scatter 24.71 -> 24.07,
+// gather 22.07 -> 22.09. More than 64 KiB in flight per CU makes the DRAM
+// side slower, not faster (fewer, longer-waiting requests win); one
+// workgroup per CU at 16 KiB pages leaves the CU idle between units (28.4 ms).
+int copy_wg_per_cu(int64_t page_bytes) {
+  if (const int64_t t = tune(DSR_TUNE_COPY_WG_PER_CU)) return (int)t;
+  const int64_t w = (64 << 10) / (2 * page_bytes);
+  return w >= 3 ? 0 : (int)(w < 1 ? 1 : w);
 }
 
 template <int DT>
@@ -340,10 +365,13 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   // and 32 KiB).
   const int G = page_bytes < kThreads * 16 ? units_per_group(page_bytes, kGatherUnroll, kMaxGroup) : 1;
   return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
-    if (G > 1)
-      kv_copy_grouped_kernel<true, kGatherUnroll><<<grid, kThreads, 0, (hipStream_t)stream>>>(b, G);
-    else
-      kv_gather_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(b);
+    const hipStream_t st = (hipStream_t)stream;
+    if (G > 1) {
+      kv_copy_grouped_kernel<true, kGatherUnroll><<<grid, kThreads, 0, st>>>(b, G);
+    } else {
+      const size_t dyn = occupancy_lds(copy_wg_per_cu(page_bytes), 0);
+      kv_gather_kernel<<<grid, kThreads, dyn, st>>>(b);
+    }
   });
 }
 
@@ -363,10 +391,19 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   // one-unit kernel measured equal or faster.
   const int G = page_bytes <= kThreads * 16 ? units_per_group(page_bytes, kScatterUnroll, kMaxGroup) : 1;
   return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
-    if (G > 1)
-      kv_copy_grouped_kernel<false, kScatterUnroll><<<grid, kThreads, 0, (hipStream_t)stream>>>(b, G);
+    const hipStream_t st = (hipStream_t)stream;
+    if (G > 1) {
+      kv_copy_grouped_kernel<false, kScatterUnroll><<<grid, kThreads, 0, st>>>(b, G);
+      return;
+    }
+    const int wpc = copy_wg_per_cu(page_bytes);
+    const size_t dyn = occupancy_lds(wpc, 0);
+    const int64_t pick = tune(DSR_TUNE_SCATTER_KERNEL);
+    const bool stream_k = pick ? pick == 2 : wpc == 1 && page_bytes % (kThreads * 8 * 16) == 0;
+    if (stream_k)
+      kv_scatter_stream_kernel<<<grid, kThreads, dyn, st>>>(b);
     else
-      kv_scatter_kernel<<<grid, kThreads, 0, (hipStream_t)stream>>>(b);
+      kv_scatter_kernel<<<grid, kThreads, dyn, st>>>(b);
   });
 }
 

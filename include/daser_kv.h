@@ -68,6 +68,10 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
  *   DSR_TUNE_SLOTS_KERNEL         1: rows of <= 8 vectors take the small-row
  *                                 kernel instead of the packed one
  *   DSR_TUNE_SLOTS_UNROLL         4|8 instructions per wave of the packed kernel
+ *   DSR_TUNE_COPY_WG_PER_CU       workgroups per CU of the one-unit page
+ *                                 gather / scatter
+ *   DSR_TUNE_SCATTER_KERNEL       one-unit page scatter: 1 the load-all-then-
+ *                                 store kernel, 2 the streaming kernel
  */
 #define DSR_TUNE_UNITS_PER_GROUP 0
 #define DSR_TUNE_MAX_WG_PER_LAUNCH 1
@@ -77,7 +81,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 #define DSR_TUNE_SLOTS_TPW 5
 #define DSR_TUNE_SLOTS_KERNEL 6
 #define DSR_TUNE_SLOTS_UNROLL 7
-#define DSR_TUNE_COUNT_ 8
+#define DSR_TUNE_COPY_WG_PER_CU 8
+#define DSR_TUNE_SCATTER_KERNEL 9
+#define DSR_TUNE_COUNT_ 10
 
 #define DSR_OK 0
 #define DSR_ERR_ARG (-1)   /* null pointer, negative count, bad enum     */

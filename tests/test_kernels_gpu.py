@@ -59,6 +59,35 @@ def test_scatter_cfg1_bit_exact_and_round_trip(gpu):
         assert not dst[l][:, (~touched).to(gpu)].view(torch.int16).any()
 
 
+@pytest.mark.parametrize("heads,head_dim,dt", [(8, 128, "bf16"), (16, 128, "bf16"),
+                                                (8, 128, "e4m3"), (4, 96, "bf16")])
+@pytest.mark.parametrize("kernel,wg_per_cu", [(0, 0), (1, 0), (2, 0), (1, 1), (2, 1), (2, 2),
+                                              (1, 3)])
+def test_page_copy_kernels_and_occupancy_match_oracle(gpu, tuning, heads, head_dim, dt,
+                                                      kernel, wg_per_cu):
+    """Both one-unit scatter kernels (load-all-then-store, streaming) at
+    every occupancy the launch policy or an override may pick, and the
+    gather at the same occupancies: the oracle's bytes, with ragged requests
+    and partial last pages (pages of 32, 64, 16 and 12 KiB)."""
+    print(f"case: page copy H{heads} D{head_dim} {dt} kernel={kernel} wpc={wg_per_cu}",
+          flush=True)
+    tuning("scatter_kernel", kernel)
+    tuning("copy_wg_per_cu", wg_per_cu)
+    shape = KVShape(3, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    wl = workloads.ragged(shape, 6, 1, 400, seed=heads + head_dim, pool_slack=1.3)
+    caches = rand_caches(shape, wl.num_blocks, dt, gpu, seed=9, scale=3.0)
+    staging, ref = _gather_both(wl, caches, dt, gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(staging.cpu().numpy(), ref)
+    dst = rand_caches(shape, wl.num_blocks, dt, gpu, seed=10)
+    dst_ref = _np_layers(dst, dt)
+    ops.scatter(ops.LayerTable(dst), wl.page_ids, wl.slot_offsets, staging)
+    oracle.scatter(dst_ref, wl.page_ids, wl.slot_offsets, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    for l in range(shape.num_layers):
+        assert np.array_equal(to_bits_np(dst[l], dt), dst_ref[l]), f"layer {l}"
+
+
 @pytest.mark.parametrize("dt", ["e4m3", "fp16"])
 def test_gather_scatter_other_dtypes_bit_exact(gpu, dt):
     print(f"case: gather/scatter {dt}", flush=True)
