@@ -25,7 +25,7 @@ cost of the connector's worker hooks on serving-shaped steps; neither is
 `value`.
 
 Usage: python bench.py [--steps K] [--warmup W] [--configs 2,3,4,5,6] [--no-cpu]
-                       [--no-ref-loop] [--io] [--serving] [--calibrate]
+                       [--no-ref-loop] [--io] [--serving] [--patterns] [--calibrate]
 """
 
 from __future__ import annotations
@@ -250,7 +250,7 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
     tc = Timer(torch)
     for _ in range(steps):
         with tc:
-            ops.scatter(table, ids, offs, src)
+            ops.scatter(table, ids, offs, src, shared_records=shared)
     torch.cuda.synchronize()
     copy_ms = tc.mean_ms()
     P = wl.n_pages * shape.slot_bytes
@@ -527,6 +527,69 @@ def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int 
     return out
 
 
+def bench_patterns(torch, ops, dev, reps: int = 5) -> dict:
+    """The same bytes as config 2 (P = 17,742 pages x 2 MiB records) moved in
+    other patterns, for scale: torch's own kernels for a plain sequential
+    copy (copy_), a sequential-read -> permuted-32 KiB-row write
+    (index_copy_) and a permuted-read -> sequential write (index_select), and
+    this library's scatter / gather over the same caches with an identity
+    page list (both sides sequential; 8 pages fewer) and with config 2's
+    permutation. Mean
+    kernel time over `reps` launches (HIP events), GB/s = 2P / time."""
+    from daser_amd import workloads
+
+    wl = workloads.config(2)
+    sh = wl.shape
+    P = wl.payload_bytes
+    rows = P // sh.page_bytes  # 32 KiB rows
+    out = {"payload_bytes": P, "row_bytes": sh.page_bytes}
+
+    def timed(fn):
+        t = Timer(torch)
+        fn()
+        for _ in range(reps):
+            with t:
+                fn()
+        torch.cuda.synchronize()
+        return round(2 * P / (t.mean_ms() * 1e-3) / 1e9, 1)
+
+    g = torch.Generator().manual_seed(0)
+    src = torch.empty(P, dtype=torch.uint8, device=dev).fill_(3)
+    pool_rows = int(rows * 1.05)
+    dst = torch.empty(pool_rows * sh.page_bytes, dtype=torch.uint8, device=dev)
+    perm = torch.randperm(pool_rows, generator=g)[:rows].to(dev)
+    src2 = src.view(rows, sh.page_bytes)
+    dst2 = dst.view(pool_rows, sh.page_bytes)
+    out["torch_copy_sequential_GBps"] = timed(lambda: dst[:P].copy_(src))
+    out["torch_index_copy_permuted_write_GBps"] = timed(lambda: dst2.index_copy_(0, perm, src2))
+    out["torch_index_select_permuted_read_GBps"] = timed(
+        lambda: torch.index_select(dst2, 0, perm, out=src2))
+    del src, dst, src2, dst2
+    torch.cuda.empty_cache()
+    full, caches, _ = fill_caches(torch, sh, wl.num_blocks, "bf16", dev, seed=1)
+    table = ops.LayerTable(caches)
+    st = torch.empty(wl.staging_bytes, dtype=torch.uint8, device=dev)
+    offs = torch.from_numpy(wl.slot_offsets).to(dev)
+    # the identity list covers 8 pages fewer, so that a profile tells its
+    # launches (grid) from config 2's; its rate is scaled to its own bytes
+    n_id = wl.n_pages - 8
+    ident = torch.arange(n_id, dtype=torch.int32, device=dev)
+    ids = torch.from_numpy(wl.page_ids).to(dev)
+    s_ids_np, s_offs_np, _ = ops.dest_order(wl.page_ids, wl.slot_offsets)
+    s_ids = torch.from_numpy(s_ids_np.astype(np.int32)).to(dev)
+    s_offs = torch.from_numpy(s_offs_np).to(dev)
+    scale = n_id / wl.n_pages
+    out["gather_identity_GBps"] = round(
+        scale * timed(lambda: ops.gather(table, ident, offs[:n_id], st)), 1)
+    out["scatter_identity_GBps"] = round(
+        scale * timed(lambda: ops.scatter(table, ident, offs[:n_id], st)), 1)
+    out["gather_cfg2_GBps"] = timed(lambda: ops.gather(table, ids, offs, st))
+    out["scatter_cfg2_GBps"] = timed(lambda: ops.scatter(table, s_ids, s_offs, st))
+    del full, caches, table, st
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_model() -> str:
     """The host CPU's model name (/proc/cpuinfo)."""
     try:
@@ -693,6 +756,10 @@ def main() -> int:
     ap.add_argument("--serving", action="store_true",
                     help="also time the connector's worker hooks on serving-shaped "
                          "steps (host cost per hook, save and load latency)")
+    ap.add_argument("--patterns", action="store_true",
+                    help="also time config 2's bytes in other patterns: torch's copy_, "
+                         "index_copy_ and index_select, and this library's kernels over "
+                         "the identity page list")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 4 GiB device copy (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -805,6 +872,10 @@ def main() -> int:
         out.update({"value": round(r.get("tokens_per_s", 0.0)), "unit": "tokens/s",
                     "ms_per_step": round(r.get("kernel_ms", 0.0), 3), "dtype": "bf16",
                     "config": {"workload": workloads.CONFIG_NAMES[configs[0]]}})
+    if args.patterns:
+        log("[bench] patterns: config 2's bytes in other access patterns")
+        out["patterns"] = bench_patterns(torch, ops, dev)
+        log(f"[bench] patterns: {json.dumps(out['patterns'])}")
     if args.io:
         log("[bench] io: PCIe/file-inclusive save and load")
         out["pcie_inclusive"] = bench_io(torch, dev)

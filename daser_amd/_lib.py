@@ -20,7 +20,7 @@ LIB_PATH = os.environ.get("DASER_KV_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so"
 )
 
-DSR_ABI_VERSION = 6
+DSR_ABI_VERSION = 7
 DSR_OK = 0
 DSR_ERR_ARG = -1
 DSR_ERR_ALIGN = -2
@@ -39,7 +39,8 @@ DSR_DTYPE_FP8_E4M3 = 2
 DSR_ROPE_NEOX = 0
 DSR_ROPE_GPTJ = 1
 
-DSR_REROTATE_SHARED_RECORDS = 1
+DSR_SHARED_RECORDS = 1
+DSR_REROTATE_SHARED_RECORDS = DSR_SHARED_RECORDS
 
 # dsr_set_tuning knobs (measurements and tests only)
 TUNE = {"units_per_group": 0, "max_wg_per_launch": 1, "rot_kernel": 2, "rot_wg_per_cu": 3,
@@ -60,6 +61,7 @@ SIGNATURES = {
     "dsr_set_tuning": ([_I, _I64], _I),
     "dsr_gather": (_COPY_ARGS, _I),
     "dsr_scatter": (_COPY_ARGS, _I),
+    "dsr_scatter_ex": (_COPY_ARGS[:-1] + [ctypes.c_uint, _P], _I),
     "dsr_gather_slots": (_SLOT_ARGS, _I),
     "dsr_scatter_slots": (_SLOT_ARGS, _I),
     "dsr_ring_open": ([ctypes.c_char_p, _I64, _I, _I, ctypes.POINTER(_P)], _I),

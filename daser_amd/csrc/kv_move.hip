@@ -375,11 +375,11 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   });
 }
 
-int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
-                int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
-                const int32_t* page_ids, const int64_t* slot_offsets,
-                int n_pages, const void* staging, int64_t staging_bytes,
-                int64_t layer_bytes, int layer0, dsr_stream_t stream) {
+int dsr_scatter_ex(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                   int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                   const int32_t* page_ids, const int64_t* slot_offsets,
+                   int n_pages, const void* staging, int64_t staging_bytes,
+                   int64_t layer_bytes, int layer0, unsigned flags, dsr_stream_t stream) {
   int rc = check_common(layer_base, n_layers, kv_stride, page_stride, page_bytes,
                         num_blocks, page_ids, slot_offsets, n_pages, staging,
                         staging_bytes, layer_bytes, layer0);
@@ -396,7 +396,11 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
       kv_copy_grouped_kernel<false, kScatterUnroll><<<grid, kThreads, 0, st>>>(b, G);
       return;
     }
-    const int wpc = copy_wg_per_cu(page_bytes);
+    // records read by several pages are partly served by the caches, so
+    // more bytes in flight pay (the 70B share's 64 shared chunks: 50.5 ms at
+    // the registers' 3 workgroups per CU vs 52.6 ms at one)
+    const int wpc = (flags & DSR_SHARED_RECORDS) && !tune(DSR_TUNE_COPY_WG_PER_CU)
+                        ? 0 : copy_wg_per_cu(page_bytes);
     const size_t dyn = occupancy_lds(wpc, 0);
     const int64_t pick = tune(DSR_TUNE_SCATTER_KERNEL);
     const bool stream_k = pick ? pick == 2 : wpc == 1 && page_bytes % (kThreads * 8 * 16) == 0;
@@ -405,6 +409,16 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
     else
       kv_scatter_kernel<<<grid, kThreads, dyn, st>>>(b);
   });
+}
+
+int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                const int32_t* page_ids, const int64_t* slot_offsets,
+                int n_pages, const void* staging, int64_t staging_bytes,
+                int64_t layer_bytes, int layer0, dsr_stream_t stream) {
+  return dsr_scatter_ex(layer_base, n_layers, kv_stride, page_stride, page_bytes, num_blocks,
+                        page_ids, slot_offsets, n_pages, staging, staging_bytes, layer_bytes,
+                        layer0, 0u, stream);
 }
 
 }  // extern "C"

@@ -484,7 +484,8 @@ class KVDataPlane:
                 continue
             src = plan.src_offsets[sel] - base
             if tabs is None:
-                ops.scatter(self.table, plan.page_ids[sel], src, buf)
+                ops.scatter(self.table, plan.page_ids[sel], src, buf,
+                            shared_records=plan.shared_records)
             else:
                 ops.scatter_rerotate(self.table, plan.page_ids[sel], src, buf, tabs,
                                      plan.rope_idx[sel], rot_dim=self.rotary_dim,

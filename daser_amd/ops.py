@@ -344,13 +344,32 @@ def scatter(
     *,
     layer0: int = 0,
     layers: Optional[tuple[int, int]] = None,
+    shared_records: Optional[bool] = None,
 ) -> None:
-    """Unpacks slot records into pages (reference load loop, :536-551)."""
+    """Unpacks slot records into pages (reference load loop, :536-551).
+
+    ``shared_records``: several pages read the same records; shapes the
+    launch for cache-served reads. None: inferred from host ``slot_offsets``
+    (at most half of them distinct), False for device tables. Results do
+    not depend on it."""
+    if shared_records is None:
+        shared_records = _shared_offsets(slot_offsets)
     page_ids, slot_offsets, _ = dest_order(page_ids, slot_offsets)
     args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
+    stream = _stream_handle(table.layout.device)
+    if shared_records and table.layout.k_layout != "hnd":
+        rc = _lib.lib().dsr_scatter_ex(*args, _lib.DSR_SHARED_RECORDS, stream)
+        _lib.check("dsr_scatter_ex", rc)
+        return
     fn, name, extra = _copy_entry(table.layout, "dsr_scatter")
-    rc = fn(*args, *extra, _stream_handle(table.layout.device))
+    rc = fn(*args, *extra, stream)
     _lib.check(name, rc)
+
+
+def _shared_offsets(slot_offsets) -> bool:
+    """At most half of the host record offsets are distinct."""
+    offs_h = _host_array(slot_offsets, np.int64)
+    return offs_h is not None and offs_h.size > 1 and 2 * np.unique(offs_h).size <= offs_h.size
 
 
 def scatter_rerotate(
@@ -410,9 +429,7 @@ def scatter_rerotate(
             raise IndexError("layer_group needs one group in [-1, n_groups) per layer")
         lg_d = _as_device_table(layer_group, torch.int32, lay.device, "layer_group")
     if shared_records is None:
-        offs_h = _host_array(slot_offsets, np.int64)
-        shared_records = offs_h is not None and offs_h.size > 1 and \
-            2 * np.unique(offs_h).size <= offs_h.size
+        shared_records = _shared_offsets(slot_offsets)
     page_ids, slot_offsets, rope_idx = dest_order(page_ids, slot_offsets, rope_idx)
     args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
     ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")

@@ -47,9 +47,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 /* Bumped whenever an entry point's signature changes or one is added:
  * 2 layer_group on the re-rotation, 3 dsr_scatter_rerotate_kx, 4 the
  * re-rotations' flags, 5 the head-major (_hnd) entry points, 6
- * dsr_set_tuning. Callers check
+ * dsr_set_tuning, 7 dsr_scatter_ex. Callers check
  * dsr_abi_version() against it. */
-#define DSR_ABI_VERSION 6
+#define DSR_ABI_VERSION 7
 
 /*
  * Kernel choice and launch shape follow from the geometry. dsr_set_tuning()
@@ -102,8 +102,11 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 #define DSR_ROPE_NEOX 0 /* rotate-half: pairs (j, j + rot_dim/2)  (Llama) */
 #define DSR_ROPE_GPTJ 1 /* interleaved: pairs (2j, 2j + 1)                */
 
-/* dsr_scatter_rerotate* flags */
-#define DSR_REROTATE_SHARED_RECORDS 1u
+/* dsr_scatter_ex / dsr_scatter_rerotate* flags: several pages of the call
+ * read the same records (a cached chunk placed in several requests). A
+ * launch-shape hint; results do not depend on it. */
+#define DSR_SHARED_RECORDS 1u
+#define DSR_REROTATE_SHARED_RECORDS DSR_SHARED_RECORDS
 
 /* Returns DSR_ABI_VERSION. */
 int dsr_abi_version(void);
@@ -159,6 +162,15 @@ int dsr_scatter(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
                 const int32_t* page_ids, const int64_t* slot_offsets,
                 int n_pages, const void* staging, int64_t staging_bytes,
                 int64_t layer_bytes, int layer0, dsr_stream_t stream);
+
+/* dsr_scatter with launch hints (flags: DSR_SHARED_RECORDS); the same
+ * bytes. Same reference loop as dsr_scatter (daser_connector.py:536-551);
+ * the hint is for loads in which requests share cached chunks. */
+int dsr_scatter_ex(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                   int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                   const int32_t* page_ids, const int64_t* slot_offsets,
+                   int n_pages, const void* staging, int64_t staging_bytes,
+                   int64_t layer_bytes, int layer0, unsigned flags, dsr_stream_t stream);
 
 /*
  * Load scatter with fused RoPE position-delta re-rotation of K.

@@ -88,6 +88,32 @@ def test_page_copy_kernels_and_occupancy_match_oracle(gpu, tuning, heads, head_d
         assert np.array_equal(to_bits_np(dst[l], dt), dst_ref[l]), f"layer {l}"
 
 
+@pytest.mark.parametrize("shared", [True, False, None])
+@pytest.mark.parametrize("heads", [8, 1])
+def test_scatter_shared_records_hint_matches_oracle(gpu, heads, shared):
+    """Pages reading the same records (one cached chunk placed in several
+    requests) through dsr_scatter_ex with and without the shared-records
+    hint, and with the hint inferred from host offsets: the oracle's bytes."""
+    print(f"case: scatter shared={shared} H{heads}", flush=True)
+    shape = KVShape(3, heads, 128, 16, 2)
+    n_src, n = 6, 40
+    rng = np.random.default_rng(heads)
+    nb = 64
+    src = rand_caches(shape, nb, "bf16", gpu, seed=12)
+    st = torch.zeros(n_src * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(src), rng.permutation(nb)[:n_src].astype(np.int32),
+               np.arange(n_src) * shape.slot_bytes, st)
+    offs = rng.integers(0, n_src, n) * shape.slot_bytes
+    ids = rng.permutation(nb)[:n].astype(np.int32)
+    dst = rand_caches(shape, nb, "bf16", gpu, seed=13)
+    ref = _np_layers(dst, "bf16")
+    ops.scatter(ops.LayerTable(dst), ids, offs, st, shared_records=shared)
+    oracle.scatter(ref, ids, offs, st.cpu().numpy(), shape.layer_bytes)
+    torch.cuda.synchronize()
+    for l in range(shape.num_layers):
+        assert np.array_equal(to_bits_np(dst[l], "bf16"), ref[l]), f"layer {l}"
+
+
 @pytest.mark.parametrize("dt", ["e4m3", "fp16"])
 def test_gather_scatter_other_dtypes_bit_exact(gpu, dt):
     print(f"case: gather/scatter {dt}", flush=True)
