@@ -97,6 +97,20 @@ __device__ __forceinline__ int64_t layer_major_unit(int64_t n_units, int n_layer
   return v < 0 ? -1 : layer_major_of(v, n_units, n_layers);
 }
 
+// The same layer-major walk in hardware dispatch order: consecutive
+// workgroups (dealt round-robin to the 8 XCDs) take consecutive units, so at
+// any moment the whole chip works on one stretch of one layer's
+// destination-ordered pages. Used by the streaming scatter at one workgroup
+// per CU: 256 adjacent pages in flight write one K and one V window of
+// 8 MiB each, against 8 XCDs x 2 windows in the XCD-contiguous order.
+// Measured in-process: 11.87 vs 12.29 ms at config 2 and 6.70 vs 6.97 ms
+// at config 3's pages; the kernels at three workgroups per CU, the
+// re-rotations and the e4m3 (16 KiB) pages ran 1-14% slower in this order.
+__device__ __forceinline__ int64_t layer_major_unit_hw(int64_t n_units, int n_layers) {
+  const int64_t b = blockIdx.x;
+  return b < n_units ? layer_major_of(b, n_units, n_layers) : -1;
+}
+
 // Resolves the cache-side and record-side addresses of unit (page, layer),
 // page-major. Returns false when the unit's block id or record range is out
 // of bounds (the unit is then skipped, never touched).

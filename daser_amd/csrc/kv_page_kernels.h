@@ -39,12 +39,13 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_kernel(UnitArgs a) {
 // in-process at the Llama-3-8B shape (32 KiB pages) on three boxes: 12.27 vs
 // 12.60 ms, 11.98 vs 12.08, 11.97 vs 12.09 for kv_scatter_kernel at its
 // register-limited 3 workgroups per CU; kv_scatter_kernel itself at one
-// workgroup per CU 12.54-12.56 ms.
+// workgroup per CU 12.54-12.56 ms. Units in hardware dispatch order
+// (layer_major_unit_hw): a further 3.5%.
 __global__ __launch_bounds__(kThreads) void kv_scatter_stream_kernel(UnitArgs a) {
   constexpr int U = 8;
   uint8_t *cache, *rec;
   int l;
-  const int64_t u = layer_major_unit(a.n_units, a.n_layers);
+  const int64_t u = layer_major_unit_hw(a.n_units, a.n_layers);
   if (u < 0 || !unit_addresses(a, u, &cache, &rec, &l)) return;
   const int64_t pb = a.page_bytes;
   const rsrc_t sk = make_rsrc(rec, pb), sv = make_rsrc(rec + pb, pb);

@@ -221,6 +221,22 @@ def _validate(layout: PagedKVLayout, page_ids, slot_offsets, staging, layer0, n_
             raise ValueError("slot records of two pages overlap")
 
 
+def check_tables(table: "LayerTable", page_ids, slot_offsets, staging: torch.Tensor, *,
+                 layer0: int = 0, records_written: bool = False) -> None:
+    """The checks the copy wrappers run on host tables, for device-resident
+    ones (which the wrappers trust: the kernels skip a page whose block id or
+    record range is out of bounds instead of faulting, where the reference's
+    indexing would raise). Copies the tables to the host, so it synchronises
+    the stream: for debugging and for callers that build tables on the
+    device and want the reference's errors."""
+    def host(x, dt):
+        return x.detach().cpu().numpy().astype(dt) if isinstance(x, torch.Tensor) \
+            else np.asarray(x, dt)
+
+    _validate(table.layout, host(page_ids, np.int64), host(slot_offsets, np.int64), staging,
+              layer0, table.layout.num_layers, records_written)
+
+
 def dest_order(page_ids, slot_offsets, extra=None):
     """Host tables of a scatter, reordered by destination block (stable).
 

@@ -88,6 +88,36 @@ def test_page_copy_kernels_and_occupancy_match_oracle(gpu, tuning, heads, head_d
         assert np.array_equal(to_bits_np(dst[l], dt), dst_ref[l]), f"layer {l}"
 
 
+def test_device_tables_out_of_range_are_skipped_or_checked(gpu):
+    """Device-resident tables are trusted: a page with an out-of-range block
+    id or record offset is skipped (nothing written, no fault), the others
+    are copied; ops.check_tables raises the host wrappers' errors for them."""
+    print("case: device tables out of range", flush=True)
+    shape = KVShape(2, 2, 64, 16, 2)
+    nb = 8
+    caches = rand_caches(shape, nb, "bf16", gpu, seed=14)
+    st = torch.zeros(4 * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    table = ops.LayerTable(caches)
+    ids = torch.tensor([1, nb + 3, 4, -2], dtype=torch.int32, device=gpu)
+    offs = torch.tensor([0, 1, 2, 3], dtype=torch.int64, device=gpu) * shape.slot_bytes
+    ops.gather(table, ids, offs, st)
+    torch.cuda.synchronize()
+    rec = st.view(4, shape.num_layers, -1)
+    for l in range(shape.num_layers):
+        assert torch.equal(rec[0, l], caches[l][:, 1].reshape(-1).view(torch.uint8))
+        assert torch.equal(rec[2, l], caches[l][:, 4].reshape(-1).view(torch.uint8))
+    assert not rec[1].any() and not rec[3].any()
+    with pytest.raises(IndexError, match="block id"):
+        ops.check_tables(table, ids, offs, st, records_written=True)
+    bad_offs = offs.clone()
+    bad_offs[2] = 4 * shape.slot_bytes  # past the staging buffer
+    with pytest.raises(IndexError, match="staging"):
+        ops.check_tables(table, torch.tensor([1, 2, 4, 5], dtype=torch.int32, device=gpu),
+                         bad_offs, st)
+    ops.check_tables(table, torch.tensor([1, 2, 4, 5], dtype=torch.int32, device=gpu), offs, st,
+                     records_written=True)
+
+
 @pytest.mark.parametrize("shared", [True, False, None])
 @pytest.mark.parametrize("heads", [8, 1])
 def test_scatter_shared_records_hint_matches_oracle(gpu, heads, shared):
