@@ -28,8 +28,10 @@
  *   - launches are stream-ordered on `stream` (0 = the null stream), never
  *     synchronise, never allocate, and are reentrant across streams;
  *   - pages whose block id lies outside [0, num_blocks), or whose record
- *     would end beyond staging_bytes, are skipped by the kernel (the host
- *     wrappers reject them before launching);
+ *     would end beyond staging_bytes, are skipped by the kernel, never
+ *     touched and not reported (the Python wrappers reject them in host
+ *     tables before launching; daser_amd.ops.check_tables checks
+ *     device-resident ones on request);
  *   - return value: 0 on success, a DSR_ERR_* code (< 0) for argument errors,
  *     or a positive hipError_t from the launch.
  */
