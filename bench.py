@@ -384,6 +384,25 @@ class _BenchIPC:
         return {"ok": True}
 
 
+class _IndexServer:
+    """Stands in for the store server's sync client: match_and_alloc over a
+    retrieval index, with the reply the reference server builds
+    (daser/server/ipc_server.py:256-291); hits allocate nothing."""
+
+    def __init__(self, index, slot_bytes):
+        self.index, self.slot = index, slot_bytes
+
+    def match_and_alloc(self, tokens, chunk_key, model_id):
+        import asyncio
+
+        hits = asyncio.run(self.index.lookup(tokens, model_id))
+        return {"chunks": [{"chunk_key": m.chunk_key, "start_slot": m.start_slot,
+                            "num_slots": m.num_slots, "token_count": m.token_count,
+                            "pos_offset": m.pos_offset, "model_id": m.model_id,
+                            "file_offset": m.start_slot * self.slot} for m in hits],
+                "alloc": None}
+
+
 def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int = 16,
                   hit_pages: int = 128) -> dict:
     """Host cost and latency of the connector's worker hooks on serving-shaped
@@ -435,6 +454,67 @@ def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int 
                                            blocks[s0:s0 + chunk_pages], s0 * slot,
                                            chunk_pages * 16)
         return C.DaserConnectorMeta(reqs_to_store=reqs)
+
+    def rag_case(w, n_docs: int = 16, per_prompt: int = 10, n_prompts: int = 4):
+        """RAG prompts through both connector roles: n_docs cached 512-token
+        chunks (records already in the store file, stored at position 0) in a
+        ChunkAssemblyIndex; each prompt = per_prompt chunks drawn at random
+        + a 20-token question. The scheduler places the chunks (segments at
+        0, 512, ...) and the worker loads them, re-rotating each chunk's K
+        from 0 to its place. Times the scheduler hooks per request and the
+        worker's start_load_kv per step (n_prompts requests)."""
+        import asyncio
+
+        from daser_amd.retrieval import ChunkAssemblyIndex, ChunkMeta, chunk_key
+
+        bs, ct = shape.block_size, 512
+        idx = ChunkAssemblyIndex(bs)
+        trng = np.random.default_rng(9)
+        docs = [trng.integers(0, 120000, ct).tolist() for _ in range(n_docs)]
+        for i, t in enumerate(docs):
+            asyncio.run(idx.insert(ChunkMeta(chunk_key(t), i * (ct // bs), ct // bs, ct, 0,
+                                             "default")))
+        cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(
+            kv_connector_extra_config={"block_tokens": bs}))
+        sched = C.DaserConnector(cfg, C.KVConnectorRole.SCHEDULER,
+                                 ipc_client=_IndexServer(idx, slot))
+        sched_ms, load_ms, placed = [], [], []
+        need = per_prompt * ct // bs + 2
+        n_prompts = min(n_prompts, nb // need)
+        for it in range(steps + 1):
+            blocks = rng.permutation(nb)
+            meta_all = C.DaserConnectorMeta()
+            t0 = time.perf_counter()
+            for r in range(n_prompts):
+                pick = trng.choice(n_docs, per_prompt, replace=False)
+                prompt = [t for i in pick for t in docs[i]] + trng.integers(0, 120000, 20).tolist()
+                req = SimpleNamespace(request_id=f"rag{it}_{r}", prompt_token_ids=prompt)
+                n, _ = sched.get_num_new_matched_tokens(req, 0)
+                placed.append(n)
+                mine = blocks[r * need:(r + 1) * need].tolist()
+                sched.update_state_after_alloc(
+                    req, SimpleNamespace(blocks=[[SimpleNamespace(block_id=b) for b in mine]]), n)
+                m = sched.build_connector_meta(
+                    SimpleNamespace(num_scheduled_tokens={req.request_id: len(prompt)}))
+                meta_all.reqs_to_load.update(m.reqs_to_load)
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            w.bind_connector_metadata(meta_all)
+            w.start_load_kv(None)
+            torch.cuda.synchronize()
+            t3 = time.perf_counter()
+            w.clear_connector_metadata()
+            if it:
+                sched_ms.append((t1 - t0) * 1e3 / n_prompts)
+                load_ms.append((t3 - t2) * 1e3)
+        tok = n_prompts * per_prompt * ct
+        return {"tokens_placed_per_request": int(np.median(placed)),
+                "scheduler_ms_per_request_median": round(float(np.median(sched_ms)), 3),
+                "start_load_kv_ms_median": round(float(np.median(load_ms)), 3),
+                "loaded_tokens_per_s": round(tok / (np.median(load_ms) * 1e-3)),
+                "sample": f"{n_prompts} requests per step, each {per_prompt} of {n_docs} cached "
+                          f"{ct}-token chunks + 20 question tokens; records from the page cache"}
 
     try:
         for mode in ("blocking", "async_save"):
@@ -494,6 +574,7 @@ def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int 
         out["load_rerotate"] = load_case(n_req, hit_pages, True)
         out["load_one_chunk_rerotate"] = load_case(1, chunk_pages, True)
         out["load_one_chunk"] = load_case(1, chunk_pages, False)
+        out["rag_assembly"] = rag_case(w)
         w.shutdown()
 
         # the reference's loops for the same step sizes (device copies only, no I/O)
