@@ -208,8 +208,14 @@ size_t rot_occupancy_lds(int wg_per_cu) {
 // gather 22.07 -> 22.09. More than 64 KiB in flight per CU makes the DRAM
 // side slower, not faster (fewer, longer-waiting requests win); one
 // workgroup per CU at 16 KiB pages leaves the CU idle between units (28.4 ms).
-int copy_wg_per_cu(int64_t page_bytes) {
+// Launches of fewer than kPacedMinUnits units (a single layer's save of a
+// step, ...) keep the registers' occupancy: they end before a steady state,
+// and the limit measured 0-11% slower there (one layer, 1,024-4,096 pages:
+// gather 21.8 vs 19.6 us, 99 vs 94 us), against 1% faster from 8,192 units.
+constexpr int64_t kPacedMinUnits = 8192;
+int copy_wg_per_cu(int64_t page_bytes, int64_t n_units) {
   if (const int64_t t = tune(DSR_TUNE_COPY_WG_PER_CU)) return (int)t;
+  if (n_units < kPacedMinUnits) return 0;
   const int64_t w = (64 << 10) / (2 * page_bytes);
   return w >= 3 ? 0 : (int)(w < 1 ? 1 : w);
 }
@@ -369,7 +375,7 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
     if (G > 1) {
       kv_copy_grouped_kernel<true, kGatherUnroll><<<grid, kThreads, 0, st>>>(b, G);
     } else {
-      const size_t dyn = occupancy_lds(copy_wg_per_cu(page_bytes), 0);
+      const size_t dyn = occupancy_lds(copy_wg_per_cu(page_bytes, b.n_units), 0);
       kv_gather_kernel<<<grid, kThreads, dyn, st>>>(b);
     }
   });
@@ -400,7 +406,7 @@ int dsr_scatter_ex(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
     // more bytes in flight pay (the 70B share's 64 shared chunks: 50.5 ms at
     // the registers' 3 workgroups per CU vs 52.6 ms at one)
     const int wpc = (flags & DSR_SHARED_RECORDS) && !tune(DSR_TUNE_COPY_WG_PER_CU)
-                        ? 0 : copy_wg_per_cu(page_bytes);
+                        ? 0 : copy_wg_per_cu(page_bytes, b.n_units);
     const size_t dyn = occupancy_lds(wpc, 0);
     const int64_t pick = tune(DSR_TUNE_SCATTER_KERNEL);
     const bool stream_k = pick ? pick == 2 : wpc == 1 && page_bytes % (kThreads * 8 * 16) == 0;
