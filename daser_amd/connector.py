@@ -333,7 +333,12 @@ class DaserConnector(KVConnectorBase_V1):
         placed = place_chunks(tokens[:lookup_len], reply.get("chunks") or [], bs)
         if not placed:
             return 0, False
-        new_tokens = placed[-1][0] + int(placed[-1][1]["token_count"]) - num_computed_tokens
+        matched = placed[-1][0] + int(placed[-1][1]["token_count"])
+        # vLLM computes at least the last prompt token itself (its logits
+        # start the decode): a hit covering the whole prompt reports one token
+        # less. The load still fills the last page; the recomputed token's
+        # KV overwrites its own slot.
+        new_tokens = min(matched, len(tokens) - 1) - num_computed_tokens
         if new_tokens <= 0:
             return 0, False
         self._pending_loads[rid] = {"placed": placed}

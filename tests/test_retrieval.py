@@ -201,3 +201,17 @@ def test_load_spec_clips_to_the_blocks_given():
     one = C.load_spec(placed, [9, 8], BS)
     assert one.segments == [] and one.num_slots == 2 and one.block_ids == [9, 8]
     assert C.load_spec(placed, [], BS) is None
+
+
+def test_whole_prompt_hit_leaves_one_token_to_compute():
+    """A cached chunk covering the whole (block-aligned) prompt reports one
+    token less, so vLLM computes the last one; the load still covers every
+    page of the chunk."""
+    rng = np.random.default_rng(5)
+    a = rng.integers(0, 30000, size=64).tolist()
+    idx = IncrementalPrefixIndex(BS)
+    run(idx.insert(meta_for(a, 3)))
+    n, spec = _schedule(_scheduler(ServerWithIndex(idx)), "r", a, 8)
+    assert n == 63
+    assert spec.num_slots == 4 and spec.block_ids == [1000, 1001, 1002, 1003]
+    assert (spec.pos_offset, spec.new_pos) == (0, 0)
