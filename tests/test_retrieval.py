@@ -215,3 +215,21 @@ def test_whole_prompt_hit_leaves_one_token_to_compute():
     assert n == 63
     assert spec.num_slots == 4 and spec.block_ids == [1000, 1001, 1002, 1003]
     assert (spec.pos_offset, spec.new_pos) == (0, 0)
+
+
+# The reference's own index behaviours (tests/retrieval/test_prefix_index.py:
+# exact hit, a longer query finds the prefix, miss, remove, model isolation),
+# held by both indexes at block size 4.
+@pytest.mark.parametrize("cls", [IncrementalPrefixIndex, ChunkAssemblyIndex])
+def test_reference_index_behaviours(cls):
+    toks = [1, 2, 3, 4]
+    meta = ChunkMeta(chunk_key(toks), 0, 1, 4, 0, "m")
+    idx = cls(4)
+    assert run(idx.lookup(toks, "m")) == []
+    run(idx.insert(meta))
+    assert [m.chunk_key for m in run(idx.lookup(toks, "m"))] == [meta.chunk_key]
+    assert [m.chunk_key for m in run(idx.lookup([1, 2, 3, 4, 5, 6, 7, 8], "m"))] == \
+        [meta.chunk_key]
+    assert run(idx.lookup(toks, "other-model")) == []
+    run(idx.remove(meta.chunk_key))
+    assert run(idx.lookup(toks, "m")) == []
