@@ -209,13 +209,16 @@ size_t rot_occupancy_lds(int wg_per_cu) {
 // side slower, not faster (fewer, longer-waiting requests win); one
 // workgroup per CU at 16 KiB pages leaves the CU idle between units (28.4 ms).
 // Launches of fewer than kPacedMinUnits units (a single layer's save of a
-// step, ...) keep the registers' occupancy: they end before a steady state,
-// and the limit measured 0-11% slower there (one layer, 1,024-4,096 pages:
-// gather 21.8 vs 19.6 us, 99 vs 94 us), against 1% faster from 8,192 units.
+// step, ...) keep the registers' three workgroups per CU, with dynamic LDS
+// sized for three (one layer's scatter of 1,024-4,096 pages: 23.1 vs 24.4
+// and 83.4 vs 86.0 us without LDS; gathers alike): they end before a steady
+// state, and one per CU measured 0-11% slower there (one layer, 1,024-4,096
+// pages: gather 21.8 vs 19.6 us, 99 vs 94 us), against 1% faster from 8,192
+// units.
 constexpr int64_t kPacedMinUnits = 8192;
 int copy_wg_per_cu(int64_t page_bytes, int64_t n_units) {
   if (const int64_t t = tune(DSR_TUNE_COPY_WG_PER_CU)) return (int)t;
-  if (n_units < kPacedMinUnits) return 0;
+  if (n_units < kPacedMinUnits) return 3;
   const int64_t w = (64 << 10) / (2 * page_bytes);
   return w >= 3 ? 0 : (int)(w < 1 ? 1 : w);
 }
@@ -399,7 +402,10 @@ int dsr_scatter_ex(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
     const hipStream_t st = (hipStream_t)stream;
     if (G > 1) {
-      kv_copy_grouped_kernel<false, kScatterUnroll><<<grid, kThreads, 0, st>>>(b, G);
+      // dynamic LDS for the registers' three workgroups per CU: 6.95 vs
+      // 7.10 ms at the 70B TP8 share's 4 KiB pages (the same effect as for
+      // the token kernels; the gather measured alike with and without)
+      kv_copy_grouped_kernel<false, kScatterUnroll><<<grid, kThreads, occupancy_lds(3, 0), st>>>(b, G);
       return;
     }
     // records read by several pages are partly served by the caches, so
@@ -790,9 +796,9 @@ int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t 
       else
         kv_slots_small_kernel<false, 4><<<grid, kThreads, 0, s>>>(b);
     } else if (gather) {
-      kv_slots_kernel<true><<<grid, kThreads, 0, s>>>(b);
+      kv_slots_kernel<true><<<grid, kThreads, occupancy_lds(3, 0), s>>>(b);
     } else {
-      kv_slots_kernel<false><<<grid, kThreads, 0, s>>>(b);
+      kv_slots_kernel<false><<<grid, kThreads, occupancy_lds(3, 0), s>>>(b);
     }
     const int rc = (int)hipGetLastError();
     if (rc != 0) return rc;
