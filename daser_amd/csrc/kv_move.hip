@@ -275,6 +275,11 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
   return launch_page_ranges(ra.u, n_pages, GL, [&](const UnitArgs& b, unsigned grid) {
     RotArgs rb = ra;
     rb.u = b;
+    // one unit per workgroup over distinct records: the whole chip on one
+    // stretch of one layer, as the streaming scatter (config 3: 6.89-6.92 vs
+    // 7.04-7.05 ms on two boxes); several units per workgroup (8.1% slower
+    // at the TP8 share) and shared records (equal) keep the XCD order
+    rb.hw_order = grouped && GL == 1 && !(flags & DSR_SHARED_RECORDS);
     rb.rope_idx = ra.rope_idx + (b.page_ids - ra.u.page_ids);
     if (grouped) {
       if (hnd && style == DSR_ROPE_NEOX)

@@ -148,6 +148,9 @@ struct RotArgs {
   int32_t kx_row_shift = 0;
   int32_t kx_bs_shift = 0;
   int32_t kx_dist = 0;
+  // Grouped kernel: walk its groups in hardware dispatch order (consecutive
+  // workgroups take consecutive groups) instead of XCD-contiguous eighths.
+  int32_t hw_order = 0;
 };
 
 // Split-x K: the lane-consecutive vector index i of a page -> the vector it
@@ -679,7 +682,9 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
   constexpr int U = rot_contig_unroll<DT>();
   __shared__ float2 tab[kMaxRotHalf];
   const UnitArgs& a = ra.u;
-  const int64_t g = xcd_unit((a.n_units + G - 1) / G);
+  const int64_t ng = (a.n_units + G - 1) / G;
+  const int64_t g = ra.hw_order ? ((int64_t)blockIdx.x < ng ? (int64_t)blockIdx.x : -1)
+                                : xcd_unit(ng);
   if (g < 0) return;
   const int64_t n_pages = a.n_units / a.n_layers;
   const int nvec = (int)(a.page_bytes >> 4);
