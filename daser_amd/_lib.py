@@ -35,6 +35,7 @@ DSR_RING_NO_URING = 4
 DSR_DTYPE_BF16 = 0
 DSR_DTYPE_FP16 = 1
 DSR_DTYPE_FP8_E4M3 = 2
+DSR_DTYPE_FP8_E5M2 = 3
 
 DSR_ROPE_NEOX = 0
 DSR_ROPE_GPTJ = 1

@@ -390,10 +390,12 @@ class DaserConnector(KVConnectorBase_V1):
 
     # --------------------------------------------------------------- worker
     def register_kv_caches(self, kv_caches: dict[str, torch.Tensor]) -> None:
-        if self._cache_dtype in ("fp8", "fp8_e4m3"):
+        fp8 = {"fp8": torch.float8_e4m3fn, "fp8_e4m3": torch.float8_e4m3fn,
+               "fp8_e5m2": torch.float8_e5m2}.get(self._cache_dtype)
+        if fp8 is not None:
             # vLLM may hold an fp8 cache as raw uint8; the re-rotation needs the
-            # element format (OCP e4m3fn on gfx950). A view, no copy.
-            kv_caches = {n: t.view(torch.float8_e4m3fn) if t.dtype == torch.uint8 else t
+            # element format (OCP e4m3fn or e5m2 on gfx950). A view, no copy.
+            kv_caches = {n: t.view(fp8) if t.dtype == torch.uint8 else t
                          for n, t in kv_caches.items()}
         self._slot_size = self._plane.register(kv_caches, self._slot_size)
         logger.info("[CONNECTOR] %d layers, slot_size=%d", len(kv_caches), self._slot_size)
@@ -419,12 +421,13 @@ class DaserConnector(KVConnectorBase_V1):
         if self._meta is None or not self._meta.reqs_to_load or self._plane.table is None:
             return
         plan = plan_load(self._meta.reqs_to_load, self._slot_size)
-        if plan.deltas and self._plane.table.layout.dtype == torch.float8_e4m3fn:
+        if plan.deltas and self._plane.table.layout.dtype in (torch.float8_e4m3fn,
+                                                               torch.float8_e5m2):
             self._plane.k_scales = self._fp8_k_scales(forward_context)
         self._plane.load(plan)
 
     def _fp8_k_scales(self, forward_context: Any) -> torch.Tensor:
-        """Per-layer K scales of an e4m3 cache, in registration order: the
+        """Per-layer K scales of an fp8 (e4m3 or e5m2) cache, in registration order: the
         attention modules' ``_k_scale`` (vLLM keeps them there; the forward
         context maps layer names to the modules in ``no_compile_layers``), or
         ``kv_connector_extra_config["k_scale"]`` for one scale everywhere.

@@ -152,7 +152,7 @@ int launch_page_ranges(const UnitArgs& a, int n_pages, int G, F launch) {
 // 30.1 ms at 2).
 template <int DT>
 constexpr int rot_wg_per_cu() {
-  return DT == DSR_DTYPE_FP8_E4M3 ? 4 : 2;
+  return is_fp8<DT>() ? 4 : 2;
 }
 // The same for the grouped re-rotation kernel (pages below U * 4 KiB; env
 // DSR_ROT_GROUPED_WG_PER_CU overrides). Measured in-process at the
@@ -161,7 +161,7 @@ constexpr int rot_wg_per_cu() {
 // pages 12.96 ms at 8 (13.72 at 4).
 template <int DT>
 constexpr int rot_grouped_wg_per_cu() {
-  return DT == DSR_DTYPE_FP8_E4M3 ? 8 : 4;
+  return is_fp8<DT>() ? 8 : 4;
 }
 // The grouped kernel with one unit per workgroup (16-bit pages of exactly
 // U * 4 KiB, the Llama-3-8B/70B shapes): 3 per CU. Measured in-process:
@@ -259,7 +259,7 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
   const int64_t nvec = ra.u.page_bytes >> 4;
   const bool single = contig && nvec % kThreads == 0 &&
                       nvec == (int64_t)rot_contig_unroll<DT>() * kThreads;
-  bool grouped = G > 1 || (single && DT != DSR_DTYPE_FP8_E4M3);
+  bool grouped = G > 1 || (single && !is_fp8<DT>());
   if (rot_kernel == kRotContig && contig) grouped = false;
   if (rot_kernel == kRotGrouped && (G > 1 || single)) grouped = true;
   if (grouped) {
@@ -471,6 +471,7 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
       ve = 8;
       break;
     case DSR_DTYPE_FP8_E4M3:
+    case DSR_DTYPE_FP8_E5M2:
       esize = 1;
       ve = 16;
       break;
@@ -497,7 +498,7 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
                                                                    : rot_dim / ve;
   if (n_pages == 0 || n_layers == 0) return DSR_OK;
   if (!rope_idx || (n_tables > 0 && !cos_sin)) return DSR_ERR_ARG;
-  if (dtype == DSR_DTYPE_FP8_E4M3 && !k_scale) return DSR_ERR_ARG;
+  if (esize == 1 && !k_scale) return DSR_ERR_ARG;
 
   RotArgs ra;
   ra.u = make_unit(layer_base, n_layers, kv_stride, page_stride, page_bytes,
@@ -537,8 +538,11 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
       case DSR_DTYPE_FP16:
         return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, true, s, false, flags,
                                                true);
-      default:
+      case DSR_DTYPE_FP8_E4M3:
         return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, true, s, false,
+                                                   flags, true);
+      default:
+        return launch_rerotate<DSR_DTYPE_FP8_E5M2>(ra, n_pages, rope_style, true, s, false,
                                                    flags, true);
     }
   }
@@ -560,8 +564,10 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
           return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, true, s, true, flags);
         case DSR_DTYPE_FP16:
           return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, true, s, true, flags);
-        default:
+        case DSR_DTYPE_FP8_E4M3:
           return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, true, s, true, flags);
+        default:
+          return launch_rerotate<DSR_DTYPE_FP8_E5M2>(ra, n_pages, rope_style, true, s, true, flags);
       }
     }
     switch (dtype) {
@@ -569,8 +575,10 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
         return launch_rerotate_pairs<DSR_DTYPE_BF16>(ra, n_pages, rope_style, s);
       case DSR_DTYPE_FP16:
         return launch_rerotate_pairs<DSR_DTYPE_FP16>(ra, n_pages, rope_style, s);
-      default:
+      case DSR_DTYPE_FP8_E4M3:
         return launch_rerotate_pairs<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, s);
+      default:
+        return launch_rerotate_pairs<DSR_DTYPE_FP8_E5M2>(ra, n_pages, rope_style, s);
     }
   }
   switch (dtype) {
@@ -578,8 +586,10 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
       return launch_rerotate<DSR_DTYPE_BF16>(ra, n_pages, rope_style, vec_ok, s, false, flags);
     case DSR_DTYPE_FP16:
       return launch_rerotate<DSR_DTYPE_FP16>(ra, n_pages, rope_style, vec_ok, s, false, flags);
-    default:
+    case DSR_DTYPE_FP8_E4M3:
       return launch_rerotate<DSR_DTYPE_FP8_E4M3>(ra, n_pages, rope_style, vec_ok, s, false, flags);
+    default:
+      return launch_rerotate<DSR_DTYPE_FP8_E5M2>(ra, n_pages, rope_style, vec_ok, s, false, flags);
   }
 }
 

@@ -66,6 +66,40 @@ __device__ __forceinline__ uint32_t f32x4_to_e4m3(const float* y) {
   return w ^ ff_bytes(w);
 }
 
+// OCP e5m2 (bias 15, infinities, S.11111.{01,10,11} = NaN) through the
+// gfx950 bf8 conversions (v_cvt_pk_f32_bf8 / v_cvt_pk_bf8_f32, round to
+// nearest even). Encoding saturates as for e4m3: finite values and
+// infinities clamp to +-57344 (compare-select keeps NaN), so an encoded byte
+// with an all-ones exponent is NaN, rewritten to torch's canonical 0x7F.
+__device__ __forceinline__ float clamp57344(float f) {
+  f = f > 57344.0f ? 57344.0f : f;
+  return f < -57344.0f ? -57344.0f : f;
+}
+__device__ __forceinline__ void e5m2x4_to_f32(uint32_t w, float* x) {
+  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, false);
+  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_bf8((int)w, true);
+  x[0] = lo.x;
+  x[1] = lo.y;
+  x[2] = hi.x;
+  x[3] = hi.y;
+}
+__device__ __forceinline__ uint32_t f32x4_to_e5m2(const float* y) {
+  int e = __builtin_amdgcn_cvt_pk_bf8_f32(clamp57344(y[0]), clamp57344(y[1]), 0, false);
+  e = __builtin_amdgcn_cvt_pk_bf8_f32(clamp57344(y[2]), clamp57344(y[3]), e, true);
+  const uint32_t w = (uint32_t)e;
+  // bytes whose exponent bits (0x7C) are all set: 0x80 in each such byte
+  const uint32_t x = (w & 0x7c7c7c7cu) ^ 0x7c7c7c7cu;  // zero byte <=> exponent all ones
+  const uint32_t nan = ~(((x & 0x7f7f7f7fu) + 0x7f7f7f7fu) | x | 0x7f7f7f7fu);
+  const uint32_t bytes = (nan >> 7) * 0xffu;
+  return (w & ~bytes) | (0x7f7f7f7fu & bytes);
+}
+
+// The 8-bit formats: one byte per element, K scaled by the layer's k_scale.
+template <int DT>
+constexpr bool is_fp8() {
+  return DT == DSR_DTYPE_FP8_E4M3 || DT == DSR_DTYPE_FP8_E5M2;
+}
+
 template <int DT>
 struct Codec;
 
@@ -118,6 +152,21 @@ struct Codec<DSR_DTYPE_FP8_E4M3> {
     u32x4 v;
 #pragma unroll
     for (int k = 0; k < 4; ++k) v[k] = f32x4_to_e4m3(y + 4 * k);
+    return v;
+  }
+};
+
+template <>
+struct Codec<DSR_DTYPE_FP8_E5M2> {
+  static constexpr int VE = 16;
+  __device__ static void decode(u32x4 v, float* x) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) e5m2x4_to_f32(v[k], x + 4 * k);
+  }
+  __device__ static u32x4 encode(const float* y) {
+    u32x4 v;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = f32x4_to_e5m2(y + 4 * k);
     return v;
   }
 };
@@ -232,7 +281,7 @@ struct KRound {
   __device__ __forceinline__ void store(rsrc_t rd, const float2* tab, int half_off,
                                         float scale, float inv_scale) {
     using C = Codec<DT>;
-    constexpr bool kScaled = DT == DSR_DTYPE_FP8_E4M3;
+    constexpr bool kScaled = is_fp8<DT>();
 #pragma unroll
     for (int k = 0; k < kRotUnroll; ++k) {
       if (kind[k] == 1) {
@@ -345,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
   const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
   for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
   float scale = 1.0f, inv_scale = 1.0f;
-  if (DT == DSR_DTYPE_FP8_E4M3) {
+  if (is_fp8<DT>()) {
     scale = ra.k_scale[ra.u.layer0 + l];
     inv_scale = 1.0f / scale;
   }
@@ -373,7 +422,7 @@ __device__ __forceinline__ u32x4 rotate_vec(const RotArgs& ra, u32x4 own, u32x4 
                                             const float2* tab, float scale, float inv_scale) {
   using C = Codec<DT>;
   constexpr int VE = C::VE;
-  constexpr bool kScaled = DT == DSR_DTYPE_FP8_E4M3;
+  constexpr bool kScaled = is_fp8<DT>();
   if (c >= ra.rot_vecs) return own;
   float x[VE];
   C::decode(own, x);
@@ -441,7 +490,7 @@ __device__ __forceinline__ void rotate_contig_round(const RotArgs& ra, VRound<U>
 // 16 KiB e4m3 Llama page.
 template <int DT>
 constexpr int rot_contig_unroll() {
-  return DT == DSR_DTYPE_FP8_E4M3 ? 4 : 8;
+  return is_fp8<DT>() ? 4 : 8;
 }
 
 template <int DT, int STYLE, bool KX, bool HND = false>
@@ -474,7 +523,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
   const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
   for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
   float scale = 1.0f, inv_scale = 1.0f;
-  if (DT == DSR_DTYPE_FP8_E4M3) {
+  if (is_fp8<DT>()) {
     scale = ra.k_scale[ra.u.layer0 + l];
     inv_scale = 1.0f / scale;
   }
@@ -550,7 +599,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_rows_kernel(RotA
   const float2* src_tab = ra.cos_sin + (int64_t)ti * ra.rot_half;
   for (int j = threadIdx.x; j < ra.rot_half; j += kThreads) tab[j] = src_tab[j];
   float scale = 1.0f, inv_scale = 1.0f;
-  if (DT == DSR_DTYPE_FP8_E4M3) {
+  if (is_fp8<DT>()) {
     scale = ra.k_scale[ra.u.layer0 + l];
     inv_scale = 1.0f / scale;
   }
@@ -585,6 +634,7 @@ template <int DT>
 __device__ __forceinline__ float elem_decode(uint32_t bits) {
   if (DT == DSR_DTYPE_BF16) return bf16_to_f32(bits);
   if (DT == DSR_DTYPE_FP16) return fp16_to_f32(bits);
+  if (DT == DSR_DTYPE_FP8_E5M2) return __builtin_amdgcn_cvt_pk_f32_bf8((int)bits, false)[0];
   return __builtin_amdgcn_cvt_pk_f32_fp8((int)bits, false)[0];
 }
 
@@ -592,9 +642,9 @@ template <int DT, int STYLE>
 __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_lds_kernel(RotArgs ra) {
   using C = Codec<DT>;
   constexpr int VE = C::VE;
-  constexpr int EB = DT == DSR_DTYPE_FP8_E4M3 ? 8 : 16;  // bits per element
+  constexpr int EB = is_fp8<DT>() ? 8 : 16;  // bits per element
   constexpr int PER = 32 / EB;                           // elements per dword
-  constexpr bool kScaled = DT == DSR_DTYPE_FP8_E4M3;
+  constexpr bool kScaled = is_fp8<DT>();
   constexpr int kChunkVecs = 2048;  // 32 KiB of K rows per pass
   __shared__ u32x4 buf[kChunkVecs];
   __shared__ float2 tab[kMaxRotHalf];
@@ -713,7 +763,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
     kd[k] = make_rsrc(u.cache, u.n);
     vd[k] = make_rsrc(u.cache + a.kv_stride, u.n);
     tj[k] = u.n && rope_table(ra, u.p, u.l) >= 0 ? j : -1;
-    sc[k] = DT == DSR_DTYPE_FP8_E4M3 && u.n ? ra.k_scale[a.layer0 + u.l] : 1.0f;
+    sc[k] = is_fp8<DT>() && u.n ? ra.k_scale[a.layer0 + u.l] : 1.0f;
   }
   // tables of the group's units, fetched while the page loads are in flight
   for (int e = threadIdx.x; e < (int)n_here * ra.rot_half; e += kThreads) {

@@ -28,7 +28,9 @@ _DTYPE_CODES = {
     torch.bfloat16: _lib.DSR_DTYPE_BF16,
     torch.float16: _lib.DSR_DTYPE_FP16,
     torch.float8_e4m3fn: _lib.DSR_DTYPE_FP8_E4M3,
+    torch.float8_e5m2: _lib.DSR_DTYPE_FP8_E5M2,
 }
+FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
 
 ROPE_STYLES = {"neox": _lib.DSR_ROPE_NEOX, "gptj": _lib.DSR_ROPE_GPTJ}
 
@@ -452,7 +454,7 @@ def scatter_rerotate(
     if ridx_d.numel() != _tables[0].numel():
         raise ValueError("rope_idx and page_ids differ in length")
     ks_ptr = None
-    if lay.dtype == torch.float8_e4m3fn:
+    if lay.dtype in FP8_DTYPES:
         if k_scale is None:
             raise ValueError("fp8 re-rotation needs per-layer k_scale")
         if (

@@ -99,6 +99,7 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 #define DSR_DTYPE_BF16 0
 #define DSR_DTYPE_FP16 1
 #define DSR_DTYPE_FP8_E4M3 2 /* OCP e4m3fn: bias 7, max 448, NaN 0x7F/0xFF */
+#define DSR_DTYPE_FP8_E5M2 3 /* OCP e5m2: bias 15, max 57344, infinities, NaN */
 
 /* RoPE pairings. */
 #define DSR_ROPE_NEOX 0 /* rotate-half: pairs (j, j + rot_dim/2)  (Llama) */

@@ -11,7 +11,8 @@
  *       the reference loops (bytes(kv[:, b]) at i*SLOT + l*LAYER), the
  *       reference's slot-size constants, and the round-trip identity;
  *   orc_decode / orc_encode     against torch's bfloat16 / float16 /
- *       float8_e4m3fn conversions (all 256 e4m3 codes, sweeps of fp32 values);
+ *       float8_e4m3fn / float8_e5m2 conversions (all 256 codes of each 8-bit
+ *       format, sweeps of fp32 values);
  *   orc_scatter_rerotate        against closed forms: zero delta is a copy,
  *       R(a)R(-a) = I, R(a)R(b) = R(a+b), pair norms preserved, the complex
  *       multiplication (x1 + i x2) e^{i delta w_j}, and single-pair known
@@ -26,6 +27,8 @@
 #define ORC_BF16 0
 #define ORC_FP16 1
 #define ORC_E4M3 2
+#define ORC_E5M2 3
+#define ORC_IS_FP8(d) ((d) == ORC_E4M3 || (d) == ORC_E5M2)
 
 #define ORC_NEOX 0
 #define ORC_GPTJ 1
@@ -71,16 +74,19 @@ void orc_scatter(uint8_t* const* layer_base, int n_layers, int64_t kv_stride,
  * bf16: IEEE binary32 truncated to 1+8+7 bits.
  * fp16: IEEE binary16, 1+5+10, bias 15.
  * e4m3: OCP 8-bit float e4m3fn, 1+4+3, bias 7, no infinities, only
- *       S.1111.111 is NaN, max finite 448. */
+ *       S.1111.111 is NaN, max finite 448.
+ * e5m2: OCP 8-bit float e5m2, 1+5+2, bias 15, IEEE-style infinities
+ *       (S.11111.00) and NaNs (S.11111.{01,10,11}), max finite 57344. */
 typedef struct {
   int mbits, emin, bias, sign_shift;
   double maxv;
 } fmt_t;
 
-static const fmt_t FMT[3] = {
+static const fmt_t FMT[4] = {
     {7, -126, 127, 15, 3.38953138925153547590470800371487866880e38},
     {10, -14, 15, 15, 65504.0},
     {3, -6, 7, 7, 448.0},
+    {2, -14, 15, 7, 57344.0},
 };
 
 double orc_decode(int dtype, uint32_t bits) {
@@ -106,14 +112,15 @@ double orc_decode(int dtype, uint32_t bits) {
 
 /* Rounds v to the format (round to nearest, ties to even, at the format's
  * precision and subnormal spacing) and returns its bit pattern.
- * e4m3 saturates to +-448 before rounding (so never overflows); bf16/fp16
- * overflow to infinity. NaN -> 0x7FC0 / 0x7E00 / 0x7F. */
+ * The 8-bit formats saturate to +-max (448, 57344) before rounding, so they
+ * never overflow (e5m2 infinities included, as a saturating conversion
+ * does); bf16/fp16 overflow to infinity. NaN -> 0x7FC0 / 0x7E00 / 0x7F. */
 uint32_t orc_encode(int dtype, double v) {
   const fmt_t* f = &FMT[dtype];
   if (isnan(v)) return dtype == ORC_BF16 ? 0x7fc0u : dtype == ORC_FP16 ? 0x7e00u : 0x7fu;
-  if (dtype == ORC_E4M3) {
-    if (v > 448.0) v = 448.0;
-    if (v < -448.0) v = -448.0;
+  if (ORC_IS_FP8(dtype)) {
+    if (v > f->maxv) v = f->maxv;
+    if (v < -f->maxv) v = -f->maxv;
   }
   const uint32_t s = signbit(v) ? 1u : 0u;
   double a = fabs(v);
@@ -143,14 +150,14 @@ uint32_t orc_encode(int dtype, double v) {
 }
 
 static uint32_t load_elem(const uint8_t* row, int dtype, int j) {
-  if (dtype == ORC_E4M3) return row[j];
+  if (ORC_IS_FP8(dtype)) return row[j];
   uint16_t h;
   memcpy(&h, row + 2 * j, 2);
   return h;
 }
 
 static void store_elem(uint8_t* row, int dtype, int j, uint32_t bits) {
-  if (dtype == ORC_E4M3) {
+  if (ORC_IS_FP8(dtype)) {
     row[j] = (uint8_t)bits;
   } else {
     uint16_t h = (uint16_t)bits;
@@ -178,8 +185,8 @@ static void rot(double* x1, double* x2, double a) {
  * is the same map for finite inputs, but turns an infinite element into NaN
  * through inf * sin(0) when a position is 0.)
  * Pairs: neox (j, j + rot_dim/2); gptj (2j, 2j + 1). Elements >= rot_dim and
- * V are copied. e4m3: x = decode(q) * k_scale[layer], result / k_scale is
- * encoded (saturating). The result is rounded once to the storage format. */
+ * V are copied. e4m3 / e5m2: x = decode(q) * k_scale[layer], result /
+ * k_scale is encoded (saturating). The result is rounded once to the storage format. */
 void orc_scatter_rerotate(uint8_t* const* layer_base, int n_layers,
                           int64_t kv_stride, int64_t page_stride,
                           int64_t page_bytes, const int32_t* page_ids,
@@ -190,7 +197,7 @@ void orc_scatter_rerotate(uint8_t* const* layer_base, int n_layers,
                           const int64_t* stored_pos, const int64_t* new_pos,
                           const int8_t* rotate, double theta,
                           const double* inv_freq) {
-  const int esize = dtype == ORC_E4M3 ? 1 : 2;
+  const int esize = ORC_IS_FP8(dtype) ? 1 : 2;
   const int64_t row_bytes = (int64_t)head_dim * esize;
   const int64_t rows = page_bytes / row_bytes;
   const int half = rot_dim / 2;
@@ -203,7 +210,7 @@ void orc_scatter_rerotate(uint8_t* const* layer_base, int n_layers,
   for (int p = 0; p < n_pages; ++p) {
     if (!rotate[p]) continue;
     for (int l = 0; l < n_layers; ++l) {
-      const double sc = dtype == ORC_E4M3 ? (double)k_scale[layer0 + l] : 1.0;
+      const double sc = ORC_IS_FP8(dtype) ? (double)k_scale[layer0 + l] : 1.0;
       uint8_t* dst = layer_base[l] + (int64_t)page_ids[p] * page_stride;
       const uint8_t* src = staging + slot_offsets[p] + (int64_t)(layer0 + l) * layer_bytes;
       for (int64_t r = 0; r < rows; ++r) {

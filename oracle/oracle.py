@@ -5,7 +5,7 @@ bench.py's cpu_baseline leg, never by the daser_amd package.
 
 Arrays are host numpy arrays. A layer cache is a C-contiguous array of shape
 (2, num_blocks, block_size, num_heads, head_dim) holding raw element bits
-(uint16 for bf16/fp16, uint8 for e4m3); staging is a uint8 array.
+(uint16 for bf16/fp16, uint8 for e4m3 / e5m2); staging is a uint8 array.
 """
 
 from __future__ import annotations
@@ -20,7 +20,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkv_oracle.so")
 
-BF16, FP16, E4M3 = 0, 1, 2
+BF16, FP16, E4M3, E5M2 = 0, 1, 2, 3
 NEOX, GPTJ = 0, 1
 
 _lib: Optional[ctypes.CDLL] = None
@@ -184,7 +184,7 @@ def encode(dtype: int, values) -> np.ndarray:
 
 def ulp_steps(a: np.ndarray, b: np.ndarray, dtype: int) -> np.ndarray:
     """Representable steps between two sign-magnitude bit patterns."""
-    sign = 1 << (7 if dtype == E4M3 else 15)
+    sign = 1 << (7 if dtype in (E4M3, E5M2) else 15)
 
     def ordered(x):
         x = np.asarray(x).astype(np.int64)

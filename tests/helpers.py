@@ -8,10 +8,11 @@ import torch
 from daser_amd.workloads import KVShape
 from oracle import oracle
 
-TORCH_DT = {"bf16": torch.bfloat16, "fp16": torch.float16, "e4m3": torch.float8_e4m3fn}
-BITS_NP = {"bf16": np.uint16, "fp16": np.uint16, "e4m3": np.uint8}
-BITS_T = {"bf16": torch.int16, "fp16": torch.int16, "e4m3": torch.uint8}
-ORC_DT = {"bf16": 0, "fp16": 1, "e4m3": 2}
+TORCH_DT = {"bf16": torch.bfloat16, "fp16": torch.float16, "e4m3": torch.float8_e4m3fn,
+            "e5m2": torch.float8_e5m2}
+BITS_NP = {"bf16": np.uint16, "fp16": np.uint16, "e4m3": np.uint8, "e5m2": np.uint8}
+BITS_T = {"bf16": torch.int16, "fp16": torch.int16, "e4m3": torch.uint8, "e5m2": torch.uint8}
+ORC_DT = {"bf16": 0, "fp16": 1, "e4m3": 2, "e5m2": 3}
 
 
 def rand_caches(shape: KVShape, num_blocks: int, dt: str, device, seed: int,
@@ -34,7 +35,7 @@ def ordered(bits: np.ndarray, dt: str) -> np.ndarray:
     """Maps sign-magnitude float bits to integers ordered like the values,
     so that |ordered(a) - ordered(b)| counts representable steps (ulps)."""
     b = bits.astype(np.int64)
-    sign = 1 << (15 if dt != "e4m3" else 7)
+    sign = 1 << (7 if dt in ("e4m3", "e5m2") else 15)
     mag = b & (sign - 1)
     return np.where(b & sign, -mag, mag)
 

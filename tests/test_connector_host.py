@@ -342,6 +342,7 @@ def test_fp8_rotated_load_needs_k_scales(tmp_path):
 
 @pytest.mark.parametrize("cache_dtype,expect", [("fp8", "float8_e4m3fn"),
                                                  ("fp8_e4m3", "float8_e4m3fn"),
+                                                 ("fp8_e5m2", "float8_e5m2"),
                                                  ("auto", "uint8")])
 def test_uint8_fp8_cache_viewed_as_e4m3(tmp_path, cache_dtype, expect):
     """vLLM may allocate an fp8 cache as uint8; with cache_config.cache_dtype

@@ -15,6 +15,8 @@ from tests.helpers import ORC_DT, rand_caches, rotation_within_tolerance, to_bit
 
 pytestmark = pytest.mark.gpu
 
+FP8 = ("e4m3", "e5m2")
+
 
 def _np_layers(caches, dt):
     return [to_bits_np(c, dt) for c in caches]
@@ -73,7 +75,7 @@ def test_page_copy_kernels_and_occupancy_match_oracle(gpu, tuning, heads, head_d
           flush=True)
     tuning("scatter_kernel", kernel)
     tuning("copy_wg_per_cu", wg_per_cu)
-    shape = KVShape(3, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    shape = KVShape(3, heads, head_dim, 16, 1 if dt in FP8 else 2)
     wl = workloads.ragged(shape, 6, 1, 400, seed=heads + head_dim, pool_slack=1.3)
     caches = rand_caches(shape, wl.num_blocks, dt, gpu, seed=9, scale=3.0)
     staging, ref = _gather_both(wl, caches, dt, gpu)
@@ -144,10 +146,10 @@ def test_scatter_shared_records_hint_matches_oracle(gpu, heads, shared):
         assert np.array_equal(to_bits_np(dst[l], "bf16"), ref[l]), f"layer {l}"
 
 
-@pytest.mark.parametrize("dt", ["e4m3", "fp16"])
+@pytest.mark.parametrize("dt", ["e4m3", "e5m2", "fp16"])
 def test_gather_scatter_other_dtypes_bit_exact(gpu, dt):
     print(f"case: gather/scatter {dt}", flush=True)
-    shape = KVShape(4, 8, 128, 16, 1 if dt == "e4m3" else 2)
+    shape = KVShape(4, 8, 128, 16, 1 if dt in FP8 else 2)
     wl = workloads.ragged(shape, 5, 1, 300, seed=3, pool_slack=1.5)
     caches = rand_caches(shape, wl.num_blocks, dt, gpu, seed=4, scale=3.0)
     staging, ref = _gather_both(wl, caches, dt, gpu)
@@ -220,14 +222,14 @@ def test_per_layer_rerotate_matches_all_layer_launch(gpu, heads, head_dim, dt):
     bytes as one launch over all layers: every kernel reads layer l's K scale
     at k_scale[layer0 + l]."""
     print(f"case: per-layer rerotate H{heads} D{head_dim} {dt}", flush=True)
-    shape = KVShape(6, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    shape = KVShape(6, heads, head_dim, 16, 1 if dt in FP8 else 2)
     wl = workloads.ragged(shape, 4, 40, 400, seed=13, num_blocks=128)
-    src = rand_caches(shape, wl.num_blocks, dt, gpu, seed=80, scale=40.0 if dt == "e4m3" else 1.0)
+    src = rand_caches(shape, wl.num_blocks, dt, gpu, seed=80, scale=40.0 if dt in FP8 else 1.0)
     st = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
     ops.gather(ops.LayerTable(src), wl.page_ids, wl.slot_offsets, st)
     ridx = (np.arange(wl.n_pages) % 3 - 1).astype(np.int32)
     tabs = position.delta_tables([517, 32767], head_dim, 500000.0, device=gpu)
-    ks = torch.linspace(0.05, 0.6, shape.num_layers, device=gpu) if dt == "e4m3" else None
+    ks = torch.linspace(0.05, 0.6, shape.num_layers, device=gpu) if dt in FP8 else None
     dst = np.random.default_rng(2).permutation(wl.num_blocks)[:wl.n_pages].astype(np.int32)
     one = [torch.zeros_like(c) for c in src]
     ops.scatter_rerotate(ops.LayerTable(one), dst, wl.slot_offsets, st, tabs, ridx, k_scale=ks)
@@ -312,7 +314,7 @@ def test_device_tables_out_of_range_skipped(gpu):
 def _rerotate_case(gpu, dt, style, head_dim, rot_dim, heads=4, layers=3, seed=0,
                    deltas=(0, 1, 517, 32767, 123), theta=500000.0, scale=1.0,
                    inputs=None):
-    shape = KVShape(layers, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    shape = KVShape(layers, heads, head_dim, 16, 1 if dt in FP8 else 2)
     rng = np.random.default_rng(seed)
     chunk_pages = [int(x) for x in rng.integers(1, 4, size=len(deltas))]
     n = sum(chunk_pages)
@@ -329,7 +331,7 @@ def _rerotate_case(gpu, dt, style, head_dim, rot_dim, heads=4, layers=3, seed=0,
     tabs = position.delta_tables(uniq or [0], rot_dim, theta, device=gpu)
     k_scale = None
     ks_np = None
-    if dt == "e4m3":
+    if dt in FP8:
         ks_np = (rng.random(layers).astype(np.float32) * 0.5 + 0.01)
         k_scale = torch.from_numpy(ks_np).to(gpu)
     ops.scatter_rerotate(ops.LayerTable(dst), page_ids, offs, staging, tabs, ridx,
@@ -384,6 +386,10 @@ def _exact_rotation(staging, offsets, shape, layer, page_delta, rot_dim, style, 
         ("fp16", "gptj", 256, 128),
         ("e4m3", "neox", 128, 128),
         ("e4m3", "gptj", 128, 96),
+        ("e5m2", "neox", 128, 128),
+        ("e5m2", "gptj", 128, 96),
+        ("e5m2", "neox", 192, 192),
+        ("e5m2", "neox", 128, 40),
         # partner distance not a power of two: the row-aligned kernel
         ("bf16", "neox", 80, 80),
         ("fp16", "neox", 96, 96),
@@ -401,7 +407,7 @@ def test_rerotate_matches_oracle(gpu, dt, style, head_dim, rot_dim):
     print(f"case: rerotate {dt} {style} D{head_dim} R{rot_dim}", flush=True)
     inputs = {}
     shape, dst, dst_ref, page_ids, page_delta = _rerotate_case(
-        gpu, dt, style, head_dim, rot_dim, scale=40.0 if dt == "e4m3" else 1.0, inputs=inputs)
+        gpu, dt, style, head_dim, rot_dim, scale=40.0 if dt in FP8 else 1.0, inputs=inputs)
     for l in range(shape.num_layers):
         got = to_bits_np(dst[l], dt)
         ref = dst_ref[l]
@@ -433,7 +439,7 @@ def test_rerotate_pair_task_kernel_matches_oracle(gpu, tuning, dt, head_dim):
     print(f"case: rerotate pair-task {dt} D{head_dim}", flush=True)
     tuning("rot_kernel", "pairs")
     shape, dst, dst_ref, page_ids, page_delta = _rerotate_case(
-        gpu, dt, "neox", head_dim, head_dim, scale=40.0 if dt == "e4m3" else 1.0)
+        gpu, dt, "neox", head_dim, head_dim, scale=40.0 if dt in FP8 else 1.0)
     for l in range(shape.num_layers):
         got = to_bits_np(dst[l], dt)
         assert np.array_equal(got[1], dst_ref[l][1])
@@ -448,7 +454,7 @@ def test_rerotate_single_kv_head(gpu, dt):
     print(f"case: rerotate single head {dt}", flush=True)
     shape, dst, dst_ref, page_ids, page_delta = _rerotate_case(
         gpu, dt, "neox", 128, 128, heads=1, layers=5, seed=9,
-        scale=40.0 if dt == "e4m3" else 1.0)
+        scale=40.0 if dt in FP8 else 1.0)
     for l in range(shape.num_layers):
         got = to_bits_np(dst[l], dt)
         assert np.array_equal(got[1], dst_ref[l][1])
@@ -492,14 +498,15 @@ def test_rerotate_bad_geometry_rejected(gpu):
                              k_scale=torch.ones(1, device=gpu))
 
 
-@pytest.mark.parametrize("dt", ["bf16", "e4m3"])
+@pytest.mark.parametrize("dt", ["bf16", "e4m3", "e5m2"])
 def test_rerotate_special_values(gpu, dt):
-    """NaN, +-Inf (bf16), +-0, subnormals and the e4m3 extremes follow the
-    oracle: NaN stays canonical NaN, zero delta is bit-exact, e4m3 saturates."""
+    """NaN, +-Inf (bf16, e5m2), +-0, subnormals and the 8-bit extremes follow
+    the oracle: NaN stays canonical NaN, zero delta is bit-exact (infinities
+    included), the 8-bit formats saturate."""
     print(f"case: rerotate special values {dt}", flush=True)
-    shape = KVShape(2, 2, 64, 16, 1 if dt == "e4m3" else 2)
+    shape = KVShape(2, 2, 64, 16, 1 if dt in FP8 else 2)
     nb = 4
-    caches = rand_caches(shape, nb, dt, gpu, seed=40, scale=30.0 if dt == "e4m3" else 1.0)
+    caches = rand_caches(shape, nb, dt, gpu, seed=40, scale=30.0 if dt in FP8 else 1.0)
     if dt == "bf16":
         special = torch.tensor([float("nan"), float("inf"), -float("inf"), 0.0, -0.0,
                                 1e-40, -3e-39, 65504.0], dtype=torch.float32).to(torch.bfloat16)
@@ -509,7 +516,9 @@ def test_rerotate_special_values(gpu, dt):
             v[0, :, 0, 0, :8] = bits.to(gpu)          # first-half elements
             v[0, :, 1, 1, 32:40] = bits.to(gpu)       # their neox partners
     else:
-        codes = torch.tensor([0x7F, 0xFF, 0x00, 0x80, 0x01, 0x81, 0x7E, 0xFE], dtype=torch.uint8)
+        codes = torch.tensor([0x7F, 0xFF, 0x00, 0x80, 0x01, 0x81, 0x7E, 0xFE] if dt == "e4m3"
+                             else [0x7F, 0xFD, 0x00, 0x80, 0x01, 0x7C, 0xFC, 0x7B],
+                             dtype=torch.uint8)
         for c in caches:
             v = c.view(torch.uint8)
             v[0, :, 0, 0, :8] = codes.to(gpu)
@@ -522,7 +531,7 @@ def test_rerotate_special_values(gpu, dt):
     deltas = [0, 1, 777, 32767]
     ridx, uniq = position.page_rope_index([1] * nb, deltas)
     tabs = position.delta_tables(uniq, 64, 500000.0, device=gpu)
-    ks = torch.tensor([0.5, 2.0], device=gpu) if dt == "e4m3" else None
+    ks = torch.tensor([0.5, 2.0], device=gpu) if dt in FP8 else None
     ops.scatter_rerotate(ops.LayerTable(dst), ids, offs, st, tabs, ridx, k_scale=ks)
     ref = [np.zeros_like(to_bits_np(c, dt)) for c in caches]
     oracle.scatter_rerotate(ref, ids, offs, st.cpu().numpy(), shape.layer_bytes,
@@ -664,9 +673,9 @@ def test_grouped_units_match_oracle(gpu, tuning, layers, heads, head_dim, dt, gr
         tuning("units_per_group", int(group_cap))
     else:
         tuning("units_per_group", 0)
-    shape = KVShape(layers, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    shape = KVShape(layers, heads, head_dim, 16, 1 if dt in FP8 else 2)
     nb = 9
-    src = rand_caches(shape, nb, dt, gpu, seed=60, scale=40.0 if dt == "e4m3" else 1.0)
+    src = rand_caches(shape, nb, dt, gpu, seed=60, scale=40.0 if dt in FP8 else 1.0)
     ids = np.array([5, 0, 7], dtype=np.int32)
     offs = np.array([2, 0, 1], dtype=np.int64) * shape.slot_bytes
     staging = torch.zeros(3 * shape.slot_bytes, dtype=torch.uint8, device=gpu)
@@ -691,7 +700,7 @@ def test_grouped_units_match_oracle(gpu, tuning, layers, heads, head_dim, dt, gr
     tabs = position.delta_tables(uniq, head_dim, 500000.0, device=gpu)
     ks_np = None
     k_scale = None
-    if dt == "e4m3":
+    if dt in FP8:
         ks_np = np.linspace(0.05, 0.5, layers).astype(np.float32)
         k_scale = torch.from_numpy(ks_np).to(gpu)
     rot = [torch.zeros_like(c) for c in src]
@@ -760,12 +769,12 @@ def test_launch_split_matches_single_launch(gpu, tuning, layers, heads, head_dim
     launches over page (token) ranges; forced here with a limit of 16
     workgroups, every entry point writes the same bytes as one launch."""
     print(f"case: launch split L{layers} H{heads} {dt}", flush=True)
-    shape = KVShape(layers, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    shape = KVShape(layers, heads, head_dim, 16, 1 if dt in FP8 else 2)
     wl = workloads.ragged(shape, 6, 40, 700, seed=12, num_blocks=256)
-    src = rand_caches(shape, wl.num_blocks, dt, gpu, seed=70, scale=40.0 if dt == "e4m3" else 1.0)
+    src = rand_caches(shape, wl.num_blocks, dt, gpu, seed=70, scale=40.0 if dt in FP8 else 1.0)
     ridx = np.arange(wl.n_pages, dtype=np.int32) % 3 - 1  # -1 (copy), 0, 1
     tabs = position.delta_tables([517, 32767], head_dim, 500000.0, device=gpu)
-    ks = torch.linspace(0.05, 0.5, layers, device=gpu) if dt == "e4m3" else None
+    ks = torch.linspace(0.05, 0.5, layers, device=gpu) if dt in FP8 else None
     tables, k = [], 0
     for n in wl.req_pages:
         tables.append(wl.page_ids[k:k + n].tolist())
@@ -862,8 +871,8 @@ def _random_cases(n, seed):
     rng = np.random.default_rng(seed)
     cases = []
     while len(cases) < n:
-        dt = ["bf16", "fp16", "e4m3"][rng.integers(3)]
-        e = 1 if dt == "e4m3" else 2
+        dt = ["bf16", "fp16", "e4m3", "e5m2"][rng.integers(4)]
+        e = 1 if dt in FP8 else 2
         ve = 16 if e == 1 else 8
         D = int(rng.choice([64, 80, 96, 128, 192, 256]))
         H = int(rng.choice([1, 2, 3, 4, 8]))
@@ -890,11 +899,11 @@ def test_random_geometry_parity(gpu, dt, D, H, bs, style, R, L, seed):
     partial rotary, gptj) through gather, scatter and re-rotation, against
     the oracle."""
     print(f"case: random {dt} D{D} H{H} bs{bs} {style} R{R} L{L} seed{seed}", flush=True)
-    shape = KVShape(L, H, D, bs, 1 if dt == "e4m3" else 2)
+    shape = KVShape(L, H, D, bs, 1 if dt in FP8 else 2)
     rng = np.random.default_rng(seed)
     nb = int(rng.integers(8, 40))
     n = int(rng.integers(1, nb))
-    src = rand_caches(shape, nb, dt, gpu, seed=seed % 1000, scale=40.0 if dt == "e4m3" else 1.0)
+    src = rand_caches(shape, nb, dt, gpu, seed=seed % 1000, scale=40.0 if dt in FP8 else 1.0)
     ids = rng.permutation(nb)[:n].astype(np.int32)
     offs = rng.permutation(n).astype(np.int64) * shape.slot_bytes
     st = torch.zeros(n * shape.slot_bytes, dtype=torch.uint8, device=gpu)
@@ -908,7 +917,7 @@ def test_random_geometry_parity(gpu, dt, D, H, bs, style, R, L, seed):
     deltas = rng.integers(-4000, 32768, size=n) * (rng.random(n) < 0.8)
     ridx, uniq = position.page_rope_index([1] * n, deltas)
     tabs = position.delta_tables(uniq or [0], R, 500000.0, device=gpu)
-    ks_np = (rng.random(L).astype(np.float32) * 0.5 + 0.01) if dt == "e4m3" else None
+    ks_np = (rng.random(L).astype(np.float32) * 0.5 + 0.01) if dt in FP8 else None
     ks = torch.from_numpy(ks_np).to(gpu) if ks_np is not None else None
     dst = [torch.zeros_like(c) for c in src]
     ops.scatter(ops.LayerTable(dst), dst_ids, offs, st)
@@ -982,7 +991,7 @@ def test_random_geometry_slots_parity(gpu, dt, D, H, bs, style, R, L, seed):
     """Token-granular gather / scatter on random geometries and random
     slot mappings (ragged requests, partial pages, padding) vs the oracle."""
     print(f"case: random slots {dt} D{D} H{H} bs{bs} L{L} seed{seed}", flush=True)
-    shape = KVShape(L, H, D, bs, 1 if dt == "e4m3" else 2)
+    shape = KVShape(L, H, D, bs, 1 if dt in FP8 else 2)
     rng = np.random.default_rng(seed)
     nb = int(rng.integers(16, 64))
     toks = [int(x) for x in rng.integers(1, 6 * bs, size=int(rng.integers(1, 5)))]
@@ -1021,7 +1030,7 @@ def test_shared_records_hint_does_not_change_results(gpu, heads, head_dim, dt):
     reading the same records give the same bits with and without it (token-
     major and split-x pages), and match the oracle."""
     print(f"case: shared-records hint H{heads} D{head_dim} {dt}", flush=True)
-    shape = KVShape(3, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    shape = KVShape(3, heads, head_dim, 16, 1 if dt in FP8 else 2)
     rng = np.random.default_rng(4)
     n_src, n = 3, 12
     nb = n + 4
@@ -1032,7 +1041,7 @@ def test_shared_records_hint_does_not_change_results(gpu, heads, head_dim, dt):
     page_ids = rng.permutation(nb)[:n].astype(np.int32)
     ridx = (np.arange(n) % 2).astype(np.int32)
     tabs = position.delta_tables([77, 30001], head_dim, 500000.0, device=gpu)
-    ks = torch.full((3,), 0.05, dtype=torch.float32, device=gpu) if dt == "e4m3" else None
+    ks = torch.full((3,), 0.05, dtype=torch.float32, device=gpu) if dt in FP8 else None
     outs = []
     for flat in (False, True):
         for hint in (False, True):
@@ -1082,6 +1091,8 @@ def test_rerotate_contig_override_on_small_pages(gpu, tuning, heads, head_dim, d
     (8, 128, "bf16", None),    # grouped kernel, one unit per workgroup
     (1, 128, "bf16", None),    # grouped, several units per workgroup
     (8, 128, "e4m3", None),    # contig kernel
+    (8, 128, "e5m2", None),    # contig kernel, e5m2
+    (1, 128, "e5m2", None),    # grouped, e5m2
     (4, 96, "bf16", None),     # row-aligned kernel
     (4, 96, "bf16", "pairs"),  # pair-task kernel
     (16, 128, "bf16", None),   # 64 KiB pages: contig kernel in rounds
@@ -1100,17 +1111,17 @@ def test_rerotate_per_layer_groups(gpu, tuning, heads, head_dim, dt, kernel):
     L = 6
     groups = np.array([0, 1, -1, 0, 1, -1], np.int32)
     thetas = [10000.0, 1000000.0]
-    shape = KVShape(L, heads, head_dim, 16, 1 if dt == "e4m3" else 2)
+    shape = KVShape(L, heads, head_dim, 16, 1 if dt in FP8 else 2)
     rng = np.random.default_rng(heads * 1000 + head_dim)
     nb, n = 24, 10
-    src = rand_caches(shape, nb, dt, gpu, seed=91, scale=40.0 if dt == "e4m3" else 1.0)
+    src = rand_caches(shape, nb, dt, gpu, seed=91, scale=40.0 if dt in FP8 else 1.0)
     st = torch.zeros(n * shape.slot_bytes, dtype=torch.uint8, device=gpu)
     offs = np.arange(n, dtype=np.int64) * shape.slot_bytes
     ops.gather(ops.LayerTable(src), rng.permutation(nb)[:n].astype(np.int32), offs, st)
     deltas = rng.integers(1, 32768, size=n) * (np.arange(n) % 4 != 0)  # some pages unmoved
     ridx, uniq = position.page_rope_index([1] * n, deltas)
     tabs = torch.stack([position.delta_tables(uniq, rot, t, device=gpu) for t in thetas])
-    ks_np = (rng.random(L).astype(np.float32) * 0.5 + 0.01) if dt == "e4m3" else None
+    ks_np = (rng.random(L).astype(np.float32) * 0.5 + 0.01) if dt in FP8 else None
     ks = torch.from_numpy(ks_np).to(gpu) if ks_np is not None else None
     dst_ids = rng.permutation(nb)[:n].astype(np.int32)
     out = [torch.zeros_like(c) for c in src]
@@ -1217,6 +1228,7 @@ def test_flat_cache_copies_bit_exact(gpu):
     ("fp16", "neox", 8, 128, 128),
     ("e4m3", "neox", 2, 128, 128),
     ("e4m3", "gptj", 1, 128, 96),
+    ("e5m2", "neox", 2, 128, 128),
     ("bf16", "neox", 3, 96, 96),     # 12-vector columns: the pair-task kernel
 ])
 @pytest.mark.parametrize("kernel", ["auto", "pairs"])
@@ -1231,7 +1243,7 @@ def test_rerotate_kx_layout_matches_oracle(gpu, tuning, dt, style, heads, head_d
     if kernel == "pairs":
         tuning("rot_kernel", "pairs")
     bs, L = 16, 3
-    shape = KVShape(L, heads, head_dim, bs, 1 if dt == "e4m3" else 2)
+    shape = KVShape(L, heads, head_dim, bs, 1 if dt in FP8 else 2)
     rng = np.random.default_rng(17)
     deltas = (0, 5, 4097, 32767)
     chunk_pages = [2, 1, 3, 2]
@@ -1249,7 +1261,7 @@ def test_rerotate_kx_layout_matches_oracle(gpu, tuning, dt, style, heads, head_d
     ridx, uniq = position.page_rope_index(chunk_pages, deltas)
     tabs = position.delta_tables(uniq, rot_dim, 500000.0, device=gpu)
     ks_np = k_scale = None
-    if dt == "e4m3":
+    if dt in FP8:
         ks_np = rng.random(L).astype(np.float32) * 0.5 + 0.01
         k_scale = torch.from_numpy(ks_np).to(gpu)
     table = ops.LayerTable(dst, **geo)
@@ -1259,7 +1271,7 @@ def test_rerotate_kx_layout_matches_oracle(gpu, tuning, dt, style, heads, head_d
     # oracle in token-major order: permute caches and records, rotate, compare
     to_nhd = lambda a: oracle.kx_to_nhd(a, bs, heads, head_dim)  # noqa: E731
     ref = [np.ascontiguousarray(to_nhd(b)) for b in before]
-    el = np.uint8 if dt == "e4m3" else np.uint16
+    el = np.uint8 if dt in FP8 else np.uint16
     recs = staging.cpu().numpy().view(el).reshape(n, L, 2, -1)
     recs_nhd = np.ascontiguousarray(to_nhd(recs)).reshape(-1).view(np.uint8)
     page_delta = np.repeat(np.asarray(deltas, np.int64), chunk_pages)
@@ -1306,7 +1318,7 @@ def test_hnd_copies_match_oracle(gpu, heads, head_dim, bs, dt):
     """Gather from head-major pages writes the records of the logical page
     (the reference's reshape(-1) of kv[:, b]); scatter writes them back."""
     print(f"case: hnd copies H{heads} D{head_dim} bs{bs} {dt}", flush=True)
-    shape = KVShape(3, heads, head_dim, bs, 1 if dt == "e4m3" else 2)
+    shape = KVShape(3, heads, head_dim, bs, 1 if dt in FP8 else 2)
     wl = workloads.ragged(shape, 4, 1, 200, seed=5, pool_slack=1.5)
     caches = _hnd_caches(shape, wl.num_blocks, dt, gpu, seed=70)
     table = ops.LayerTable(caches)
@@ -1342,6 +1354,7 @@ def test_hnd_copies_match_oracle(gpu, heads, head_dim, bs, dt):
     (8, 128, 128, "bf16", "neox"), (2, 64, 64, "bf16", "neox"), (4, 128, 128, "e4m3", "neox"),
     (2, 128, 128, "bf16", "gptj"), (4, 128, 64, "bf16", "neox"),
     (2, 128, 128, "e4m3", "neox"),  # 4 KiB e4m3 pages: grouped
+    (4, 128, 128, "e5m2", "gptj"),
     (2, 32, 32, "bf16", "neox"),    # 2 KiB pages: grouped, 16 units per workgroup
     (16, 128, 128, "bf16", "neox"),  # 64 KiB pages: contig in rounds
 ])
@@ -1368,7 +1381,7 @@ def test_hnd_rerotate_equals_token_major(gpu, heads, head_dim, rot, dt, style):
     ridx, uniq = position.page_rope_index(chunk_pages, (0, 1, 517, 32767, 123))
     tabs = position.delta_tables(uniq, rot, 500000.0, device=gpu)
     ks = None
-    if dt == "e4m3":
+    if dt in FP8:
         ks = torch.from_numpy(rng.random(3).astype(np.float32) * 0.5 + 0.01).to(gpu)
     ops.scatter_rerotate(ops.LayerTable(hnd), ids, offs, staging, tabs, ridx, rot_dim=rot,
                          style=style, k_scale=ks)

@@ -17,7 +17,7 @@ from daser_amd import ops, position
 from daser_amd.workloads import KVShape
 from oracle import oracle
 
-BF16, FP16, E4M3 = oracle.BF16, oracle.FP16, oracle.E4M3
+BF16, FP16, E4M3, E5M2 = oracle.BF16, oracle.FP16, oracle.E4M3, oracle.E5M2
 
 
 # ---------------------------------------------------------------------------
@@ -168,6 +168,38 @@ def test_e4m3_encode_saturates_and_keeps_nan():
     assert list(out) == [0x7E, 0x7E, 0xFE, 0x7E, 0xFE, 0x7F]
 
 
+def test_e5m2_decode_all_codes():
+    codes = np.arange(256, dtype=np.uint32)
+    ours = oracle.decode(oracle.E5M2, codes)
+    ref = torch.from_numpy(codes.astype(np.uint8)).view(torch.float8_e5m2).double().numpy()
+    assert np.array_equal(np.isnan(ours), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(ours[ok], ref[ok])
+    assert np.isnan(ours).sum() == 6 and ours[0x7C] == np.inf and ours[0xFC] == -np.inf
+    assert ours[0x7B] == 57344.0 and ours[0x01] == 2.0 ** -16
+
+
+def test_e5m2_encode_matches_torch_rne():
+    rng = np.random.default_rng(13)
+    v = _fp32_sweep(rng, 20000, 2.0 ** -18, 57344.0)
+    codes = np.arange(0, 0x7C, dtype=np.uint32)  # every finite positive code
+    a = oracle.decode(oracle.E5M2, codes)
+    mid = ((a[:-1] + a[1:]) / 2).astype(np.float32)  # exact ties, subnormals included
+    v = np.concatenate([v, mid, -mid, np.float32([0.0, -0.0, 57344.0, -57344.0, 60000.0])])
+    ours = oracle.encode(oracle.E5M2, v.astype(np.float64)).astype(np.uint8)
+    ref = torch.from_numpy(v).to(torch.float8_e5m2).view(torch.uint8).numpy()
+    assert np.array_equal(ours, ref)
+
+
+def test_e5m2_encode_saturates_and_keeps_nan():
+    """Beyond the largest finite value torch's conversion gives infinity;
+    the oracle (and the kernels) saturate, as the 8-bit KV cache writes do,
+    and keep NaN as torch's 0x7F."""
+    out = oracle.encode(oracle.E5M2, [61440.0, 1e30, -70000.0, np.inf, -np.inf, np.nan])
+    assert list(out) == [0x7B, 0x7B, 0xFB, 0x7B, 0xFB, 0x7F]
+    assert torch.tensor([np.nan]).to(torch.float8_e5m2).view(torch.uint8).item() == 0x7F
+
+
 @pytest.mark.parametrize("dt,tdt", [(BF16, torch.bfloat16), (FP16, torch.float16)])
 def test_16bit_codecs_match_torch(dt, tdt):
     codes = np.arange(65536, dtype=np.uint32)
@@ -202,7 +234,8 @@ def _rot_case(dt, L=2, H=3, D=16, nb=6, scale=1.0, seed=5):
     if dt == FP16:
         bits = torch.from_numpy(vals.astype(np.float32)).to(torch.float16).view(torch.int16)
         return [bits.numpy().view(np.uint16).copy() for _ in range(L)]
-    bits = torch.from_numpy(vals.astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8)
+    tdt = torch.float8_e4m3fn if dt == E4M3 else torch.float8_e5m2
+    bits = torch.from_numpy(vals.astype(np.float32)).to(tdt).view(torch.uint8)
     return [bits.numpy().copy() for _ in range(L)]
 
 
@@ -227,10 +260,10 @@ def _rerotate(caches, ids, dt, stored, new, rot_dim=None, style=oracle.NEOX,
 
 
 def test_zero_delta_is_bit_exact_copy():
-    for dt in (BF16, FP16, E4M3):
+    for dt in (BF16, FP16, E4M3, E5M2):
         c = _rot_case(dt, scale=3.0)
         out = _rerotate(c, [1, 4], dt, stored=777, new=777,
-                        k_scale=np.float32([0.7, 1.3]) if dt == E4M3 else None)
+                        k_scale=np.float32([0.7, 1.3]) if dt in (E4M3, E5M2) else None)
         for a, b in zip(out, c):
             assert np.array_equal(a[:, [1, 4]], b[:, [1, 4]])
 
@@ -311,16 +344,17 @@ def test_partial_rotary_copies_tail():
     assert np.array_equal(out[0][0, 1, ..., :16], full[0][0, 1])
 
 
-def test_fp8_dequant_rotate_requant():
-    c = _rot_case(E4M3, D=16, scale=40.0, seed=13)
+@pytest.mark.parametrize("dt", [E4M3, E5M2])
+def test_fp8_dequant_rotate_requant(dt):
+    c = _rot_case(dt, D=16, scale=40.0, seed=13)
     ks = np.float32([0.25, 3.0])
-    out = _rerotate(c, [0, 2], E4M3, stored=0, new=2024, k_scale=ks, theta=500000.0)
+    out = _rerotate(c, [0, 2], dt, stored=0, new=2024, k_scale=ks, theta=500000.0)
     for l in range(2):
-        x = oracle.decode(E4M3, c[l][0, [0, 2]]) * float(ks[l])
+        x = oracle.decode(dt, c[l][0, [0, 2]]) * float(ks[l])
         z = x[..., :8] + 1j * x[..., 8:]
         w = 500000.0 ** (-2.0 * np.arange(8) / 16)
         zr = z * np.exp(1j * 2024 * w) / float(ks[l])
-        exp = oracle.encode(E4M3, np.concatenate([zr.real, zr.imag], axis=-1))
+        exp = oracle.encode(dt, np.concatenate([zr.real, zr.imag], axis=-1))
         assert np.array_equal(out[l][0, [0, 2]], exp.astype(np.uint8))
 
 
