@@ -29,6 +29,10 @@ def _e4m3_bits(x: np.ndarray) -> np.ndarray:
     return torch.from_numpy(x.astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
 
 
+def _e5m2_bits(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(x.astype(np.float32)).to(torch.float8_e5m2).view(torch.uint8).numpy()
+
+
 def gather_scatter_case():
     rng = np.random.default_rng(100)
     L, nb, bs, H, D = 2, 8, 16, 2, 64
@@ -50,11 +54,12 @@ def gather_scatter_case():
 def rerotate_case(name, dt, style, rot_dim):
     rng = np.random.default_rng(200 + dt * 10 + style)
     L, nb, bs, H, D = 2, 6, 16, 2, 64
+    fp8 = {oracle.E4M3: _e4m3_bits, oracle.E5M2: _e5m2_bits}.get(dt)
     if dt == oracle.BF16:
         src = np.stack([_bf16_bits(rng.normal(size=(2, nb, bs, H, D))) for _ in range(L)])
         k_scale = np.ones(L, np.float32)
     else:
-        src = np.stack([_e4m3_bits(rng.normal(size=(2, nb, bs, H, D)) * 50) for _ in range(L)])
+        src = np.stack([fp8(rng.normal(size=(2, nb, bs, H, D)) * 50) for _ in range(L)])
         k_scale = np.float32([0.125, 2.5])
     esz = src.dtype.itemsize
     layer_bytes = 2 * bs * H * D * esz
@@ -64,7 +69,7 @@ def rerotate_case(name, dt, style, rot_dim):
     stg = np.zeros(4 * slot, dtype=np.uint8)
     oracle.gather(list(src), rec_ids, offs, stg, layer_bytes)
     dst0 = np.stack([_bf16_bits(rng.normal(size=(2, nb, bs, H, D))) if dt == oracle.BF16
-                     else _e4m3_bits(rng.normal(size=(2, nb, bs, H, D))) for _ in range(L)])
+                     else fp8(rng.normal(size=(2, nb, bs, H, D))) for _ in range(L)])
     page_ids = np.array([5, 0, 3, 1], dtype=np.int32)
     deltas = np.array([0, 1, 4097, 32767], dtype=np.int64)
     out = [c.copy() for c in dst0]
@@ -82,4 +87,5 @@ if __name__ == "__main__":
     rerotate_case("rerotate_bf16_neox.npz", oracle.BF16, oracle.NEOX, 64)
     rerotate_case("rerotate_bf16_gptj_partial.npz", oracle.BF16, oracle.GPTJ, 32)
     rerotate_case("rerotate_e4m3_neox.npz", oracle.E4M3, oracle.NEOX, 64)
+    rerotate_case("rerotate_e5m2_gptj.npz", oracle.E5M2, oracle.GPTJ, 64)
     print("golden vectors written to", HERE)

@@ -46,7 +46,9 @@ def test_oracle_reproduces_rerotate_vectors(name):
     assert np.array_equal(np.stack(out), g["expected"])
 
 
-_TDT = {oracle.BF16: torch.bfloat16, oracle.E4M3: torch.float8_e4m3fn}
+_TDT = {oracle.BF16: torch.bfloat16, oracle.E4M3: torch.float8_e4m3fn,
+        oracle.E5M2: torch.float8_e5m2}
+_FP8 = (oracle.E4M3, oracle.E5M2)
 
 
 def _to_device(bits: np.ndarray, tdt, dev):
@@ -84,14 +86,14 @@ def test_kernel_reproduces_rerotate_vectors(gpu, name):
     stg = torch.from_numpy(g["staging"]).to(gpu)
     ridx, uniq = position.page_rope_index([1] * g["page_ids"].size, g["deltas"])
     tabs = position.delta_tables(uniq, int(g["rot_dim"]), float(g["theta"]), device=gpu)
-    ks = torch.from_numpy(g["k_scale"]).to(gpu) if dt == oracle.E4M3 else None
+    ks = torch.from_numpy(g["k_scale"]).to(gpu) if dt in _FP8 else None
     ops.scatter_rerotate(ops.LayerTable(dst), g["page_ids"], g["slot_offsets"], stg, tabs, ridx,
                          rot_dim=int(g["rot_dim"]),
                          style="neox" if int(g["style"]) == oracle.NEOX else "gptj", k_scale=ks)
     torch.cuda.synchronize()
     for l, d in enumerate(dst):
-        bits = d.view(torch.int16 if dt != oracle.E4M3 else torch.uint8).cpu().numpy()
-        bits = bits.view(np.uint16) if dt != oracle.E4M3 else bits
+        bits = d.view(torch.uint8 if dt in _FP8 else torch.int16).cpu().numpy()
+        bits = bits if dt in _FP8 else bits.view(np.uint16)
         exp = g["expected"][l]
         assert np.array_equal(bits[1], exp[1])
         ok, msg = oracle.rotation_within_tolerance(bits[0], exp[0], dt)
