@@ -165,12 +165,30 @@ def bench_copy(torch, ops, wl, dtype, dev, steps, warmup, position=None):
                 ops.gather_slots(table, sm, ro, staging)
             with tss:
                 ops.scatter_slots(table, sm_s, ro_s, staging)
+        # the token-form load with every request re-rotated (a delta each)
+        from daser_amd import position as _position
+
+        rng = np.random.default_rng(11)
+        deltas = rng.integers(1, 32768, size=len(wl.req_tokens)).tolist()
+        req_idx, uniq = _position.page_rope_index([1] * len(deltas), deltas)
+        tabs = _position.delta_tables(uniq, shape.head_dim, THETA, device=dev)
+        tok_idx = np.repeat(np.asarray(req_idx, np.int64), wl.req_tokens)[order]
+        ridx_s = torch.from_numpy(tok_idx.astype(np.int32)).to(dev)
+        tsr = Timer(torch)
+        for i in range(warmup + steps):
+            if i < warmup:
+                ops.scatter_slots_rerotate(table, sm_s, ro_s, staging, tabs, ridx_s)
+                continue
+            with tsr:
+                ops.scatter_slots_rerotate(table, sm_s, ro_s, staging, tabs, ridx_s)
         torch.cuda.synchronize()
         tokP = wl.tokens * row * 2 * shape.num_layers
         rot = {"slots_gather_ms": tsg.mean_ms(), "slots_scatter_ms": tss.mean_ms(),
+               "slots_rerotate_ms": tsr.mean_ms(),
                "slots_payload_bytes": tokP,
                "slots_gather_GBps": 2 * tokP / (tsg.mean_ms() * 1e-3) / 1e9,
-               "slots_scatter_GBps": 2 * tokP / (tss.mean_ms() * 1e-3) / 1e9}
+               "slots_scatter_GBps": 2 * tokP / (tss.mean_ms() * 1e-3) / 1e9,
+               "slots_rerotate_GBps": 2 * tokP / (tsr.mean_ms() * 1e-3) / 1e9}
     if dtype == "fp8" and position is not None:
         rng = np.random.default_rng(7)
         deltas = rng.integers(1, 32768, size=len(wl.req_pages)).tolist()
@@ -931,6 +949,9 @@ def main() -> int:
         out["kernels"]["scatter_slots"] = {
             "ms": round(r["slots_scatter_ms"], 4), "GBps": round(r["slots_scatter_GBps"], 1),
             "frac": round(r["slots_scatter_GBps"] / HBM_PEAK_GBS, 4)}
+        out["kernels"]["scatter_slots_rerotate"] = {
+            "ms": round(r["slots_rerotate_ms"], 4), "GBps": round(r["slots_rerotate_GBps"], 1),
+            "frac": round(r["slots_rerotate_GBps"] / HBM_PEAK_GBS, 4)}
         out["check"] = {"round_trip_probe": r["probe_ok"]}
     for c in (3, 5, 6):
         if c in res:

@@ -20,7 +20,7 @@ LIB_PATH = os.environ.get("DASER_KV_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so"
 )
 
-DSR_ABI_VERSION = 7
+DSR_ABI_VERSION = 8
 DSR_OK = 0
 DSR_ERR_ARG = -1
 DSR_ERR_ALIGN = -2
@@ -65,6 +65,8 @@ SIGNATURES = {
     "dsr_scatter_ex": (_COPY_ARGS[:-1] + [ctypes.c_uint, _P], _I),
     "dsr_gather_slots": (_SLOT_ARGS, _I),
     "dsr_scatter_slots": (_SLOT_ARGS, _I),
+    "dsr_scatter_slots_rerotate": (
+        _SLOT_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P], _I),
     "dsr_ring_open": ([ctypes.c_char_p, _I64, _I, _I, ctypes.POINTER(_P)], _I),
     "dsr_ring_write": ([_P, _P, _I64, _I64, _P], _I),
     "dsr_ring_read": ([_P, _P, _I64, _I64, _P], _I),

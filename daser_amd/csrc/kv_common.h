@@ -14,6 +14,7 @@
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;     // 4 wave64 per workgroup
 constexpr int kWave = 64;
@@ -139,6 +140,10 @@ __device__ __forceinline__ rsrc_t make_rsrc(const uint8_t* p, int64_t bytes) {
 }
 __device__ __forceinline__ u32x4 bload(rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kLoadPolicy);
+}
+// 8-byte load with the default (cached) policy, for small shared tables
+__device__ __forceinline__ u32x2 bload_b64(rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
 }
 __device__ __forceinline__ void bstore(rsrc_t r, int off, u32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kStorePolicy);

@@ -723,6 +723,8 @@ int dsr_scatter_hnd(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
                   layer_bytes, layer0, block_size, num_heads, stream);
 }
 
+}  // extern "C"
+
 namespace {
 
 int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t kv_stride,
@@ -823,7 +825,108 @@ int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t 
   return DSR_OK;
 }
 
+// Token-form scatter with re-rotation: argument checks, then
+// kv_slots_rerotate_kernel over token ranges that fit one launch each.
+int slots_rerotate_launch(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                          int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                          int block_size, int64_t row_bytes, const int64_t* slot_mapping,
+                          const int64_t* row_offsets, int n_tokens, const void* staging,
+                          int64_t staging_bytes, int64_t layer_bytes, int layer0,
+                          const float* cos_sin, const int32_t* rope_idx, int n_tables,
+                          const int32_t* layer_group, int n_groups, int head_dim, int rot_dim,
+                          int rope_style, int dtype, const float* k_scale, dsr_stream_t stream) {
+  if (n_tokens < 0 || n_layers < 0 || layer0 < 0 || num_blocks < 0 || staging_bytes < 0 ||
+      block_size <= 0 || row_bytes <= 0 || page_bytes <= 0 || n_tables < 0 ||
+      (layer_group && n_groups < 1))
+    return DSR_ERR_ARG;
+  if (rope_style != DSR_ROPE_NEOX && rope_style != DSR_ROPE_GPTJ) return DSR_ERR_ARG;
+  const int esize = dtype == DSR_DTYPE_BF16 || dtype == DSR_DTYPE_FP16 ? 2
+                    : dtype == DSR_DTYPE_FP8_E4M3 || dtype == DSR_DTYPE_FP8_E5M2 ? 1 : 0;
+  if (!esize) return DSR_ERR_ARG;
+  if (n_tokens == 0 || n_layers == 0) return DSR_OK;
+  if (!layer_base || !slot_mapping || !row_offsets || !staging || !rope_idx ||
+      (n_tables > 0 && !cos_sin) || (esize == 1 && !k_scale))
+    return DSR_ERR_ARG;
+  // heads of a power-of-two number of vectors <= 64, rotary width in whole
+  // vectors (both halves for neox), at most 256 rotated dims
+  const int64_t head_bytes = (int64_t)head_dim * esize;
+  const int ve = 16 / esize;
+  const int hv = (int)(head_bytes / 16);
+  if (head_dim <= 0 || rot_dim <= 0 || rot_dim > head_dim || rot_dim % 2 ||
+      head_bytes % 16 || row_bytes % head_bytes || hv > kWave || (hv & (hv - 1)) ||
+      rot_dim / 2 > kSlotRotMaxHalf ||
+      (rope_style == DSR_ROPE_NEOX ? (rot_dim / 2) % ve : rot_dim % ve))
+    return DSR_ERR_SHAPE;
+  if (page_bytes < (int64_t)block_size * row_bytes || layer_bytes < 2 * page_bytes ||
+      row_bytes > 0x7fffffffLL)
+    return DSR_ERR_SHAPE;
+  if (!aligned16(kv_stride) || !aligned16(page_stride) || !aligned16(page_bytes) ||
+      !aligned16(row_bytes) || !aligned16(layer_bytes) || !aligned16p(staging))
+    return DSR_ERR_ALIGN;
+  const int64_t blocks = ((int64_t)n_tokens + kTokPerWg - 1) / kTokPerWg;
+  if (blocks * n_layers > 0x7fffffffLL) return DSR_ERR_ARG;
+  SlotArgs a;
+  a.layer_base = layer_base;
+  a.kv_stride = kv_stride;
+  a.page_stride = page_stride;
+  a.page_bytes = page_bytes;
+  a.num_blocks = num_blocks;
+  a.row_bytes = row_bytes;
+  a.slot_mapping = slot_mapping;
+  a.row_offsets = row_offsets;
+  a.staging = const_cast<uint8_t*>(static_cast<const uint8_t*>(staging));
+  a.staging_bytes = staging_bytes;
+  a.layer_bytes = layer_bytes;
+  a.n_tokens = n_tokens;
+  a.n_layers = n_layers;
+  a.layer0 = layer0;
+  a.block_size = block_size;
+  a.block_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+  RotArgs ra;
+  ra.u.layer0 = layer0;
+  ra.cos_sin = reinterpret_cast<const float2*>(cos_sin);
+  ra.rope_idx = rope_idx;
+  ra.n_tables = n_tables;
+  ra.layer_group = layer_group;
+  ra.n_groups = layer_group ? n_groups : 1;
+  ra.row_vecs = hv;
+  ra.rot_half = rot_dim / 2;
+  ra.rot_vecs = rot_dim * esize / 16;
+  ra.half_vecs = rope_style == DSR_ROPE_NEOX ? rot_dim / 2 * esize / 16 : 0;
+  ra.k_scale = k_scale;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t per = items_per_launch(n_layers, kTokPerWg) / kTokPerWg * kTokPerWg;
+  if (per <= 0) return DSR_ERR_ARG;
+  for (int64_t t0 = 0; t0 < n_tokens; t0 += per) {
+    SlotArgs b = a;
+    b.slot_mapping += t0;
+    b.row_offsets += t0;
+    b.n_tokens = (int32_t)(n_tokens - t0 < per ? n_tokens - t0 : per);
+    RotArgs rb = ra;
+    rb.rope_idx = rope_idx + t0;
+    const int64_t units = ((int64_t)b.n_tokens + kTokPerWg - 1) / kTokPerWg * n_layers;
+    const unsigned grid = (unsigned)((units + kXcds - 1) / kXcds * kXcds);
+    const size_t dyn = occupancy_lds(3, sizeof(float2) * kTokPerWg * kSlotRotMaxHalf);
+    const bool neox = rope_style == DSR_ROPE_NEOX;
+#define DSR_SLOT_ROT(DT)                                                                  \
+  (neox ? kv_slots_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(b, rb) \
+        : kv_slots_rerotate_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(b, rb))
+    switch (dtype) {
+      case DSR_DTYPE_BF16: DSR_SLOT_ROT(DSR_DTYPE_BF16); break;
+      case DSR_DTYPE_FP16: DSR_SLOT_ROT(DSR_DTYPE_FP16); break;
+      case DSR_DTYPE_FP8_E4M3: DSR_SLOT_ROT(DSR_DTYPE_FP8_E4M3); break;
+      default: DSR_SLOT_ROT(DSR_DTYPE_FP8_E5M2); break;
+    }
+#undef DSR_SLOT_ROT
+    const int rc = (int)hipGetLastError();
+    if (rc != 0) return rc;
+  }
+  return DSR_OK;
+}
+
 }  // namespace
+
+extern "C" {
 
 int dsr_gather_slots(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
                      int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
@@ -845,6 +948,22 @@ int dsr_scatter_slots(const uint64_t* layer_base, int n_layers, int64_t kv_strid
   return slots_launch(false, layer_base, n_layers, kv_stride, page_stride, page_bytes,
                       num_blocks, block_size, row_bytes, slot_mapping, row_offsets, n_tokens,
                       staging, staging_bytes, layer_bytes, layer0, stream);
+}
+
+int dsr_scatter_slots_rerotate(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                               int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                               int block_size, int64_t row_bytes, const int64_t* slot_mapping,
+                               const int64_t* row_offsets, int n_tokens, const void* staging,
+                               int64_t staging_bytes, int64_t layer_bytes, int layer0,
+                               const float* cos_sin, const int32_t* rope_idx, int n_tables,
+                               const int32_t* layer_group, int n_groups, int head_dim,
+                               int rot_dim, int rope_style, int dtype, const float* k_scale,
+                               dsr_stream_t stream) {
+  return slots_rerotate_launch(layer_base, n_layers, kv_stride, page_stride, page_bytes,
+                               num_blocks, block_size, row_bytes, slot_mapping, row_offsets,
+                               n_tokens, staging, staging_bytes, layer_bytes, layer0, cos_sin,
+                               rope_idx, n_tables, layer_group, n_groups, head_dim, rot_dim,
+                               rope_style, dtype, k_scale, stream);
 }
 
 }  // extern "C"

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "kv_common.h"
+#include "kv_rotate.h"
 
 namespace {
 
@@ -235,6 +236,123 @@ __global__ __launch_bounds__(kThreads, 4) void kv_slots_packed_kernel(SlotArgs a
     if (ok[k]) {
       *reinterpret_cast<u32x4*>(dst[k]) = xk[k];
       *reinterpret_cast<u32x4*>(dst[k] + dvs) = xv[k];
+    }
+  }
+}
+
+// Token-form load scatter with the fused re-rotation: kv_slots_kernel's
+// scatter (16 tokens per workgroup, 4 per wave, lanes across the row,
+// branch-free) where the K vectors of a token with rope_idx[t] >= 0 go
+// through rotate_vec with that token's (cos, sin) table. Each wave stages
+// its own 4 tokens' tables in its slice of LDS with loads that write LDS
+// directly (no registers), issued before the rows; one wait for all of the
+// wave's loads then covers them. Heads are row_vecs (a power of two <= 64)
+// vectors, so a head never straddles a 64-vector slice of the row and its
+// neox partner sits half_vecs lanes away in the same load. At most 168
+// VGPRs keep 3 waves per SIMD.
+constexpr int kSlotRotMaxHalf = 128;  // rot_dim <= 256
+// s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+template <int DT, int STYLE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+void kv_slots_rerotate_kernel(SlotArgs a, RotArgs ra) {
+  __shared__ float2 tab[kTokPerWg][kSlotRotMaxHalf];
+  const int64_t nu = ((int64_t)a.n_tokens + kTokPerWg - 1) / kTokPerWg * a.n_layers;
+  const int64_t unit = layer_major_unit(nu, a.n_layers);
+  if (unit < 0) return;
+  const int64_t tb = unit / a.n_layers;
+  const int l = (int)(unit - tb * a.n_layers);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int vpr = (int)(a.row_bytes >> 4);
+  // layer l's group block of tables (-1: no RoPE in this layer)
+  int gbase = 0;
+  if (ra.layer_group) {
+    const int g = ra.layer_group[ra.u.layer0 + l];
+    gbase = g < 0 || g >= ra.n_groups ? -1 : g * ra.n_tables;
+  }
+  rsrc_t ck[kTokPerWave], cv[kTokPerWave], rk[kTokPerWave], rv[kTokPerWave];
+  int ti[kTokPerWave];
+#pragma unroll
+  for (int j = 0; j < kTokPerWave; ++j) {
+    const int64_t t = tb * kTokPerWg + wave * kTokPerWave + j;
+    ck[j] = cv[j] = rk[j] = rv[j] = make_rsrc(a.staging, 0);
+    ti[j] = -1;
+    if (t < a.n_tokens) {
+      const int64_t slot = a.slot_mapping[t];
+      const int64_t ro = a.row_offsets[t];
+      const int r = ra.rope_idx[t];
+      const int64_t blk = slot >= 0 ? slot / a.block_size : -1;
+      const int64_t off = ro + (int64_t)(a.layer0 + l) * a.layer_bytes;
+      if (blk >= 0 && blk < a.num_blocks && off >= 0 &&
+          off + a.page_bytes + a.row_bytes <= a.staging_bytes) {
+        const uint8_t* row = reinterpret_cast<const uint8_t*>(a.layer_base[l]) +
+                             blk * a.page_stride + (slot - blk * a.block_size) * a.row_bytes;
+        ck[j] = make_rsrc(row, a.row_bytes);
+        cv[j] = make_rsrc(row + a.kv_stride, a.row_bytes);
+        rk[j] = make_rsrc(a.staging + off, a.row_bytes);
+        rv[j] = make_rsrc(a.staging + off + a.page_bytes, a.row_bytes);
+        ti[j] = r < 0 || r >= ra.n_tables || gbase < 0 ? -1 : gbase + r;
+      }
+    }
+  }
+  // this wave's tables straight into its LDS slice (16 bytes = 2 pairs per
+  // lane: one load covers 128 pairs); zero-size descriptors for tokens that
+  // keep their K
+#pragma unroll
+  for (int j = 0; j < kTokPerWave; ++j) {
+    const uint8_t* tp = reinterpret_cast<const uint8_t*>(ra.cos_sin);
+    const rsrc_t tr = ti[j] >= 0 ? make_rsrc(tp + (int64_t)ti[j] * ra.rot_half * sizeof(float2),
+                                             ra.rot_half * (int64_t)sizeof(float2))
+                                 : make_rsrc(tp, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        tr, (__attribute__((address_space(3))) void*)&tab[wave * kTokPerWave + j][0], 16,
+        lane * 16, 0, 0, 0);
+  }
+  float scale = 1.0f, inv_scale = 1.0f;
+  if (is_fp8<DT>()) {
+    scale = ra.k_scale[a.layer0 + l];
+    inv_scale = 1.0f / scale;
+  }
+  const int hv = ra.row_vecs;  // vectors per head
+  // 64-vector slices per round: fp8 rows of up to 1 KiB fit one
+  constexpr int RU = is_fp8<DT>() ? 1 : kRowUnroll;
+  for (int vb = 0; vb < vpr; vb += kWave * RU) {
+    u32x4 xk[kTokPerWave][RU], xv[kTokPerWave][RU];
+#pragma unroll
+    for (int j = 0; j < kTokPerWave; ++j) {
+#pragma unroll
+      for (int m = 0; m < RU; ++m) {
+        const int v = vb + m * kWave + lane;
+        xk[j][m] = bload(rk[j], v << 4);
+        xv[j][m] = bload(rv[j], v << 4);
+      }
+    }
+    if (vb == 0) {  // the tables (loaded first) and this round's rows have landed
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __builtin_amdgcn_wave_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);  // no LDS read moves above the wait
+    }
+#pragma unroll
+    for (int j = 0; j < kTokPerWave; ++j)
+#pragma unroll
+      for (int m = 0; m < RU; ++m) bstore(cv[j], (vb + m * kWave + lane) << 4, xv[j][m]);
+#pragma unroll
+    for (int j = 0; j < kTokPerWave; ++j) {
+#pragma unroll
+      for (int m = 0; m < RU; ++m) {
+        const int v = vb + m * kWave + lane;
+        u32x4 q = xk[j][m];
+        if (STYLE == DSR_ROPE_NEOX) {  // the partner half_vecs away inside the same head
+          const int c = v & (hv - 1);
+          const int src = c < ra.half_vecs ? lane + ra.half_vecs : lane - ra.half_vecs;
+#pragma unroll
+          for (int x = 0; x < 4; ++x) q[x] = (unsigned)__shfl((int)xk[j][m][x], src);
+        }
+        const u32x4 r = rotate_vec<DT, STYLE>(ra, xk[j][m], q, v & (hv - 1),
+                                              tab[wave * kTokPerWave + j], scale, inv_scale);
+        bstore(ck[j], v << 4, ti[j] >= 0 ? r : xk[j][m]);
+      }
     }
   }
 }

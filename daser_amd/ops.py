@@ -390,6 +390,50 @@ def _shared_offsets(slot_offsets) -> bool:
     return offs_h is not None and offs_h.size > 1 and 2 * np.unique(offs_h).size <= offs_h.size
 
 
+def _rope_args(lay: PagedKVLayout, cos_sin: torch.Tensor, rope_idx, rot_dim, k_scale,
+               layer0: int, layer_group):
+    """Checks the re-rotation inputs shared by the page and token forms;
+    returns (rot_dim, n_tables, n_groups or 0, device layer_group or None,
+    k_scale pointer or None)."""
+    if lay.dtype not in _DTYPE_CODES:
+        raise TypeError(f"re-rotation does not support KV dtype {lay.dtype}")
+    if not lay.has_geometry:
+        raise ValueError("re-rotation needs the K page geometry: register caches that are "
+                         "not 5-D with block_size and head_dim")
+    rot_dim = lay.head_dim if rot_dim is None else rot_dim
+    grouped = layer_group is not None
+    if cos_sin.dtype != torch.float32 or cos_sin.dim() != (4 if grouped else 3) or \
+            cos_sin.shape[-2:] != (rot_dim // 2, 2):
+        shape = "[groups, n, {}, 2]" if grouped else "[n, {}, 2]"
+        raise ValueError("cos_sin must be float32 " + shape.format(rot_dim // 2))
+    if cos_sin.device != lay.device or not cos_sin.is_contiguous():
+        raise ValueError("cos_sin must be a contiguous device tensor")
+    n_groups = cos_sin.shape[0] if grouped else 1
+    n_tables = cos_sin.shape[-3]
+    ridx = _host_array(rope_idx, np.int64)
+    if ridx is not None and ridx.size and (ridx.max() >= n_tables or ridx.min() < -1):
+        raise IndexError("rope_idx outside [-1, n_tables)")
+    lg_d = None
+    if grouped:
+        lg = _host_array(layer_group, np.int64)
+        if lg is not None and (lg.size < layer0 + lay.num_layers or
+                               (lg.size and (lg.min() < -1 or lg.max() >= n_groups))):
+            raise IndexError("layer_group needs one group in [-1, n_groups) per layer")
+        lg_d = _as_device_table(layer_group, torch.int32, lay.device, "layer_group")
+    ks_ptr = None
+    if lay.dtype in FP8_DTYPES:
+        if k_scale is None:
+            raise ValueError("fp8 re-rotation needs per-layer k_scale")
+        if (
+            k_scale.dtype != torch.float32
+            or k_scale.device != lay.device
+            or k_scale.numel() < layer0 + lay.num_layers
+        ):
+            raise ValueError("k_scale must be a float32 device tensor with one scale per layer")
+        ks_ptr = k_scale.data_ptr()
+    return rot_dim, n_tables, n_groups if grouped else 0, lg_d, ks_ptr
+
+
 def scatter_rerotate(
     table: LayerTable,
     page_ids,
@@ -421,31 +465,8 @@ def scatter_rerotate(
     distinct), False for device tables. Results do not depend on it.
     """
     lay = table.layout
-    if lay.dtype not in _DTYPE_CODES:
-        raise TypeError(f"re-rotation does not support KV dtype {lay.dtype}")
-    if not lay.has_geometry:
-        raise ValueError("re-rotation needs the K page geometry: register caches that are "
-                         "not 5-D with block_size and head_dim")
-    rot_dim = lay.head_dim if rot_dim is None else rot_dim
-    grouped = layer_group is not None
-    if cos_sin.dtype != torch.float32 or cos_sin.dim() != (4 if grouped else 3) or \
-            cos_sin.shape[-2:] != (rot_dim // 2, 2):
-        shape = "[groups, n, {}, 2]" if grouped else "[n, {}, 2]"
-        raise ValueError("cos_sin must be float32 " + shape.format(rot_dim // 2))
-    if cos_sin.device != lay.device or not cos_sin.is_contiguous():
-        raise ValueError("cos_sin must be a contiguous device tensor")
-    n_groups = cos_sin.shape[0] if grouped else 1
-    n_tables = cos_sin.shape[-3]
-    ridx = _host_array(rope_idx, np.int64)
-    if ridx is not None and ridx.size and (ridx.max() >= n_tables or ridx.min() < -1):
-        raise IndexError("rope_idx outside [-1, n_tables)")
-    lg_d = None
-    if grouped:
-        lg = _host_array(layer_group, np.int64)
-        if lg is not None and (lg.size < layer0 + lay.num_layers or
-                               (lg.size and (lg.min() < -1 or lg.max() >= n_groups))):
-            raise IndexError("layer_group needs one group in [-1, n_groups) per layer")
-        lg_d = _as_device_table(layer_group, torch.int32, lay.device, "layer_group")
+    rot_dim, n_tables, n_groups, lg_d, ks_ptr = _rope_args(
+        lay, cos_sin, rope_idx, rot_dim, k_scale, layer0, layer_group)
     if shared_records is None:
         shared_records = _shared_offsets(slot_offsets)
     page_ids, slot_offsets, rope_idx = dest_order(page_ids, slot_offsets, rope_idx)
@@ -453,19 +474,8 @@ def scatter_rerotate(
     ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")
     if ridx_d.numel() != _tables[0].numel():
         raise ValueError("rope_idx and page_ids differ in length")
-    ks_ptr = None
-    if lay.dtype in FP8_DTYPES:
-        if k_scale is None:
-            raise ValueError("fp8 re-rotation needs per-layer k_scale")
-        if (
-            k_scale.dtype != torch.float32
-            or k_scale.device != lay.device
-            or k_scale.numel() < layer0 + lay.num_layers
-        ):
-            raise ValueError("k_scale must be a float32 device tensor with one scale per layer")
-        ks_ptr = k_scale.data_ptr()
     common = (*args, cos_sin.data_ptr(), ridx_d.data_ptr(), n_tables,
-              None if lg_d is None else lg_d.data_ptr(), n_groups if grouped else 0,
+              None if lg_d is None else lg_d.data_ptr(), n_groups,
               lay.head_dim, rot_dim, ROPE_STYLES[style], _DTYPE_CODES[lay.dtype], ks_ptr)
     flags = _lib.DSR_REROTATE_SHARED_RECORDS if shared_records else 0
     if lay.k_layout in ("kx", "hnd"):
@@ -542,6 +552,38 @@ def scatter_slots(table: LayerTable, slot_mapping, row_offsets, staging: torch.T
     args, _tables = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, False)
     rc = _lib.lib().dsr_scatter_slots(*args, _stream_handle(table.layout.device))
     _lib.check("dsr_scatter_slots", rc)
+
+
+def scatter_slots_rerotate(table: LayerTable, slot_mapping, row_offsets,
+                           staging: torch.Tensor, cos_sin: torch.Tensor, rope_idx, *,
+                           rot_dim: Optional[int] = None, style: str = "neox",
+                           k_scale: Optional[torch.Tensor] = None, layer0: int = 0,
+                           layers: Optional[tuple[int, int]] = None,
+                           layer_group=None) -> None:
+    """:func:`scatter_slots` with each valid token's K rotated by
+    ``cos_sin[rope_idx[t]]`` (-1 = copy), as :func:`scatter_rerotate` rotates
+    a page row (same tables, scales and layer groups). Host tables are
+    processed in destination-slot order."""
+    lay = table.layout
+    rot_dim, n_tables, n_groups, lg_d, ks_ptr = _rope_args(
+        lay, cos_sin, rope_idx, rot_dim, k_scale, layer0, layer_group)
+    sm = _host_array(slot_mapping, np.int64)
+    ro = _host_array(row_offsets, np.int64)
+    ri = _host_array(rope_idx, np.int64)
+    if sm is not None and ro is not None and ri is not None and sm.size:
+        if ri.shape != sm.shape:
+            raise ValueError("rope_idx and slot_mapping differ in length")
+        order = np.argsort(sm, kind="stable")
+        slot_mapping, row_offsets, rope_idx = sm[order], ro[order], ri[order]
+    args, _tables = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, False)
+    ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")
+    if ridx_d.numel() != _tables[0].numel():
+        raise ValueError("rope_idx and slot_mapping differ in length")
+    rc = _lib.lib().dsr_scatter_slots_rerotate(
+        *args, cos_sin.data_ptr(), ridx_d.data_ptr(), n_tables,
+        None if lg_d is None else lg_d.data_ptr(), n_groups, lay.head_dim, rot_dim,
+        ROPE_STYLES[style], _DTYPE_CODES[lay.dtype], ks_ptr, _stream_handle(lay.device))
+    _lib.check("dsr_scatter_slots_rerotate", rc)
 
 
 def token_row_offsets(req_tokens: Sequence[int], slot_bytes: int, block_size: int,

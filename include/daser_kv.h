@@ -49,9 +49,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 /* Bumped whenever an entry point's signature changes or one is added:
  * 2 layer_group on the re-rotation, 3 dsr_scatter_rerotate_kx, 4 the
  * re-rotations' flags, 5 the head-major (_hnd) entry points, 6
- * dsr_set_tuning, 7 dsr_scatter_ex. Callers check
+ * dsr_set_tuning, 7 dsr_scatter_ex, 8 dsr_scatter_slots_rerotate. Callers check
  * dsr_abi_version() against it. */
-#define DSR_ABI_VERSION 7
+#define DSR_ABI_VERSION 8
 
 /*
  * Kernel choice and launch shape follow from the geometry. dsr_set_tuning()
@@ -343,6 +343,27 @@ int dsr_scatter_slots(const uint64_t* layer_base, int n_layers, int64_t kv_strid
                       const int64_t* row_offsets, int n_tokens, const void* staging,
                       int64_t staging_bytes, int64_t layer_bytes, int layer0,
                       dsr_stream_t stream);
+
+/*
+ * Token-form load with the fused re-rotation: dsr_scatter_slots, and the K
+ * row of each valid token t with rope_idx[t] >= 0 has every head's first
+ * rot_dim dims rotated by the table cos_sin[rope_idx[t]] exactly as
+ * dsr_scatter_rerotate rotates a page row (same pairs, scales, rounding,
+ * layer groups). Heads must be a power-of-two number of 16-byte vectors
+ * (<= 64), rot_dim <= 256 in whole vectors (each half, for neox); else
+ * DSR_ERR_SHAPE. Per-token form of the load loop of
+ * daser/connector/daser_connector.py:536-551 plus the re-rotation, which
+ * the reference does not have.
+ */
+int dsr_scatter_slots_rerotate(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                               int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                               int block_size, int64_t row_bytes, const int64_t* slot_mapping,
+                               const int64_t* row_offsets, int n_tokens, const void* staging,
+                               int64_t staging_bytes, int64_t layer_bytes, int layer0,
+                               const float* cos_sin, const int32_t* rope_idx, int n_tables,
+                               const int32_t* layer_group, int n_groups, int head_dim,
+                               int rot_dim, int rope_style, int dtype, const float* k_scale,
+                               dsr_stream_t stream);
 
 /*
  * Pinned-host staging ring between device records and the store file.

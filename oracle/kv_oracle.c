@@ -286,3 +286,52 @@ void orc_scatter_slots(uint8_t* const* layer_base, int n_layers, int64_t kv_stri
     }
   }
 }
+
+/* Token form of orc_scatter_rerotate: orc_scatter_slots, then for every
+ * valid token t with rotate[t] != 0 each head of its K row (in every layer)
+ * is rotated by delta = new_pos[t] - stored_pos[t] exactly as a page row is
+ * (pairs, frequencies, scales and the one rounding of orc_scatter_rerotate).
+ * Net-new like the page form; the copies follow daser_connector.py:536-551. */
+void orc_scatter_slots_rerotate(uint8_t* const* layer_base, int n_layers, int64_t kv_stride,
+                                int64_t page_stride, int64_t page_bytes, int block_size,
+                                int64_t row_bytes, const int64_t* slot_mapping,
+                                const int64_t* row_offsets, int n_tokens,
+                                const uint8_t* staging, int64_t layer_bytes, int layer0,
+                                int num_heads, int head_dim, int rot_dim, int style, int dtype,
+                                const float* k_scale, const int64_t* stored_pos,
+                                const int64_t* new_pos, const int8_t* rotate, double theta,
+                                const double* inv_freq) {
+  const int esize = ORC_IS_FP8(dtype) ? 1 : 2;
+  const int64_t head_bytes = (int64_t)head_dim * esize;
+  const int half = rot_dim / 2;
+  double w[1024];
+  for (int j = 0; j < half; ++j)
+    w[j] = inv_freq ? inv_freq[j] : pow(theta, -2.0 * j / rot_dim);
+  orc_scatter_slots(layer_base, n_layers, kv_stride, page_stride, page_bytes, block_size,
+                    row_bytes, slot_mapping, row_offsets, n_tokens, staging, layer_bytes,
+                    layer0);
+  double x[2048];
+  for (int t = 0; t < n_tokens; ++t) {
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0 || !rotate[t]) continue;
+    const double delta = (double)(new_pos[t] - stored_pos[t]);
+    for (int l = 0; l < n_layers; ++l) {
+      const double sc = ORC_IS_FP8(dtype) ? (double)k_scale[layer0 + l] : 1.0;
+      uint8_t* drow = layer_base[l] + (slot / block_size) * page_stride +
+                      (slot % block_size) * row_bytes;
+      const uint8_t* srow = staging + row_offsets[t] + (int64_t)(layer0 + l) * layer_bytes;
+      for (int h = 0; h < num_heads; ++h) {
+        const uint8_t* s = srow + h * head_bytes;
+        uint8_t* d = drow + h * head_bytes;
+        for (int j = 0; j < rot_dim; ++j) x[j] = orc_decode(dtype, load_elem(s, dtype, j)) * sc;
+        for (int j = 0; j < half; ++j) {
+          if (style == ORC_NEOX)
+            rot(&x[j], &x[j + half], delta * w[j]);
+          else
+            rot(&x[2 * j], &x[2 * j + 1], delta * w[j]);
+        }
+        for (int j = 0; j < rot_dim; ++j) store_elem(d, dtype, j, orc_encode(dtype, x[j] / sc));
+      }
+    }
+  }
+}

@@ -48,10 +48,13 @@ def lib() -> ctypes.CDLL:
         slots = [P, I, I64, I64, I64, I, I64, P, P, I, P, I64, I]
         h.orc_gather_slots.argtypes = slots
         h.orc_scatter_slots.argtypes = slots
+        h.orc_scatter_slots_rerotate.argtypes = slots + [
+            I, I, I, I, I, P, P, P, P, ctypes.c_double, P,
+        ]
         h.orc_decode_array.argtypes = [I, P, P, I64]
         h.orc_encode_array.argtypes = [I, P, P, I64]
         for f in ("orc_gather", "orc_scatter", "orc_scatter_rerotate", "orc_gather_slots",
-                  "orc_scatter_slots",
+                  "orc_scatter_slots", "orc_scatter_slots_rerotate",
                   "orc_decode_array", "orc_encode_array"):
             getattr(h, f).restype = None
         _lib = h
@@ -166,6 +169,30 @@ def scatter_slots(layers, slot_mapping, row_offsets, staging: np.ndarray, layer_
                   layer0: int = 0) -> None:
     _slots_call(lib().orc_scatter_slots, layers, slot_mapping, row_offsets,
                 np.ascontiguousarray(staging), layer_bytes, layer0)
+
+
+def scatter_slots_rerotate(layers, slot_mapping, row_offsets, staging: np.ndarray,
+                           layer_bytes: int, *, dtype: int, rot_dim: int, style: int,
+                           stored_pos, new_pos, rotate, theta: float,
+                           inv_freq: Optional[np.ndarray] = None,
+                           k_scale: Optional[np.ndarray] = None, layer0: int = 0) -> None:
+    """Token form of :func:`scatter_rerotate`: per-token positions."""
+    tab, kvs, ps, pb = _layer_table(layers)
+    _, _, bs, h, d = layers[0].shape
+    row_bytes = h * d * layers[0].itemsize
+    sm = np.ascontiguousarray(slot_mapping, dtype=np.int64)
+    ro = np.ascontiguousarray(row_offsets, dtype=np.int64)
+    sp = np.ascontiguousarray(stored_pos, dtype=np.int64)
+    npos = np.ascontiguousarray(new_pos, dtype=np.int64)
+    rot = np.ascontiguousarray(rotate, dtype=np.int8)
+    ks = None if k_scale is None else np.ascontiguousarray(k_scale, dtype=np.float32)
+    inv = None if inv_freq is None else np.ascontiguousarray(inv_freq, dtype=np.float64)
+    stg = np.ascontiguousarray(staging)
+    lib().orc_scatter_slots_rerotate(
+        _ptr(tab), len(layers), kvs, ps, pb, bs, row_bytes, _ptr(sm), _ptr(ro), sm.size,
+        _ptr(stg), layer_bytes, layer0, h, d, rot_dim, style, dtype,
+        None if ks is None else _ptr(ks), _ptr(sp), _ptr(npos), _ptr(rot), float(theta),
+        None if inv is None else _ptr(inv))
 
 
 def decode(dtype: int, bits) -> np.ndarray:

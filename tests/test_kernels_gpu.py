@@ -1023,6 +1023,124 @@ def test_random_geometry_slots_parity(gpu, dt, D, H, bs, style, R, L, seed):
         assert np.array_equal(to_bits_np(dst[l], dt), dref[l]), f"layer {l}"
 
 
+def _token_tables(deltas, rot_dim, gpu, theta=500000.0):
+    """rope_idx per token (-1 where the delta is 0) and the delta tables."""
+    d = np.asarray(deltas, np.int64)
+    uniq = sorted({int(x) for x in d if x})
+    idx = np.array([uniq.index(int(x)) if x else -1 for x in d], np.int64)
+    return idx, position.delta_tables(uniq or [0], rot_dim, theta, device=gpu)
+
+
+@pytest.mark.parametrize("dt,style,D,R,H,bs", [
+    ("bf16", "neox", 128, 128, 8, 16),
+    ("bf16", "neox", 128, 96, 2, 16),   # partial rotary, half of 6 vectors
+    ("bf16", "gptj", 64, 32, 4, 8),
+    ("fp16", "neox", 256, 128, 1, 16),
+    ("fp16", "gptj", 128, 128, 8, 32),
+    ("e4m3", "neox", 128, 128, 8, 16),
+    ("e4m3", "gptj", 128, 64, 4, 16),
+    ("e5m2", "neox", 128, 64, 8, 16),
+    ("e5m2", "gptj", 256, 256, 2, 16),
+])
+def test_slots_rerotate_matches_oracle(gpu, dt, style, D, R, H, bs):
+    """Token-form load with per-request deltas (ragged requests, partial
+    pages, padding, requests kept at their position) against the oracle:
+    V bit-exact, K within the rotation tolerance."""
+    print(f"case: slots rerotate {dt} {style} D{D} R{R} H{H} bs{bs}", flush=True)
+    L = 3
+    shape = KVShape(L, H, D, bs, 1 if dt in FP8 else 2)
+    rng = np.random.default_rng(D * 7 + R + H)
+    toks = [int(x) for x in rng.integers(1, 5 * bs, size=5)]
+    pages = [(t + bs - 1) // bs for t in toks]
+    nb = sum(pages) + 7
+    perm = rng.permutation(nb).astype(np.int64)
+    tables, k = [], 0
+    for p in pages:
+        tables.append(perm[k:k + p].tolist())
+        k += p
+    row = H * D * shape.elem_bytes
+    sm = ops.slot_mapping_for(tables, toks, bs)
+    ro = ops.token_row_offsets(toks, shape.slot_bytes, bs, row)
+    sm[rng.random(sm.size) < 0.1] = -1
+    req_delta = [0, 517, -3000, 32767, 1]
+    tok_delta = np.repeat(np.asarray(req_delta, np.int64), toks)
+    ridx, tabs = _token_tables(tok_delta, R, gpu)
+    src = rand_caches(shape, nb, dt, gpu, seed=11, scale=40.0 if dt in FP8 else 1.0)
+    st = torch.zeros(sum(pages) * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather_slots(ops.LayerTable(src), ops.slot_mapping_for(tables, toks, bs), ro, st)
+    ks_np = (rng.random(L).astype(np.float32) * 0.5 + 0.01) if dt in FP8 else None
+    ks = torch.from_numpy(ks_np).to(gpu) if ks_np is not None else None
+    dst = rand_caches(shape, nb, dt, gpu, seed=12)
+    dref = [to_bits_np(c, dt) for c in dst]
+    ops.scatter_slots_rerotate(ops.LayerTable(dst), sm, ro, st, tabs, ridx, rot_dim=R,
+                               style=style, k_scale=ks)
+    oracle.scatter_slots_rerotate(
+        dref, sm, ro, st.cpu().numpy(), shape.layer_bytes, dtype=ORC_DT[dt], rot_dim=R,
+        style=0 if style == "neox" else 1, stored_pos=np.zeros(sm.size, np.int64),
+        new_pos=tok_delta, rotate=tok_delta != 0, theta=500000.0, k_scale=ks_np)
+    torch.cuda.synchronize()
+    for l in range(L):
+        got = to_bits_np(dst[l], dt)
+        assert np.array_equal(got[1], dref[l][1]), f"V layer {l}"
+        ok, msg = rotation_within_tolerance(got[0], dref[l][0], dt)
+        assert ok, f"K layer {l}: {msg}"
+
+
+@pytest.mark.parametrize("dt,style,R", [("bf16", "neox", 128), ("e4m3", "gptj", 64),
+                                        ("fp16", "neox", 64)])
+def test_slots_rerotate_equals_page_rerotate(gpu, dt, style, R):
+    """On whole pages the token form writes the same bits as the page form
+    (same tables, same fp32 arithmetic), including grouped layers with a
+    layer that has no RoPE."""
+    print(f"case: slots rerotate == pages {dt} {style} R{R}", flush=True)
+    L, bs = 4, 16
+    shape = KVShape(L, 8, 128, bs, 1 if dt in FP8 else 2)
+    rng = np.random.default_rng(5)
+    n, nb = 9, 24
+    src = rand_caches(shape, nb, dt, gpu, seed=3, scale=40.0 if dt in FP8 else 1.0)
+    offs = np.arange(n, dtype=np.int64) * shape.slot_bytes
+    st = torch.zeros(n * shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(ops.LayerTable(src), rng.permutation(nb)[:n].astype(np.int32), offs, st)
+    ids = rng.permutation(nb)[:n].astype(np.int64)
+    deltas = np.asarray([0, 9, 9, -77, 4000, 4000, 4000, 0, 123], np.int64)
+    ridx_p, uniq = position.page_rope_index([1] * n, deltas)
+    thetas = (500000.0, 10000.0)
+    tabs = torch.stack([position.delta_tables(uniq, R, t, device=gpu) for t in thetas])
+    group = torch.tensor([0, 1, -1, 0], dtype=torch.int32, device=gpu)
+    ks = torch.full((L,), 0.37, dtype=torch.float32, device=gpu) if dt in FP8 else None
+    pg = [torch.zeros_like(c) for c in src]
+    ops.scatter_rerotate(ops.LayerTable(pg), ids.astype(np.int32), offs, st, tabs, ridx_p,
+                         rot_dim=R, style=style, k_scale=ks, layer_group=group)
+    sm = (ids[:, None] * bs + np.arange(bs)[None, :]).reshape(-1)
+    row = shape.num_heads * shape.head_dim * shape.elem_bytes
+    ro = (offs[:, None] + np.arange(bs)[None, :] * row).reshape(-1)
+    ridx_t = np.repeat(np.asarray(ridx_p, np.int64), bs)
+    tk = [torch.zeros_like(c) for c in src]
+    ops.scatter_slots_rerotate(ops.LayerTable(tk), sm, ro, st, tabs, ridx_t, rot_dim=R,
+                               style=style, k_scale=ks, layer_group=group)
+    torch.cuda.synchronize()
+    for l in range(L):
+        assert torch.equal(tk[l].view(torch.uint8), pg[l].view(torch.uint8)), f"layer {l}"
+
+
+def test_slots_rerotate_rejects_unsupported_heads(gpu):
+    """Heads that are not a power-of-two number of 16-byte vectors, or a
+    rotary half wider than 128 pairs, are refused."""
+    print("case: slots rerotate shape errors", flush=True)
+    shape = KVShape(1, 2, 96, 16, 2)  # 12 vectors per head
+    caches = rand_caches(shape, 4, "bf16", gpu, seed=1)
+    st = torch.zeros(shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    tabs = position.delta_tables([5], 96, device=gpu)
+    with pytest.raises(DaserKVError):
+        ops.scatter_slots_rerotate(ops.LayerTable(caches), [0], [0], st, tabs, [0])
+    shape = KVShape(1, 1, 512, 16, 2)  # rot_dim 512 > 256
+    caches = rand_caches(shape, 2, "bf16", gpu, seed=1)
+    st = torch.zeros(shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    tabs = position.delta_tables([5], 512, device=gpu)
+    with pytest.raises(DaserKVError):
+        ops.scatter_slots_rerotate(ops.LayerTable(caches), [0], [0], st, tabs, [0])
+
+
 @pytest.mark.parametrize("heads,head_dim,dt", [(8, 128, "bf16"), (1, 128, "bf16"),
                                               (8, 128, "e4m3")])
 def test_shared_records_hint_does_not_change_results(gpu, heads, head_dim, dt):

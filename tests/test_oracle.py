@@ -432,6 +432,61 @@ def test_slot_gather_equals_page_gather_on_valid_tokens():
         assert not bt[:, others].any()
 
 
+@pytest.mark.parametrize("dt,style,rot", [(BF16, oracle.NEOX, 16), (E4M3, oracle.GPTJ, 12),
+                                          (FP16, oracle.NEOX, 8), (E5M2, oracle.NEOX, 16)])
+def test_slot_rerotate_equals_page_rerotate_on_valid_tokens(dt, style, rot):
+    """The token form of the re-rotation writes, for every valid token, the
+    bytes of the page form (pinned above by closed forms) on the same
+    records; padding tokens are skipped, tail rows of a partial page are not
+    written, and tokens without rotation are plain copies."""
+    rng = np.random.default_rng(21 + dt)
+    L, nb, bs, H, D = 2, 10, 4, 3, 16
+    c8 = dt in (E4M3, E5M2)
+    if c8:
+        caches = [_rot_case(dt, L=1, H=H, D=D, nb=nb, scale=30.0, seed=40 + l)[0]
+                  for l in range(L)]
+        caches = [np.concatenate([c] * 2, axis=2)[:, :, :bs].copy() for c in caches]
+    else:
+        caches = [_rot_case(dt, L=1, H=H, D=D, nb=nb, seed=40 + l)[0] for l in range(L)]
+        caches = [np.concatenate([c] * 2, axis=2)[:, :, :bs].copy() for c in caches]
+    ks = np.float32([0.5, 3.0]) if c8 else None
+    tables = [[7, 1, 4], [9, 0]]
+    toks = [10, 8]
+    deltas = [777, 0]  # request 1 unrotated
+    slot = _slot_size(caches)
+    row = H * D * caches[0].itemsize
+    ids = np.concatenate([np.asarray(t) for t in tables]).astype(np.int32)
+    recs = np.zeros(ids.size * slot, dtype=np.uint8)
+    oracle.gather(caches, ids, np.arange(ids.size) * slot, recs, slot // L)
+    # page form: every page of each request rotated by its delta
+    pdel = np.repeat(deltas, [len(t) for t in tables])
+    page = [np.zeros_like(c) for c in caches]
+    oracle.scatter_rerotate(page, ids, np.arange(ids.size) * slot, recs, slot // L, dtype=dt,
+                            rot_dim=rot, style=style, stored_pos=np.zeros(ids.size, np.int64),
+                            new_pos=pdel, rotate=pdel != 0, theta=500000.0, k_scale=ks)
+    # token form: per-token positions of the same requests, plus padding
+    sm = np.concatenate([ops.slot_mapping_for(tables, toks, bs), [-1, -1]])
+    ro = np.concatenate([ops.token_row_offsets(toks, slot, bs, row), [0, 0]])
+    tdel = np.concatenate([np.full(n, d) for n, d in zip(toks, deltas)] + [[5, 5]])
+    tok = [np.zeros_like(c) for c in caches]
+    oracle.scatter_slots_rerotate(tok, sm, ro, recs, slot // L, dtype=dt, rot_dim=rot,
+                                  style=style, stored_pos=np.zeros(sm.size, np.int64),
+                                  new_pos=tdel, rotate=tdel != 0, theta=500000.0, k_scale=ks)
+    valid = sm[sm >= 0]
+    others = np.setdiff1d(np.arange(nb * bs), valid)
+    for a, b in zip(tok, page):
+        at = a.reshape(2, nb * bs, H, D)
+        bt = b.reshape(2, nb * bs, H, D)
+        assert np.array_equal(at[:, valid], bt[:, valid])
+        assert not at[:, others].any()
+    moved = tok[0].reshape(2, nb * bs, H, D)[0, valid[:10]]
+    plain = [np.zeros_like(c) for c in caches]
+    oracle.scatter_slots(plain, sm, ro, recs, slot // L)
+    assert not np.array_equal(moved, plain[0].reshape(2, nb * bs, H, D)[0, valid[:10]])
+    assert np.array_equal(tok[0].reshape(2, nb * bs, H, D)[:, valid[10:]],
+                          plain[0].reshape(2, nb * bs, H, D)[:, valid[10:]])
+
+
 @pytest.mark.parametrize("itemsize,bs,h,d", [(2, 16, 2, 64), (1, 8, 3, 32), (2, 4, 1, 16)])
 def test_kx_layout_permutation_brute_force(itemsize, bs, h, d):
     """kx_to_nhd / nhd_to_kx against the split-x index formula evaluated
