@@ -106,6 +106,51 @@ def check_rerotate_sample(wl, caches, staging, src_offsets, page_delta, dtype, s
     assert moved > 0, "no K element was rotated"
 
 
+def check_slots_rerotate_sample(wl, caches, staging, sm, ro, tok_delta, seed, n_tok=256):
+    """Sampled tokens of a full-size token-form re-rotating scatter against
+    oracle.scatter_slots_rerotate run on just those tokens: their record
+    rows (all layers) are packed into a small host staging and their
+    destination slots into a small host pool. V rows bit-exact, K within the
+    rotation tolerance."""
+    sh = wl.shape
+    bs, row = sh.block_size, sh.num_heads * sh.head_dim * sh.elem_bytes
+    rng = np.random.default_rng(seed)
+    valid = np.flatnonzero(sm >= 0)
+    sel = np.sort(rng.choice(valid, size=min(n_tok, valid.size), replace=False))
+    n = sel.size
+    # token i of the sample: host record row (i // bs, row i % bs) and host
+    # slot i (block i // bs, offset i % bs)
+    ro_h = (np.arange(n) // bs) * sh.slot_bytes + (np.arange(n) % bs) * row
+    rows = staging.view(-1, row)
+    lrows, prow = sh.layer_bytes // row, sh.page_bytes // row
+    src_rows = torch.from_numpy(ro[sel] // row).to(staging.device)
+    n_slots = -(-n // bs)
+    recs = torch.zeros(n_slots * sh.slot_bytes, dtype=torch.uint8, device=staging.device)
+    dst_rows = torch.from_numpy(ro_h // row).to(staging.device)
+    rrows = recs.view(-1, row)
+    for l in range(sh.num_layers):
+        for half in (0, prow):
+            rrows[dst_rows + l * lrows + half] = rows[src_rows + l * lrows + half]
+    dt = np.uint16 if sh.elem_bytes == 2 else np.uint8
+    want = [np.zeros((2, n_slots, bs, sh.num_heads, sh.head_dim), dt)
+            for _ in range(sh.num_layers)]
+    d = np.asarray(tok_delta, np.int64)[sel]
+    oracle.scatter_slots_rerotate(
+        want, np.arange(n, dtype=np.int64), ro_h, recs.cpu().numpy(), sh.layer_bytes,
+        dtype=oracle.BF16 if sh.elem_bytes == 2 else oracle.E4M3, rot_dim=sh.head_dim,
+        style=oracle.NEOX, stored_pos=np.zeros(n, np.int64), new_pos=d, rotate=d != 0,
+        theta=THETA)
+    blk = torch.from_numpy(sm[sel] // bs).to(staging.device)
+    off = torch.from_numpy(sm[sel] % bs).to(staging.device)
+    for l in range(sh.num_layers):
+        got = _host_bits(caches[l][:, blk, off])  # (2, n, H, D)
+        w = want[l].reshape(2, n_slots * bs, sh.num_heads, sh.head_dim)[:, :n]
+        assert np.array_equal(got[1], w[1]), f"layer {l}: V differs from the oracle"
+        assert got[1].any(), f"layer {l}: sampled rows are empty"
+        ok, msg = oracle.rotation_within_tolerance(got[0], w[0], oracle.BF16)
+        assert ok, f"layer {l}: K outside tolerance: {msg}"
+
+
 def _block_tables(wl):
     tables, k = [], 0
     for n in wl.req_pages:
@@ -158,6 +203,16 @@ def test_round_trip_full_size(gpu, cfg, dtype):
         b = st2.view(-1, row)
         assert torch.equal(a[mask], b[mask])
         assert not b[~mask].any()
+        # the token-form load with every request re-rotated, sampled
+        rng = np.random.default_rng(9)
+        req_delta = rng.integers(1, 32768, size=len(wl.req_tokens))
+        tok_delta = np.repeat(req_delta, wl.req_tokens)
+        uniq = sorted(set(int(x) for x in req_delta))
+        ridx = np.searchsorted(np.asarray(uniq), tok_delta)
+        tabs = position.delta_tables(uniq, wl.shape.head_dim, THETA, device=gpu)
+        dst_full.zero_()
+        ops.scatter_slots_rerotate(ops.LayerTable(dst), sm, ro, st2, tabs, ridx)
+        check_slots_rerotate_sample(wl, dst, st2, sm, ro, tok_delta, seed=21)
     torch.cuda.synchronize()
     del full, caches, dst_full, dst, st
     torch.cuda.empty_cache()
