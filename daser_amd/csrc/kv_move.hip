@@ -83,7 +83,7 @@ UnitArgs make_unit(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
                    const int32_t* page_ids, const int64_t* slot_offsets,
                    int n_pages, const void* staging, int64_t staging_bytes,
                    int64_t layer_bytes, int layer0) {
-  UnitArgs a;
+  UnitArgs a{};
   a.layer_base = layer_base;
   a.kv_stride = kv_stride;
   a.page_stride = page_stride;
@@ -500,7 +500,7 @@ int scatter_rerotate_any(const uint64_t* layer_base, int n_layers,
   if (!rope_idx || (n_tables > 0 && !cos_sin)) return DSR_ERR_ARG;
   if (esize == 1 && !k_scale) return DSR_ERR_ARG;
 
-  RotArgs ra;
+  RotArgs ra{};
   ra.u = make_unit(layer_base, n_layers, kv_stride, page_stride, page_bytes,
                    num_blocks, page_ids, slot_offsets, n_pages, staging,
                    staging_bytes, layer_bytes, layer0);
@@ -761,7 +761,7 @@ int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t 
                      : tpw ? tpw * (kThreads / kWave) : kTokPerWg;
   const int64_t blocks = ((int64_t)n_tokens + tok_wg - 1) / tok_wg;
   if (blocks * n_layers > 0x7fffffffLL) return DSR_ERR_ARG;
-  SlotArgs a;
+  SlotArgs a{};
   a.layer_base = layer_base;
   a.kv_stride = kv_stride;
   a.page_stride = page_stride;
@@ -865,7 +865,7 @@ int slots_rerotate_launch(const uint64_t* layer_base, int n_layers, int64_t kv_s
     return DSR_ERR_ALIGN;
   const int64_t blocks = ((int64_t)n_tokens + kTokPerWg - 1) / kTokPerWg;
   if (blocks * n_layers > 0x7fffffffLL) return DSR_ERR_ARG;
-  SlotArgs a;
+  SlotArgs a{};
   a.layer_base = layer_base;
   a.kv_stride = kv_stride;
   a.page_stride = page_stride;
@@ -882,7 +882,7 @@ int slots_rerotate_launch(const uint64_t* layer_base, int n_layers, int64_t kv_s
   a.layer0 = layer0;
   a.block_size = block_size;
   a.block_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
-  RotArgs ra;
+  RotArgs ra{};
   ra.u.layer0 = layer0;
   ra.cos_sin = reinterpret_cast<const float2*>(cos_sin);
   ra.rope_idx = rope_idx;
