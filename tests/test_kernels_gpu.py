@@ -832,16 +832,32 @@ def test_hip_graph_capture_and_replay(gpu):
     st = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
     dst = [torch.zeros_like(c) for c in src]
     rot = [torch.zeros_like(c) for c in src]
-    table_d, table_r = ops.LayerTable(dst), ops.LayerTable(rot)
+    tok = [torch.zeros_like(c) for c in src]
+    table_d, table_r, table_t = ops.LayerTable(dst), ops.LayerTable(rot), ops.LayerTable(tok)
+    # the token forms: the same requests by slot_mapping, each request's
+    # tokens re-rotated by its own table or (odd requests) copied
+    tables, k = [], 0
+    for n in wl.req_pages:
+        tables.append(wl.page_ids[k:k + n].tolist())
+        k += n
+    row = shape.num_heads * shape.head_dim * shape.elem_bytes
+    sm = torch.from_numpy(ops.slot_mapping_for(tables, wl.req_tokens, shape.block_size)).to(gpu)
+    ro = torch.from_numpy(ops.token_row_offsets(wl.req_tokens, shape.slot_bytes,
+                                                shape.block_size, row)).to(gpu)
+    tidx = torch.from_numpy(np.repeat((np.arange(len(wl.req_tokens)) % 2).astype(np.int32) - 1,
+                                      wl.req_tokens)).to(gpu)
+    st_t = torch.zeros_like(st)
 
     def step():
         ops.gather(table_s, ids, offs, st)
         ops.scatter(table_d, dst_ids, offs, st)
         ops.scatter_rerotate(table_r, dst_ids, offs, st, tabs, ridx)
+        ops.gather_slots(table_s, sm, ro, st_t)
+        ops.scatter_slots_rerotate(table_t, sm, ro, st_t, tabs, tidx)
 
     def snapshot():
         torch.cuda.synchronize()
-        return [st.clone()] + [t.clone() for t in dst + rot]
+        return [st.clone(), st_t.clone()] + [t.clone() for t in dst + rot + tok]
 
     side = torch.cuda.Stream(gpu)
     side.wait_stream(torch.cuda.current_stream(gpu))
@@ -854,17 +870,17 @@ def test_hip_graph_capture_and_replay(gpu):
     for rep in range(3):
         for c in src:  # new inputs, written eagerly
             c.normal_(generator=torch.Generator(device=gpu).manual_seed(100 + rep))
-        for t in [st] + dst + rot:
+        for t in [st, st_t] + dst + rot + tok:
             t.zero_()
         g.replay()
         got = snapshot()
-        for t in [st] + dst + rot:
+        for t in [st, st_t] + dst + rot + tok:
             t.zero_()
         step()
         want = snapshot()
         for i, (a, b) in enumerate(zip(got, want)):
             assert torch.equal(a, b), f"replay {rep}, output {i}"
-    assert want[0].any()
+    assert want[0].any() and want[1].any() and want[-1].any()
 
 
 def _random_cases(n, seed):
