@@ -419,10 +419,20 @@ int dsr_scatter_ex(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
     const int wpc = (flags & DSR_SHARED_RECORDS) && !tune(DSR_TUNE_COPY_WG_PER_CU)
                         ? 0 : copy_wg_per_cu(page_bytes, b.n_units);
     const size_t dyn = occupancy_lds(wpc, 0);
+    // streaming kernel: U vectors per lane per round (8 for pages of
+    // multiples of 32 KiB, 4 for 16 KiB multiples)
     const int64_t pick = tune(DSR_TUNE_SCATTER_KERNEL);
-    const bool stream_k = pick ? pick == 2 : wpc == 1 && page_bytes % (kThreads * 8 * 16) == 0;
-    if (stream_k)
-      kv_scatter_stream_kernel<<<grid, kThreads, dyn, st>>>(b);
+    const int su = page_bytes % (kThreads * 8 * 16) == 0 ? 8
+                   : page_bytes % (kThreads * 4 * 16) == 0 ? 4 : 0;
+    const int64_t kind = pick ? pick : wpc == 1 && su == 8 ? 2 : 1;
+    if (kind == 2 && su == 8)
+      kv_scatter_stream_kernel<8, true><<<grid, kThreads, dyn, st>>>(b);
+    else if (kind == 2 && su == 4)
+      kv_scatter_stream_kernel<4, true><<<grid, kThreads, dyn, st>>>(b);
+    else if (kind == 3 && su == 8)
+      kv_scatter_stream_kernel<8, false><<<grid, kThreads, dyn, st>>>(b);
+    else if (kind == 3 && su == 4)
+      kv_scatter_stream_kernel<4, false><<<grid, kThreads, dyn, st>>>(b);
     else
       kv_scatter_kernel<<<grid, kThreads, dyn, st>>>(b);
   });

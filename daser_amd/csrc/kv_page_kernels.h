@@ -32,7 +32,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_kernel(UnitArgs a) {
 
 // Scatter of pages of 32 KiB and up, launched at one workgroup per CU (the
 // launch policy keeps about 64 KiB of each CU's units in flight; see
-// copy_wg_per_cu in kv_move.hip). Each lane keeps U = 8
+// copy_wg_per_cu in kv_move.hip). Each lane keeps U (8 at 32 KiB)
 // vectors of K and of V in flight, and every store follows its own load's
 // arrival (no wait for the whole round): at one workgroup per CU the waves
 // stream instead of alternating a load burst with a store burst. Measured
@@ -40,12 +40,17 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_kernel(UnitArgs a) {
 // 12.60 ms, 11.98 vs 12.08, 11.97 vs 12.09 for kv_scatter_kernel at its
 // register-limited 3 workgroups per CU; kv_scatter_kernel itself at one
 // workgroup per CU 12.54-12.56 ms. Units in hardware dispatch order
-// (layer_major_unit_hw): a further 3.5%.
+// (kHwOrder, layer_major_unit_hw): a further 3.5%. U = 4 serves 16 KiB
+// pages (e4m3) for measurements: at two workgroups per CU it measured
+// 23.0-23.6 ms at config 4 in three processes on one box against
+// 21.8-24.0 ms for kv_scatter_kernel, the spread being the buffers'
+// placement, so the default stays kv_scatter_kernel there.
+template <int U, bool kHwOrder>
 __global__ __launch_bounds__(kThreads) void kv_scatter_stream_kernel(UnitArgs a) {
-  constexpr int U = 8;
   uint8_t *cache, *rec;
   int l;
-  const int64_t u = layer_major_unit_hw(a.n_units, a.n_layers);
+  const int64_t u = kHwOrder ? layer_major_unit_hw(a.n_units, a.n_layers)
+                             : layer_major_unit(a.n_units, a.n_layers);
   if (u < 0 || !unit_addresses(a, u, &cache, &rec, &l)) return;
   const int64_t pb = a.page_bytes;
   const rsrc_t sk = make_rsrc(rec, pb), sv = make_rsrc(rec + pb, pb);

@@ -73,7 +73,10 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
  *   DSR_TUNE_COPY_WG_PER_CU       workgroups per CU of the one-unit page
  *                                 gather / scatter
  *   DSR_TUNE_SCATTER_KERNEL       one-unit page scatter: 1 the load-all-then-
- *                                 store kernel, 2 the streaming kernel
+ *                                 store kernel, 2 the streaming kernel in
+ *                                 hardware dispatch order, 3 the streaming
+ *                                 kernel in per-XCD layer-major order
+ *                                 (streaming: pages of 16 KiB multiples)
  */
 #define DSR_TUNE_UNITS_PER_GROUP 0
 #define DSR_TUNE_MAX_WG_PER_LAUNCH 1

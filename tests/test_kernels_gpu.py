@@ -64,11 +64,11 @@ def test_scatter_cfg1_bit_exact_and_round_trip(gpu):
 @pytest.mark.parametrize("heads,head_dim,dt", [(8, 128, "bf16"), (16, 128, "bf16"),
                                                 (8, 128, "e4m3"), (4, 96, "bf16")])
 @pytest.mark.parametrize("kernel,wg_per_cu", [(0, 0), (1, 0), (2, 0), (1, 1), (2, 1), (2, 2),
-                                              (1, 3)])
+                                              (3, 1), (3, 2), (1, 3)])
 def test_page_copy_kernels_and_occupancy_match_oracle(gpu, tuning, heads, head_dim, dt,
                                                       kernel, wg_per_cu):
-    """Both one-unit scatter kernels (load-all-then-store, streaming) at
-    every occupancy the launch policy or an override may pick, and the
+    """Both one-unit scatter kernels (load-all-then-store, streaming in
+    either unit order) at every occupancy the launch policy or an override may pick, and the
     gather at the same occupancies: the oracle's bytes, with ragged requests
     and partial last pages (pages of 32, 64, 16 and 12 KiB)."""
     print(f"case: page copy H{heads} D{head_dim} {dt} kernel={kernel} wpc={wg_per_cu}",
