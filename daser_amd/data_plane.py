@@ -79,7 +79,8 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
     delta = new_pos - pos_offset (reference :498-551 for the unrotated part).
     A segment whose store slots lie inside a range already read this step
     (the same cached chunk hit by several requests) reads nothing and
-    scatters from that range; the reference reads it once per request."""
+    scatters from that range; the reference reads it once per request. A
+    block that two loads of the step target receives the later one."""
     ids: list[int] = []
     src: list[np.ndarray] = []
     seg_pages, seg_table, seg_read, reads = [], [], [], []
@@ -116,10 +117,19 @@ def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
             seg_read.append(hit)
             ids.extend(blocks[seg.block_offset:seg.block_offset + n])
     counts = np.asarray(seg_pages, np.int64)
-    return LoadPlan(np.asarray(ids, np.int32),
-                    np.concatenate(src) if src else np.zeros(0, np.int64),
-                    np.repeat(np.asarray(seg_table, np.int32), counts), list(table.keys()),
-                    reads, base, np.repeat(np.asarray(seg_read, np.int64), counts),
+    page_ids = np.asarray(ids, np.int32)
+    src_offs = np.concatenate(src) if src else np.zeros(0, np.int64)
+    rope_idx = np.repeat(np.asarray(seg_table, np.int32), counts)
+    page_read = np.repeat(np.asarray(seg_read, np.int64), counts)
+    # A block listed twice in a step keeps its last load only: the
+    # reference's sequential copies (:536-551) leave the last one's bytes,
+    # while this plan's scatters may run in another order (by read batch).
+    _, last_rev = np.unique(page_ids[::-1], return_index=True)
+    if last_rev.size != page_ids.size:
+        keep = np.sort(page_ids.size - 1 - last_rev)
+        page_ids, src_offs = page_ids[keep], src_offs[keep]
+        rope_idx, page_read = rope_idx[keep], page_read[keep]
+    return LoadPlan(page_ids, src_offs, rope_idx, list(table.keys()), reads, base, page_read,
                     shared_records=shared)
 
 

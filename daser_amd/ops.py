@@ -243,9 +243,11 @@ def dest_order(page_ids, slot_offsets, extra=None):
     """Host tables of a scatter, reordered by destination block (stable).
 
     Processing order does not change the result (each destination block is
-    written once) but near-sequential page writes run faster. Duplicate
-    destination blocks would race inside one launch and are rejected.
-    Device tables are returned unchanged."""
+    written once) but near-sequential page writes run faster. A destination
+    block listed several times keeps only its last entry: the reference's
+    sequential copies (daser_connector.py:536-551) leave the last one's
+    bytes, while copies inside one launch would race. Device tables are
+    returned unchanged (there, duplicates race)."""
     ids = _host_array(page_ids, np.int64)
     offs = _host_array(slot_offsets, np.int64)
     if ids is None or offs is None or ids.size == 0:
@@ -253,7 +255,10 @@ def dest_order(page_ids, slot_offsets, extra=None):
     order = np.argsort(ids, kind="stable")
     sids = ids[order]
     if sids.size > 1 and np.any(sids[1:] == sids[:-1]):
-        raise ValueError("a destination block appears twice in one scatter")
+        # within a run of equal ids the stable order keeps list order: the
+        # run's last element is the list's last entry for that block
+        last = np.append(sids[1:] != sids[:-1], True)
+        order, sids = order[last], sids[last]
     ex = None
     if extra is not None:
         e = _host_array(extra, np.int64)
@@ -516,10 +521,19 @@ def _slots_args(table: LayerTable, slot_mapping, row_offsets, staging, layer0, l
                 raise IndexError("token row outside the staging buffer")
             if np.any(r % 16):
                 raise ValueError("row offsets must be multiples of 16 bytes")
-            if records_written and np.unique(r).size != r.size:
-                raise ValueError("two tokens write the same record row")
-            if not records_written and np.unique(sm[valid]).size != int(valid.sum()):
-                raise ValueError("a destination slot appears twice in one scatter")
+            # Two tokens writing the same record row (gather) or the same
+            # slot (scatter) would race inside the launch; as the reference's
+            # sequential copies leave the last one's bytes, the earlier ones
+            # become padding (slot -1) in a copy of the host table.
+            dest = r if records_written else sm[valid]
+            if np.unique(dest).size != dest.size:
+                idx = np.nonzero(valid)[0]
+                _, last_rev = np.unique(dest[::-1], return_index=True)
+                keep = np.zeros(idx.size, bool)
+                keep[idx.size - 1 - last_rev] = True
+                sm = sm.copy()
+                sm[idx[~keep]] = -1
+                slot_mapping = sm
     sm_d = _as_device_table(slot_mapping, torch.int64, lay.device, "slot_mapping")
     ro_d = _as_device_table(row_offsets, torch.int64, lay.device, "row_offsets")
     if sm_d.numel() != ro_d.numel():

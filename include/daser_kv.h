@@ -156,7 +156,8 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
  * Load scatter: the inverse of dsr_gather. Copies each slot record back into
  * the K and V pages of block page_ids[p] of every layer. A block may appear
  * once per call: pages are copied concurrently, so duplicates race (the
- * Python wrapper rejects them). Listing pages in ascending block order makes
+ * Python wrappers keep only the last entry of a block in host tables, the
+ * bytes the reference's sequential copies leave). Listing pages in ascending block order makes
  * the writes near-sequential and is measurably faster.
  *
  * Replaces the per-(request, slot, layer) copy loop of

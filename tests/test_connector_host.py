@@ -94,6 +94,32 @@ def test_plan_load_reads_a_shared_chunk_once():
     assert not alone.shared_records and len(alone.reads) == 2
 
 
+def test_plan_load_block_targeted_twice_keeps_the_last_load():
+    """The reference's sequential copies leave the last load's bytes in a
+    block that two loads of a step target; the plan keeps that load only,
+    whatever order its read batches scatter in."""
+    reqs = {
+        "x": C.ReqLoadSpec("ka", 5, 2, [3, 9], 5 * SLOT, 32),
+        "y": C.ReqLoadSpec("kb", 20, 2, [9, 4], 20 * SLOT, 32, pos_offset=0, new_pos=64),
+        "z": C.ReqLoadSpec("ka", 5, 2, [4, 11], 5 * SLOT, 32),  # reuses x's read
+    }
+    p = C.plan_load(reqs, SLOT)
+    assert p.page_ids.tolist() == [3, 9, 4, 11]
+    assert p.src_offsets.tolist() == [0, 2 * SLOT, 0, SLOT]
+    assert p.rope_idx.tolist() == [-1, 0, -1, -1]
+    assert p.page_read.tolist() == [0, 1, 0, 0]
+
+
+def test_dest_order_keeps_the_last_entry_of_a_block():
+    from daser_amd import ops
+
+    ids, offs, extra = ops.dest_order([7, 2, 7, 5, 2, 7], [0, 16, 32, 48, 64, 80],
+                                      [1, 2, 3, 4, 5, 6])
+    assert ids.tolist() == [2, 5, 7]
+    assert offs.tolist() == [64, 48, 80]
+    assert extra.tolist() == [5, 4, 6]
+
+
 # ---------------------------------------------------------------- scheduler
 
 

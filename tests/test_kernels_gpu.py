@@ -602,6 +602,41 @@ def test_slots_gather_scatter_match_oracle(gpu, tuning, shape, unroll):
         assert np.array_equal(to_bits_np(d, dt), r)
 
 
+def test_slots_duplicates_keep_the_last_token(gpu):
+    """Host tables in which two tokens target the same cache slot (scatter)
+    or the same record row (gather): the last token's bytes land, as the
+    oracle's sequential loop leaves them; the caller's table is not
+    modified."""
+    print("case: slots duplicates keep the last token", flush=True)
+    shape = KVShape(3, 2, 64, 16, 2)
+    nb = 16
+    caches = rand_caches(shape, nb, "bf16", gpu, seed=61)
+    row = shape.num_heads * shape.head_dim * shape.elem_bytes
+    host = [to_bits_np(c, "bf16") for c in caches]
+    # scatter: tokens 1 and 4 both target slot 37, tokens 2 and 5 slot 40
+    sm = np.array([5, 37, 40, 70, 37, 40, -1, 90], np.int64)
+    ro = np.arange(sm.size, dtype=np.int64) * row
+    sm_before = sm.copy()
+    rng = np.random.default_rng(62)
+    rec = rng.integers(0, 256, size=shape.slot_bytes, dtype=np.uint8)
+    st = torch.from_numpy(rec).to(gpu)
+    ops.scatter_slots(ops.LayerTable(caches), sm, ro, st)
+    oracle.scatter_slots(host, sm, ro, rec, shape.layer_bytes)
+    torch.cuda.synchronize()
+    assert np.array_equal(sm, sm_before)
+    for c, r in zip(caches, host):
+        assert np.array_equal(to_bits_np(c, "bf16"), r)
+    # gather: tokens 0 and 3 write record row 2, tokens 1 and 6 row 5
+    ro2 = np.array([2, 5, 0, 2, 1, 3, 5], np.int64) * row
+    sm2 = np.array([3, 17, 33, 49, 65, 81, 97], np.int64)
+    st2 = torch.zeros(shape.slot_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather_slots(ops.LayerTable(caches), sm2, ro2, st2)
+    ref = np.zeros(shape.slot_bytes, dtype=np.uint8)
+    oracle.gather_slots(host, sm2, ro2, ref, shape.layer_bytes)
+    torch.cuda.synchronize()
+    assert np.array_equal(st2.cpu().numpy(), ref)
+
+
 def test_slots_gather_equals_page_gather_for_full_pages(gpu):
     print("case: slots == pages", flush=True)
     shape = KVShape(4, 8, 128, 16, 2)

@@ -107,21 +107,33 @@ def test_two_chunks_assembled_at_0_and_528(gpu, tmp_path):
     w.shutdown()
 
 
-def test_duplicate_destination_block_raises_on_load(gpu, tmp_path):
-    """Two loads into one block in a step would race inside the scatter
-    launch; the connector rejects them (the reference's sequential copies
-    would let the last one win)."""
-    print("case: positions duplicate destination", flush=True)
+def test_duplicate_destination_blocks_keep_the_last_load(gpu, tmp_path):
+    """Loads of one step that target the same block leave the last one's
+    bytes, as the reference's sequential copies do (daser_connector.py:
+    536-551): x loads chunk A into [3, 9], y chunk B into [9, 4], z chunk A
+    again into [4, 11] (z reuses x's read, so without care it would be
+    scattered before y). Checked against the oracle's sequential scatter of
+    x, y, z."""
+    print("case: positions duplicate destination keeps the last load", flush=True)
     rng = np.random.default_rng(12)
-    toks = rng.integers(0, 30000, size=32).tolist()
-    w = _store_chunks(tmp_path, gpu, [(toks, 5)], seed=43)
+    ta = rng.integers(0, 30000, size=32).tolist()
+    tb = rng.integers(0, 30000, size=32).tolist()
+    w = _store_chunks(tmp_path, gpu, [(ta, 5), (tb, 20)], seed=43)
     w.shutdown()
     w2, _ = _worker(tmp_path)
-    w2.register_kv_caches(_named(rand_caches(SHAPE, NB, "bf16", gpu, seed=1)))
+    fresh = rand_caches(SHAPE, NB, "bf16", gpu, seed=1)
+    ref = [to_bits_np(c, "bf16") for c in fresh]
+    w2.register_kv_caches(_named(fresh))
     slot = SHAPE.slot_bytes
+    loads = {"x": (5, [3, 9]), "y": (20, [9, 4]), "z": (5, [4, 11])}
     w2.bind_connector_metadata(C.DaserConnectorMeta(reqs_to_load={
-        "x": C.ReqLoadSpec("k", 5, 2, [3, 9], 5 * slot, 32),
-        "y": C.ReqLoadSpec("k", 5, 2, [9, 4], 5 * slot, 32)}))
-    with pytest.raises(ValueError, match="appears twice"):
-        w2.start_load_kv(None)
+        r: C.ReqLoadSpec("k" + r, start, 2, blocks, start * slot, 32)
+        for r, (start, blocks) in loads.items()}))
+    w2.start_load_kv(None)
+    torch.cuda.synchronize()
+    for start, blocks in loads.values():
+        recs = _file_records(tmp_path / "daser.store", start, 2).copy()
+        oracle.scatter(ref, blocks, np.arange(2) * slot, recs, SHAPE.layer_bytes)
+    for l, f in enumerate(fresh):
+        assert np.array_equal(to_bits_np(f, "bf16"), ref[l]), f"layer {l}"
     w2.shutdown()
