@@ -67,6 +67,10 @@ struct UnitArgs {
   int32_t hnd_heads = 0;
   int32_t hnd_block = 0;
   int32_t hnd_row_vecs = 0;
+  // Workgroups per unit of the one-unit copies (1, or a power of two whose
+  // share of the page is a whole number of 4 KiB blocks): launches with too
+  // few units to fill the chip split each unit's runs into equal parts.
+  int32_t split = 1;
 };
 
 // Workgroup -> unit. Hardware deals consecutive workgroup ids round-robin

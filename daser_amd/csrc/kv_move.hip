@@ -223,6 +223,26 @@ int copy_wg_per_cu(int64_t page_bytes, int64_t n_units) {
   return w >= 3 ? 0 : (int)(w < 1 ? 1 : w);
 }
 
+// Workgroups per unit of a one-unit gather launch (a layer's save of a
+// serving step moves 16-4,096 pages). Few units leave most CUs idle; split
+// units finish sooner. A part stays a whole number of 4 KiB (one vector per
+// lane). Measured per launch at the Llama-3-8B shape (32 KiB pages, rocprofv3
+// kernel durations, medians of 128 launches; split 1 -> chosen): 16 pages
+// 4.32 -> 3.32 us (8), 64 pages 5.36 -> 4.32 (8), 128 pages 6.16 -> 5.68
+// (4; 8: 6.52), 512 pages 14.5-15.2 -> 13.8 (2), 1,024 pages 26.9-27.5 ->
+// 25.0 (2), 2,048 pages 49.5 -> 46.9 (2), 4,096 pages 93.3 -> 90.8 (2); at
+// 256 pages (7.7-7.8 vs 7.9-8.2) and from 6,144 pages (equal, 4 slower)
+// one workgroup per unit stays. The DSR_TUNE_GATHER_SPLIT override sets it
+// (1: off).
+int gather_split(int64_t page_bytes, int64_t n_units) {
+  int64_t s = tune(DSR_TUNE_GATHER_SPLIT);
+  if (!s)
+    s = n_units <= 64 ? 8 : n_units <= 128 ? 4 : n_units >= 512 && n_units <= 4096 ? 2 : 1;
+  while (s > 1 && (page_bytes % (s * kThreads * 16) != 0 || n_units * s > max_wg_per_launch()))
+    s /= 2;
+  return (int)(s < 1 ? 1 : s);
+}
+
 template <int DT>
 int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipStream_t s,
                     bool kx, unsigned flags, bool hnd = false) {
@@ -378,6 +398,15 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   // kernel measured faster (6.14 vs 5.57 TB/s at 4 KiB pages; 3-8% at 8, 16
   // and 32 KiB).
   const int G = page_bytes < kThreads * 16 ? units_per_group(page_bytes, kGatherUnroll, kMaxGroup) : 1;
+  if (G == 1) {
+    const int split = gather_split(page_bytes, a.n_units);
+    if (split > 1) {
+      a.split = split;
+      const unsigned grid = (unsigned)((a.n_units * split + kXcds - 1) / kXcds * kXcds);
+      kv_gather_kernel<<<grid, kThreads, occupancy_lds(3, 0), (hipStream_t)stream>>>(a);
+      return (int)hipGetLastError();
+    }
+  }
   return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
     const hipStream_t st = (hipStream_t)stream;
     if (G > 1) {

@@ -8,14 +8,19 @@
 
 namespace {
 
-// Gather: one workgroup per (page, layer) unit, XCD-contiguous order.
+// Gather: one workgroup per (page, layer) unit, XCD-contiguous order. With
+// a.split > 1 (launches of few units), a.split consecutive workgroups share
+// a unit, each copying its part of both runs.
 __global__ __launch_bounds__(kThreads) void kv_gather_kernel(UnitArgs a) {
-  const int64_t u = xcd_unit(a.n_units);
+  const int64_t w = xcd_unit(a.n_units * a.split);
+  if (w < 0) return;
+  const int64_t u = w / a.split;
+  const int64_t part = (a.page_bytes / a.split) * (w - u * a.split);
   uint8_t *cache, *rec;
   int l;
-  if (u < 0 || !unit_addresses(a, u, &cache, &rec, &l)) return;
-  copy_halves<kGatherUnroll>(cache, cache + a.kv_stride, rec, rec + a.page_bytes,
-                             a.page_bytes);
+  if (!unit_addresses(a, u, &cache, &rec, &l)) return;
+  copy_halves<kGatherUnroll>(cache + part, cache + a.kv_stride + part, rec + part,
+                             rec + a.page_bytes + part, a.page_bytes / a.split);
 }
 
 // Scatter: one workgroup per unit, layer-major per XCD (the host orders the

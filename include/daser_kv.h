@@ -77,6 +77,8 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
  *                                 hardware dispatch order, 3 the streaming
  *                                 kernel in per-XCD layer-major order
  *                                 (streaming: pages of 16 KiB multiples)
+ *   DSR_TUNE_GATHER_SPLIT         workgroups per (page, layer) unit of a
+ *                                 one-unit page gather (1: no split)
  */
 #define DSR_TUNE_UNITS_PER_GROUP 0
 #define DSR_TUNE_MAX_WG_PER_LAUNCH 1
@@ -88,7 +90,8 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 #define DSR_TUNE_SLOTS_UNROLL 7
 #define DSR_TUNE_COPY_WG_PER_CU 8
 #define DSR_TUNE_SCATTER_KERNEL 9
-#define DSR_TUNE_COUNT_ 10
+#define DSR_TUNE_GATHER_SPLIT 10
+#define DSR_TUNE_COUNT_ 11
 
 #define DSR_OK 0
 #define DSR_ERR_ARG (-1)   /* null pointer, negative count, bad enum     */

@@ -90,6 +90,38 @@ def test_page_copy_kernels_and_occupancy_match_oracle(gpu, tuning, heads, head_d
         assert np.array_equal(to_bits_np(dst[l], dt), dst_ref[l]), f"layer {l}"
 
 
+@pytest.mark.parametrize("heads,dt", [(8, "bf16"), (16, "bf16"), (8, "e4m3"), (1, "bf16")])
+@pytest.mark.parametrize("split", [0, 1, 2, 4, 8])
+@pytest.mark.parametrize("n_pages", [1, 5, 64, 700])
+def test_gather_split_units_match_oracle(gpu, tuning, heads, dt, split, n_pages):
+    """The one-unit gather with each (page, layer) unit shared by several
+    workgroups (launches of few units; split 0 = the launch policy's
+    choice): the oracle's records, for pages of 32, 64, 16 and 4 KiB (the
+    last cannot split) and one or all layers per launch."""
+    print(f"case: gather split={split} H{heads} {dt} pages={n_pages}", flush=True)
+    tuning("gather_split", split)
+    shape = KVShape(3, heads, 128, 16, 1 if dt in FP8 else 2)
+    nb = 2 * n_pages + 3
+    rng = np.random.default_rng(n_pages + heads)
+    ids = rng.permutation(nb)[:n_pages].astype(np.int32)
+    offs = rng.permutation(n_pages).astype(np.int64) * shape.slot_bytes
+    caches = rand_caches(shape, nb, dt, gpu, seed=21)
+    table = ops.LayerTable(caches)
+    host = [to_bits_np(c, dt) for c in caches]
+    ref = np.zeros(n_pages * shape.slot_bytes, dtype=np.uint8)
+    oracle.gather(host, ids, offs, ref, shape.layer_bytes)
+    st = torch.zeros(ref.size, dtype=torch.uint8, device=gpu)
+    ops.gather(table, ids, offs, st)
+    torch.cuda.synchronize()
+    assert np.array_equal(st.cpu().numpy(), ref)
+    st.zero_()
+    pg = ops.PreparedGather(table, ids, offs, st)
+    for l in range(shape.num_layers):
+        pg(l, 1, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(st.cpu().numpy(), ref)
+
+
 def test_device_tables_out_of_range_are_skipped_or_checked(gpu):
     """Device-resident tables are trusted: a page with an out-of-range block
     id or record offset is skipped (nothing written, no fault), the others
