@@ -190,7 +190,18 @@ def _as_device_table(
             raise ValueError(f"{name} must be a contiguous {dtype} tensor")
         return x
     arr = torch.as_tensor(np.asarray(x), dtype=dtype)
-    return arr.to(device, non_blocking=False)
+    return _upload(arr, device)
+
+
+def _upload(arr: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """Host table -> device, stream-ordered on the current stream without
+    blocking the host: copied into pinned memory (torch's caching host
+    allocator keeps it until the copy has run), then an asynchronous copy.
+    A pageable copy would wait for the stream's earlier work, e.g. the
+    store reads that the load's scatter follows."""
+    if device.type != "cuda":
+        return arr.to(device)
+    return arr.pin_memory().to(device, non_blocking=True)
 
 
 def _host_array(x, np_dtype) -> Optional[np.ndarray]:

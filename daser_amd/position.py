@@ -290,7 +290,12 @@ def delta_tables(
     ang = d * inv.reshape(1, -1)
     tab = np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
     t = torch.from_numpy(np.ascontiguousarray(tab))
-    return t.to(device) if device is not None else t
+    if device is None:
+        return t
+    device = torch.device(device)
+    if device.type == "cuda":  # stream-ordered, without blocking the host
+        return t.pin_memory().to(device, non_blocking=True)
+    return t.to(device)
 
 
 def page_rope_index(
