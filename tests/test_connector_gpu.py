@@ -666,3 +666,87 @@ def test_head_major_caches_save_reference_records_and_load(gpu, tmp_path):
     for a, b in zip(*outs):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     w.shutdown()
+
+
+def random_load_reqs(rng, slot: int, n_slots: int, nb: int) -> dict:
+    """Random load metadata of one step: 2-6 requests, flat or with 1-3
+    segments; some segments inside ranges read earlier in the step; some
+    blocks also loaded by the previous request; positions kept or moved."""
+    reqs, used = {}, []
+    for r in range(int(rng.integers(2, 7))):
+        n_seg = int(rng.integers(1, 4))
+        segs, boff = [], 0
+        for _ in range(n_seg):
+            n = int(rng.integers(1, 5))
+            start = int(rng.integers(0, n_slots - n + 1))
+            if used and rng.random() < 0.3:  # inside a range read earlier
+                s0, n0 = used[int(rng.integers(0, len(used)))]
+                n = min(n, n0)
+                start = s0 + int(rng.integers(0, n0 - n + 1))
+            used.append((start, n))
+            pos = int(rng.integers(0, 5000)) if rng.random() < 0.5 else 0
+            new = None if rng.random() < 0.3 else int(rng.integers(0, 20000))
+            segs.append(C.LoadSegment(start, n, boff, pos, new))
+            boff += n
+        blocks = rng.choice(nb, boff, replace=False).tolist()
+        if r and rng.random() < 0.5:  # a block an earlier request also loads
+            prev = reqs[f"r{r - 1}"].block_ids
+            b = prev[int(rng.integers(0, len(prev)))]
+            if b not in blocks:
+                blocks[int(rng.integers(0, boff))] = b
+        s0 = segs[0]
+        if n_seg == 1:
+            reqs[f"r{r}"] = C.ReqLoadSpec(f"k{r}", s0.start_slot, s0.num_slots, blocks,
+                                          s0.start_slot * slot, 16 * boff, s0.pos_offset,
+                                          s0.new_pos)
+        else:
+            reqs[f"r{r}"] = C.ReqLoadSpec(f"k{r}", 0, 0, blocks, 0, 16 * boff, segments=segs)
+    return reqs
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_load_plans_match_the_sequential_oracle(gpu, tmp_path, seed):
+    """Random loads of one step through the data plane: several requests,
+    flat specs and multi-segment ones, segments that reuse ranges read
+    earlier in the step, blocks that several loads target, positions
+    changed or kept; read in one batch or many, by one ring or several.
+    The result equals the reference order applied page by page (request
+    after request, segment after segment: the last load of a block wins),
+    with each page re-rotated by the oracle."""
+    print(f"case: random load plan seed={seed}", flush=True)
+    rng = np.random.default_rng(100 + seed)
+    slot, n_slots, nb, theta = SHAPE.slot_bytes, 40, 48, 500000.0
+    recs_all = torch.randn(n_slots * slot // 2, generator=torch.Generator().manual_seed(seed)
+                           ).to(torch.bfloat16).view(torch.uint8).numpy()
+    store = tmp_path / "daser.store"
+    preallocate_store(str(store), n_slots * slot)
+    with open(store, "r+b") as f:
+        f.write(recs_all.tobytes())
+    reqs = random_load_reqs(rng, slot, n_slots, nb)
+    init = rand_caches(SHAPE, nb, "bf16", gpu, seed=200 + seed)
+    ref = [to_bits_np(c, "bf16") for c in init]
+    for spec in reqs.values():
+        for sg in spec.resolved_segments():
+            new = sg.pos_offset if sg.new_pos is None else sg.new_pos
+            recs = np.ascontiguousarray(
+                recs_all[sg.start_slot * slot:(sg.start_slot + sg.num_slots) * slot])
+            oracle.scatter_rerotate(
+                ref, spec.block_ids[sg.block_offset:sg.block_offset + sg.num_slots],
+                np.arange(sg.num_slots) * slot, recs, SHAPE.layer_bytes, dtype=oracle.BF16,
+                rot_dim=SHAPE.head_dim, style=oracle.NEOX,
+                stored_pos=np.full(sg.num_slots, sg.pos_offset),
+                new_pos=np.full(sg.num_slots, new),
+                rotate=np.full(sg.num_slots, new != sg.pos_offset), theta=theta)
+    for batch, readers in ((1, 1), (1 << 30, 3), (3 * slot, 2)):
+        caches = [c.clone() for c in init]
+        p = C.KVDataPlane(str(store), rope_theta=theta, io_readers=readers,
+                          io_slot_bytes=4096, io_slots=2)
+        p.register(_named(caches))
+        p.load(C.plan_load(reqs, slot), batch_bytes=batch)
+        torch.cuda.synchronize()
+        p.close()
+        for l, c in enumerate(caches):
+            got = to_bits_np(c, "bf16")
+            assert np.array_equal(got[1], ref[l][1]), f"layer {l} V (batch {batch})"
+            ok, msg = oracle.rotation_within_tolerance(got[0], ref[l][0], oracle.BF16)
+            assert ok, f"layer {l} K (batch {batch}): {msg}"

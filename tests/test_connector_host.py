@@ -426,3 +426,22 @@ def test_stalled_store_io_times_out(tmp_path):
         p.load(lp)
     release.set()
     p.close()
+
+
+def test_random_load_plans_cover_shared_reads_and_repeated_blocks():
+    """The random plans of the GPU test (tests/test_connector_gpu.py) do
+    exercise what they are for: over its seeds, segments served by an
+    earlier read, blocks loaded twice in a step, moved and kept positions."""
+    from tests.test_connector_gpu import SHAPE, random_load_reqs
+
+    shared = repeated = moved = kept = 0
+    for seed in range(12):
+        reqs = random_load_reqs(np.random.default_rng(100 + seed), SHAPE.slot_bytes, 40, 48)
+        p = C.plan_load(reqs, SHAPE.slot_bytes)
+        shared += p.shared_records
+        ids = [b for s in reqs.values() for b in s.block_ids]
+        repeated += len(set(ids)) < len(ids)
+        assert np.unique(p.page_ids).size == p.page_ids.size
+        moved += int((p.rope_idx >= 0).any())
+        kept += int((p.rope_idx < 0).any())
+    assert min(shared, repeated, moved, kept) >= 3, (shared, repeated, moved, kept)
