@@ -750,3 +750,40 @@ def test_random_load_plans_match_the_sequential_oracle(gpu, tmp_path, seed):
             assert np.array_equal(got[1], ref[l][1]), f"layer {l} V (batch {batch})"
             ok, msg = oracle.rotation_within_tolerance(got[0], ref[l][0], oracle.BF16)
             assert ok, f"layer {l} K (batch {batch}): {msg}"
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_save_steps_match_the_oracle(gpu, tmp_path, seed):
+    """Random save steps through the worker hooks: 1-5 requests of 1-6
+    pages at random store slots (blocks may repeat across requests), the
+    step saved per layer or deferred, blocking or with async_save, two steps
+    in a row. Every request's records in the file equal the oracle's gather
+    of its blocks, and every chunk is committed."""
+    print(f"case: random save steps seed={seed}", flush=True)
+    rng = np.random.default_rng(300 + seed)
+    mode = ("per_layer", "deferred")[seed % 2]
+    async_save = seed % 3 == 0
+    nb, slot = 40, SHAPE.slot_bytes
+    w, ipc = _worker(tmp_path, save_mode=mode, async_save=async_save)
+    caches = rand_caches(SHAPE, nb, "bf16", gpu, seed=400 + seed)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    host = [to_bits_np(c, "bf16") for c in caches]
+    expect, free = {}, list(rng.permutation(60))
+    for step in range(2):
+        reqs = {}
+        for r in range(int(rng.integers(1, 6))):
+            n = int(rng.integers(1, 7))
+            start = int(free.pop()) * 8  # disjoint 8-slot ranges of the store
+            blocks = rng.choice(nb, n, replace=False).tolist()
+            key = f"k{step}_{r}"
+            reqs[f"s{step}_{r}"] = C.ReqStoreSpec(key, start, n, blocks, start * slot, 16 * n)
+            expect[key] = (start, blocks)
+        _save(w, named, reqs)
+    w.shutdown()  # drains async writes
+    for key, (start, blocks) in expect.items():
+        ref = np.zeros(len(blocks) * slot, dtype=np.uint8)
+        oracle.gather(host, blocks, np.arange(len(blocks)) * slot, ref, SHAPE.layer_bytes)
+        got = _file_records(tmp_path / "daser.store", start, len(blocks))
+        assert np.array_equal(got, ref), key
+    assert sorted(ipc.committed) == sorted(expect)
