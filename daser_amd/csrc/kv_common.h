@@ -67,10 +67,11 @@ struct UnitArgs {
   int32_t hnd_heads = 0;
   int32_t hnd_block = 0;
   int32_t hnd_row_vecs = 0;
-  // Workgroups per unit of the one-unit copies (1, or a power of two whose
-  // share of the page is a whole number of 4 KiB blocks): launches with too
-  // few units to fill the chip split each unit's runs into equal parts.
-  int32_t split = 1;
+  // log2 of the workgroups per unit of the one-unit gather (0: one; else a
+  // power of two whose share of the page is a whole number of 4 KiB
+  // blocks): launches with too few units to fill the chip split each unit's
+  // runs into equal parts.
+  int32_t split_shift = 0;
 };
 
 // Workgroup -> unit. Hardware deals consecutive workgroup ids round-robin
@@ -92,10 +93,13 @@ __device__ __forceinline__ int64_t xcd_unit(int64_t n_units) {
 // page-major order: -1.6% scatter and -1.8% re-rotation time at the
 // Llama-3-8B shapes. Returns the page-major unit index (page * n_layers +
 // layer), or -1 past the end.
+// Unit counts of one launch stay below 2^31 (the entry points check), so
+// the index arithmetic divides in 32 bits: a 64-bit division is a long
+// instruction sequence, paid by every workgroup.
 __device__ __forceinline__ int64_t layer_major_of(int64_t v, int64_t n_units, int n_layers) {
-  const int64_t n_pages = n_units / n_layers;
-  const int64_t l = v / n_pages;
-  return (v - l * n_pages) * n_layers + l;
+  const uint32_t n_pages = (uint32_t)n_units / (uint32_t)n_layers;
+  const uint32_t l = (uint32_t)v / n_pages;
+  return (int64_t)((uint32_t)v - l * n_pages) * n_layers + l;
 }
 __device__ __forceinline__ int64_t layer_major_unit(int64_t n_units, int n_layers) {
   const int64_t v = xcd_unit(n_units);
@@ -122,8 +126,8 @@ __device__ __forceinline__ int64_t layer_major_unit_hw(int64_t n_units, int n_la
 __device__ __forceinline__ bool unit_addresses(const UnitArgs& a, int64_t unit,
                                                uint8_t** cache, uint8_t** rec,
                                                int* layer) {
-  const int64_t p = unit / a.n_layers;
-  const int l = (int)(unit - p * a.n_layers);
+  const uint32_t p = (uint32_t)unit / (uint32_t)a.n_layers;
+  const int l = (int)((uint32_t)unit - p * (uint32_t)a.n_layers);
   const int64_t blk = a.page_ids[p];
   const int64_t off = a.slot_offsets[p] + (int64_t)(a.layer0 + l) * a.layer_bytes;
   if (blk < 0 || blk >= a.num_blocks) return false;

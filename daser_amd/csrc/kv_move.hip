@@ -401,9 +401,9 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   if (G == 1) {
     const int split = gather_split(page_bytes, a.n_units);
     if (split > 1) {
-      a.split = split;
+      a.split_shift = __builtin_ctz((unsigned)split);
       const unsigned grid = (unsigned)((a.n_units * split + kXcds - 1) / kXcds * kXcds);
-      kv_gather_kernel<<<grid, kThreads, occupancy_lds(3, 0), (hipStream_t)stream>>>(a);
+      kv_gather_kernel<true><<<grid, kThreads, occupancy_lds(3, 0), (hipStream_t)stream>>>(a);
       return (int)hipGetLastError();
     }
   }
@@ -413,7 +413,7 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
       kv_copy_grouped_kernel<true, kGatherUnroll><<<grid, kThreads, 0, st>>>(b, G);
     } else {
       const size_t dyn = occupancy_lds(copy_wg_per_cu(page_bytes, b.n_units), 0);
-      kv_gather_kernel<<<grid, kThreads, dyn, st>>>(b);
+      kv_gather_kernel<false><<<grid, kThreads, dyn, st>>>(b);
     }
   });
 }

@@ -8,19 +8,23 @@
 
 namespace {
 
-// Gather: one workgroup per (page, layer) unit, XCD-contiguous order. With
-// a.split > 1 (launches of few units), a.split consecutive workgroups share
-// a unit, each copying its part of both runs.
+// Gather: one workgroup per (page, layer) unit, XCD-contiguous order. The
+// kSplit instance (launches of few units) has 2^split_shift consecutive
+// workgroups share a unit, each copying its part of both runs; it is a
+// separate instance because the split arithmetic cost 1.7% at 4 KiB pages.
+template <bool kSplit>
 __global__ __launch_bounds__(kThreads) void kv_gather_kernel(UnitArgs a) {
-  const int64_t w = xcd_unit(a.n_units * a.split);
+  const int sh = kSplit ? a.split_shift : 0;
+  const int64_t w = xcd_unit(a.n_units << sh);
   if (w < 0) return;
-  const int64_t u = w / a.split;
-  const int64_t part = (a.page_bytes / a.split) * (w - u * a.split);
+  const int64_t u = w >> sh;
+  const int64_t bytes = a.page_bytes >> sh;
+  const int64_t part = kSplit ? bytes * (w & ((1 << sh) - 1)) : 0;
   uint8_t *cache, *rec;
   int l;
   if (!unit_addresses(a, u, &cache, &rec, &l)) return;
   copy_halves<kGatherUnroll>(cache + part, cache + a.kv_stride + part, rec + part,
-                             rec + a.page_bytes + part, a.page_bytes / a.split);
+                             rec + a.page_bytes + part, bytes);
 }
 
 // Scatter: one workgroup per unit, layer-major per XCD (the host orders the
