@@ -93,9 +93,12 @@ __device__ __forceinline__ int64_t xcd_unit(int64_t n_units) {
 // page-major order: -1.6% scatter and -1.8% re-rotation time at the
 // Llama-3-8B shapes. Returns the page-major unit index (page * n_layers +
 // layer), or -1 past the end.
-// Unit counts of one launch stay below 2^31 (the entry points check), so
-// the index arithmetic divides in 32 bits: a 64-bit division is a long
-// instruction sequence, paid by every workgroup.
+// Unit, page and token counts of one launch stay below 2^31 (the entry
+// points check), so the index arithmetic divides in 32 bits: a 64-bit
+// division is a long instruction sequence, paid by every workgroup.
+__device__ __forceinline__ int64_t udiv32(int64_t x, int64_t d) {
+  return (int64_t)((uint32_t)x / (uint32_t)d);
+}
 __device__ __forceinline__ int64_t layer_major_of(int64_t v, int64_t n_units, int n_layers) {
   const uint32_t n_pages = (uint32_t)n_units / (uint32_t)n_layers;
   const uint32_t l = (uint32_t)v / n_pages;

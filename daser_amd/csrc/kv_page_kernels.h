@@ -190,10 +190,10 @@ __device__ __forceinline__ int64_t group_start(const UnitArgs& a, int64_t g, int
                                                int64_t n_pages, int64_t* p0, int* l0) {
   const int64_t v0 = g * G;
   if (kPageMajor) {
-    *p0 = v0 / a.n_layers;
+    *p0 = udiv32(v0, a.n_layers);
     *l0 = (int)(v0 - *p0 * a.n_layers);
   } else {
-    *l0 = (int)(v0 / n_pages);
+    *l0 = (int)udiv32(v0, n_pages);
     *p0 = v0 - (int64_t)*l0 * n_pages;
   }
   return a.n_units - v0 < G ? a.n_units - v0 : G;
@@ -204,9 +204,9 @@ __device__ __forceinline__ int64_t group_start(const UnitArgs& a, int64_t g, int
 // (the cache side of each vector goes through hnd_vec).
 template <bool kGather, int U, bool HND = false>
 __global__ __launch_bounds__(kThreads) void kv_copy_grouped_kernel(UnitArgs a, int G) {
-  const int64_t g = xcd_unit((a.n_units + G - 1) / G);
+  const int64_t g = xcd_unit(udiv32(a.n_units + G - 1, G));
   if (g < 0) return;
-  const int64_t n_pages = a.n_units / a.n_layers;
+  const int64_t n_pages = udiv32(a.n_units, a.n_layers);
   const int nvec = (int)(a.page_bytes >> 4);
   int64_t p0;
   int l0;

@@ -372,7 +372,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
   int l;
   const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
   if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
-  const int64_t p = u / ra.u.n_layers;
+  const int64_t p = udiv32(u, ra.u.n_layers);
   const int ti = rope_table(ra, p, l);
   const int64_t pb = ra.u.page_bytes;
   if (ti < 0) {
@@ -500,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_contig_kernel(Ro
   int l;
   const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
   if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
-  const int64_t p = u / ra.u.n_layers;
+  const int64_t p = udiv32(u, ra.u.n_layers);
   const int ti = rope_table(ra, p, l);
   const int64_t pb = ra.u.page_bytes;
   if (ti < 0) {
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_rows_kernel(RotA
   int l;
   const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
   if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
-  const int64_t p = u / ra.u.n_layers;
+  const int64_t p = udiv32(u, ra.u.n_layers);
   const int ti = rope_table(ra, p, l);
   const int64_t pb = ra.u.page_bytes;
   if (ti < 0) {
@@ -652,7 +652,7 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_lds_kernel(RotAr
   int l;
   const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
   if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
-  const int64_t p = u / ra.u.n_layers;
+  const int64_t p = udiv32(u, ra.u.n_layers);
   const int ti = rope_table(ra, p, l);
   const int64_t pb = ra.u.page_bytes;
   if (ti < 0) {
@@ -732,11 +732,11 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
   constexpr int U = rot_contig_unroll<DT>();
   __shared__ float2 tab[kMaxRotHalf];
   const UnitArgs& a = ra.u;
-  const int64_t ng = (a.n_units + G - 1) / G;
+  const int64_t ng = udiv32(a.n_units + G - 1, G);
   const int64_t g = ra.hw_order ? ((int64_t)blockIdx.x < ng ? (int64_t)blockIdx.x : -1)
                                 : xcd_unit(ng);
   if (g < 0) return;
-  const int64_t n_pages = a.n_units / a.n_layers;
+  const int64_t n_pages = udiv32(a.n_units, a.n_layers);
   const int nvec = (int)(a.page_bytes >> 4);
   int64_t p0;
   int l0;

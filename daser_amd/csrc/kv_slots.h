@@ -30,6 +30,13 @@ struct SlotArgs {
   int32_t block_shift;  // log2(block_size) when a power of two, else -1
 };
 
+// Block of a non-negative slot: a shift for power-of-two block sizes (all
+// of vLLM's), else a 32-bit division where the slot fits.
+__device__ __forceinline__ int64_t slot_block(const SlotArgs& a, int64_t slot) {
+  if (a.block_shift >= 0) return slot >> a.block_shift;
+  return slot < (int64_t)0xffffffffLL ? udiv32(slot, a.block_size) : slot / a.block_size;
+}
+
 constexpr int kTokPerWave = 4;  // tokens whose rows a wave has in flight at once
 constexpr int kTokPerWg = kTokPerWave * (kThreads / kWave);
 constexpr int kRowUnroll = 2;   // 64-vector slices of a row per round
@@ -57,7 +64,7 @@ __global__ __launch_bounds__(kThreads) void kv_slots_kernel(SlotArgs a) {
     unit = layer_major_unit(nu, a.n_layers);
     if (unit < 0) return;
   }
-  const int64_t tb = unit / a.n_layers;
+  const int64_t tb = udiv32(unit, a.n_layers);
   const int l = (int)(unit - tb * a.n_layers);
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int vpr = (int)(a.row_bytes >> 4);
@@ -68,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void kv_slots_kernel(SlotArgs a) {
     ck[j] = cv[j] = rk[j] = rv[j] = make_rsrc(a.staging, 0);
     if (t < a.n_tokens) {
       const int64_t slot = a.slot_mapping[t];
-      const int64_t blk = slot >= 0 ? slot / a.block_size : -1;
+      const int64_t blk = slot >= 0 ? slot_block(a, slot) : -1;
       const int64_t off = a.row_offsets[t] + (int64_t)(a.layer0 + l) * a.layer_bytes;
       if (blk >= 0 && blk < a.num_blocks && off >= 0 &&
           off + a.page_bytes + a.row_bytes <= a.staging_bytes) {
@@ -125,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void kv_slots_small_kernel(SlotArgs a) {
     unit = layer_major_unit(nu, a.n_layers);
     if (unit < 0) return;
   }
-  const int64_t tb = unit / a.n_layers;
+  const int64_t tb = udiv32(unit, a.n_layers);
   const int l = (int)(unit - tb * a.n_layers);
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
   const int lane = (int)threadIdx.x % kWave;
@@ -136,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void kv_slots_small_kernel(SlotArgs a) {
   const int64_t t = t0 + lane;
   const bool live = lane < TPW && t < a.n_tokens;
   const int64_t slot = live ? a.slot_mapping[t] : -1;
-  const int64_t blk = slot < 0 ? -1 : a.block_shift >= 0 ? slot >> a.block_shift : slot / a.block_size;
+  const int64_t blk = slot < 0 ? -1 : slot_block(a, slot);
   const int64_t in_blk = slot - blk * a.block_size;
   const int64_t off = live ? a.row_offsets[t] + (int64_t)(a.layer0 + l) * a.layer_bytes : -1;
   const bool ok = blk >= 0 && blk < a.num_blocks && off >= 0 &&
@@ -193,7 +200,7 @@ __global__ __launch_bounds__(kThreads, 4) void kv_slots_packed_kernel(SlotArgs a
     unit = layer_major_unit(nu, a.n_layers);
     if (unit < 0) return;
   }
-  const int64_t tb = unit / a.n_layers;
+  const int64_t tb = udiv32(unit, a.n_layers);
   const int l = (int)(unit - tb * a.n_layers);
   const int wave = (int)threadIdx.x / kWave, lane = (int)threadIdx.x % kWave;
   const int64_t vo = (int64_t)(lane & ((1 << s) - 1)) << 4;
@@ -261,7 +268,7 @@ void kv_slots_rerotate_kernel(SlotArgs a, RotArgs ra) {
   const int64_t nu = ((int64_t)a.n_tokens + kTokPerWg - 1) / kTokPerWg * a.n_layers;
   const int64_t unit = layer_major_unit(nu, a.n_layers);
   if (unit < 0) return;
-  const int64_t tb = unit / a.n_layers;
+  const int64_t tb = udiv32(unit, a.n_layers);
   const int l = (int)(unit - tb * a.n_layers);
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int vpr = (int)(a.row_bytes >> 4);
@@ -282,7 +289,7 @@ void kv_slots_rerotate_kernel(SlotArgs a, RotArgs ra) {
       const int64_t slot = a.slot_mapping[t];
       const int64_t ro = a.row_offsets[t];
       const int r = ra.rope_idx[t];
-      const int64_t blk = slot >= 0 ? slot / a.block_size : -1;
+      const int64_t blk = slot >= 0 ? slot_block(a, slot) : -1;
       const int64_t off = ro + (int64_t)(a.layer0 + l) * a.layer_bytes;
       if (blk >= 0 && blk < a.num_blocks && off >= 0 &&
           off + a.page_bytes + a.row_bytes <= a.staging_bytes) {
