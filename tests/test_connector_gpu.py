@@ -704,27 +704,48 @@ def random_load_reqs(rng, slot: int, n_slots: int, nb: int) -> dict:
     return reqs
 
 
-@pytest.mark.parametrize("seed", range(12))
+def _head_major(caches):
+    """The same logical caches stored heads-first (vLLM's HND layout)."""
+    out = []
+    for c in caches:
+        _, nb, bs, h, d = c.shape
+        m = torch.empty((2, nb, h, bs, d), dtype=c.dtype, device=c.device)
+        v = m.permute(0, 1, 3, 2, 4)
+        v.copy_(c)
+        out.append(v)
+    return out
+
+
+@pytest.mark.parametrize("seed", range(16))
 def test_random_load_plans_match_the_sequential_oracle(gpu, tmp_path, seed):
     """Random loads of one step through the data plane: several requests,
     flat specs and multi-segment ones, segments that reuse ranges read
     earlier in the step, blocks that several loads target, positions
-    changed or kept; read in one batch or many, by one ring or several.
+    changed or kept; read in one batch or many, by one ring or several;
+    token-major or head-major caches, bf16 or e4m3 (per-layer K scales).
     The result equals the reference order applied page by page (request
     after request, segment after segment: the last load of a block wins),
     with each page re-rotated by the oracle."""
-    print(f"case: random load plan seed={seed}", flush=True)
+    layout, dt = (("nhd", "bf16"), ("hnd", "bf16"), ("nhd", "e4m3"), ("hnd", "e4m3"))[seed % 4]
+    print(f"case: random load plan seed={seed} {layout} {dt}", flush=True)
     rng = np.random.default_rng(100 + seed)
-    slot, n_slots, nb, theta = SHAPE.slot_bytes, 40, 48, 500000.0
-    recs_all = torch.randn(n_slots * slot // 2, generator=torch.Generator().manual_seed(seed)
-                           ).to(torch.bfloat16).view(torch.uint8).numpy()
+    shape = SHAPE if dt == "bf16" else KVShape(3, 2, 64, 16, 1)
+    slot, n_slots, nb, theta = shape.slot_bytes, 40, 48, 500000.0
+    gen = torch.Generator().manual_seed(seed)
+    if dt == "bf16":
+        recs_all = torch.randn(n_slots * slot // 2, generator=gen).to(torch.bfloat16)
+    else:
+        recs_all = (torch.randn(n_slots * slot, generator=gen) * 40).to(torch.float8_e4m3fn)
+    recs_all = recs_all.view(torch.uint8).numpy()
     store = tmp_path / "daser.store"
     preallocate_store(str(store), n_slots * slot)
     with open(store, "r+b") as f:
         f.write(recs_all.tobytes())
     reqs = random_load_reqs(rng, slot, n_slots, nb)
-    init = rand_caches(SHAPE, nb, "bf16", gpu, seed=200 + seed)
-    ref = [to_bits_np(c, "bf16") for c in init]
+    init = rand_caches(shape, nb, dt, gpu, seed=200 + seed, scale=1.0 if dt == "bf16" else 40.0)
+    ref = [to_bits_np(c, dt) for c in init]
+    scales = np.array([0.02, 0.05, 0.11], np.float32)
+    kind = oracle.BF16 if dt == "bf16" else oracle.E4M3
     for spec in reqs.values():
         for sg in spec.resolved_segments():
             new = sg.pos_offset if sg.new_pos is None else sg.new_pos
@@ -732,23 +753,28 @@ def test_random_load_plans_match_the_sequential_oracle(gpu, tmp_path, seed):
                 recs_all[sg.start_slot * slot:(sg.start_slot + sg.num_slots) * slot])
             oracle.scatter_rerotate(
                 ref, spec.block_ids[sg.block_offset:sg.block_offset + sg.num_slots],
-                np.arange(sg.num_slots) * slot, recs, SHAPE.layer_bytes, dtype=oracle.BF16,
-                rot_dim=SHAPE.head_dim, style=oracle.NEOX,
+                np.arange(sg.num_slots) * slot, recs, shape.layer_bytes, dtype=kind,
+                rot_dim=shape.head_dim, style=oracle.NEOX,
                 stored_pos=np.full(sg.num_slots, sg.pos_offset),
                 new_pos=np.full(sg.num_slots, new),
-                rotate=np.full(sg.num_slots, new != sg.pos_offset), theta=theta)
+                rotate=np.full(sg.num_slots, new != sg.pos_offset), theta=theta,
+                k_scale=scales if dt != "bf16" else None)
     for batch, readers in ((1, 1), (1 << 30, 3), (3 * slot, 2)):
         caches = [c.clone() for c in init]
+        if layout == "hnd":
+            caches = _head_major(caches)
         p = C.KVDataPlane(str(store), rope_theta=theta, io_readers=readers,
-                          io_slot_bytes=4096, io_slots=2)
+                          io_slot_bytes=4096, io_slots=2,
+                          k_scales=torch.from_numpy(scales).to(gpu) if dt != "bf16" else None)
         p.register(_named(caches))
+        assert p.table.layout.k_layout == layout
         p.load(C.plan_load(reqs, slot), batch_bytes=batch)
         torch.cuda.synchronize()
         p.close()
         for l, c in enumerate(caches):
-            got = to_bits_np(c, "bf16")
+            got = to_bits_np(c.contiguous(), dt)
             assert np.array_equal(got[1], ref[l][1]), f"layer {l} V (batch {batch})"
-            ok, msg = oracle.rotation_within_tolerance(got[0], ref[l][0], oracle.BF16)
+            ok, msg = oracle.rotation_within_tolerance(got[0], ref[l][0], kind)
             assert ok, f"layer {l} K (batch {batch}): {msg}"
 
 
