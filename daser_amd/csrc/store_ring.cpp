@@ -379,7 +379,7 @@ int dsr_ring_write(dsr_ring* r, const void* src, int64_t nbytes, int64_t file_of
   }
   for (int s = 0; s < r->n_slots; ++s)
     if (r->state[s] == kCopying) {  // copies issued but never written (error path)
-      if (!r->host) hipEventSynchronize(r->ev[s]);
+      if (!r->host) (void)hipEventSynchronize(r->ev[s]);  // already failing: best effort
       r->state[s] = kFree;
     }
   if (err < 0) {
@@ -485,12 +485,12 @@ int dsr_ring_close(dsr_ring* r) {
     if (r->host || r->direct)
       free(p);
     else
-      hipHostFree(p);
+      (void)hipHostFree(p);
   }
   for (hipEvent_t e : r->ev)
-    if (e) hipEventDestroy(e);
-  if (r->ready) hipEventDestroy(r->ready);
-  if (r->stream) hipStreamDestroy(r->stream);
+    if (e) (void)hipEventDestroy(e);
+  if (r->ready) (void)hipEventDestroy(r->ready);
+  if (r->stream) (void)hipStreamDestroy(r->stream);
   if (r->fd >= 0) ::close(r->fd);
   delete r;
   return rc;
