@@ -201,6 +201,10 @@ def _upload(arr: torch.Tensor, device: torch.device) -> torch.Tensor:
     store reads that the load's scatter follows."""
     if device.type != "cuda":
         return arr.to(device)
+    if torch.cuda.is_current_stream_capturing():
+        # a captured copy would replay from a pinned buffer torch reuses
+        raise ValueError("host index tables cannot be used under graph capture: pass "
+                         "device tensors")
     return arr.pin_memory().to(device, non_blocking=True)
 
 

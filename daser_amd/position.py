@@ -294,6 +294,9 @@ def delta_tables(
         return t
     device = torch.device(device)
     if device.type == "cuda":  # stream-ordered, without blocking the host
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError("delta tables cannot be built under graph capture (the copy "
+                             "would replay from a reused pinned buffer): build them before")
         return t.pin_memory().to(device, non_blocking=True)
     return t.to(device)
 

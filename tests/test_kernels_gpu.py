@@ -948,6 +948,12 @@ def test_hip_graph_capture_and_replay(gpu):
         for i, (a, b) in enumerate(zip(got, want)):
             assert torch.equal(a, b), f"replay {rep}, output {i}"
     assert want[0].any() and want[1].any() and want[-1].any()
+    # host tables under capture are refused: their upload would be replayed
+    # from a pinned buffer that torch reuses
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(ValueError, match="graph capture"):
+        with torch.cuda.graph(g2):
+            ops.gather(table_s, wl.page_ids, wl.slot_offsets, st)
 
 
 def _random_cases(n, seed):
