@@ -30,6 +30,9 @@ wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry), ``io_reade
 (rings reading a load in parallel, default 4), ``io_timeout_s`` (a blocking
 store read or write raises TimeoutError after this long, default 120 as in
 the reference; None: wait forever),
+``store_path`` may hold ``{rank}``, replaced by the worker's tensor-parallel
+rank (one store file per rank; the reference's single path would make ranks
+overwrite each other's records at the same offsets),
 ``io_backend`` ("native": the C++ io_uring ring of libdaser_kv, default;
 "direct": the same ring with the store file opened O_DIRECT;
 "python": the threaded ring of store_io.PinnedRingIO), ``k_scale`` (one K
@@ -82,7 +85,7 @@ from daser_amd.data_plane import (  # noqa: E402
 
 __all__ = ["DaserConnector", "DaserConnectorMeta", "KVDataPlane", "LoadPlan", "LoadSegment",
            "ReqLoadSpec", "ReqStoreSpec", "StorePlan", "hash_tokens", "load_spec",
-           "place_chunks", "plan_load", "plan_store"]
+           "place_chunks", "plan_load", "plan_store", "rank_store_path"]
 
 
 def hash_tokens(tokens: list[int]) -> str:
@@ -226,6 +229,30 @@ class _BgLoop:
         self.thread.join(timeout=5)
 
 
+def _tp_rank() -> int:
+    """This worker's tensor-parallel rank: vLLM's, when vLLM is running it,
+    else LOCAL_RANK / RANK from the environment, else 0."""
+    try:
+        from vllm.distributed.parallel_state import get_tensor_model_parallel_rank  # type: ignore
+
+        return int(get_tensor_model_parallel_rank())
+    except Exception:  # vLLM absent or its groups not initialised
+        import os
+
+        return int(os.environ.get("LOCAL_RANK", os.environ.get("RANK", "0")))
+
+
+def rank_store_path(path: str, rank: Optional[int] = None) -> str:
+    """``store_path`` with ``{rank}`` replaced by the tensor-parallel rank.
+    Under tensor parallelism every rank saves its own heads' records at the
+    same slot offsets, so ranks need one store file each; the reference
+    keeps one path for all ranks. A path without the placeholder is used as
+    given."""
+    if "{rank}" not in path:
+        return path
+    return path.replace("{rank}", str(_tp_rank() if rank is None else rank))
+
+
 def _default_ipc(kind: str, socket_path: str):
     """The reference's IPC clients, when its package is importable."""
     from daser.connector.ipc_client import IPCClientAsync, IPCClientSync  # type: ignore
@@ -276,6 +303,7 @@ class DaserConnector(KVConnectorBase_V1):
                                       else None),
                 "k_layout": extra.get("kv_layout"),
             }
+            self._store_path = rank_store_path(self._store_path)
             self._plane = KVDataPlane(
                 self._store_path,
                 rope_theta=float(extra.get("rope_theta", hf_theta or 10000.0)),

@@ -813,3 +813,25 @@ def test_random_save_steps_match_the_oracle(gpu, tmp_path, seed):
         got = _file_records(tmp_path / "daser.store", start, len(blocks))
         assert np.array_equal(got, ref), key
     assert sorted(ipc.committed) == sorted(expect)
+
+
+def test_store_path_per_rank(gpu, tmp_path, monkeypatch):
+    """A store_path with {rank}: the worker of tensor-parallel rank 1 writes
+    its records to its own file, in the reference's layout."""
+    print("case: connector per-rank store file", flush=True)
+    monkeypatch.setenv("LOCAL_RANK", "1")
+    cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(kv_connector_extra_config=dict(
+        store_path=str(tmp_path / "daser.{rank}.store"), io_slot_mb=0.03125, io_slots=3)))
+    w = C.DaserConnector(cfg, C.KVConnectorRole.WORKER, ipc_async=FakeAsyncIPC())
+    caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=44)
+    named = _named(caches)
+    w.register_kv_caches(named)
+    _save(w, named, _store_reqs())
+    w.shutdown()
+    assert (tmp_path / "daser.1.store").exists() and not (tmp_path / "daser.{rank}.store").exists()
+    host = [to_bits_np(c, "bf16") for c in caches]
+    ref = np.zeros(3 * SHAPE.slot_bytes, dtype=np.uint8)
+    oracle.gather(host, [5, 9, 2], np.arange(3) * SHAPE.slot_bytes, ref, SHAPE.layer_bytes)
+    with open(tmp_path / "daser.1.store", "rb") as f:
+        f.seek(3 * SHAPE.slot_bytes)
+        assert np.array_equal(np.frombuffer(f.read(ref.size), np.uint8), ref)

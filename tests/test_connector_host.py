@@ -445,3 +445,15 @@ def test_random_load_plans_cover_shared_reads_and_repeated_blocks():
         moved += int((p.rope_idx >= 0).any())
         kept += int((p.rope_idx < 0).any())
     assert min(shared, repeated, moved, kept) >= 3, (shared, repeated, moved, kept)
+
+
+def test_rank_store_path(monkeypatch):
+    """One store file per tensor-parallel rank when the path asks for it;
+    the rank comes from vLLM when it runs the worker, else the environment."""
+    assert C.rank_store_path("/s/daser.store") == "/s/daser.store"
+    assert C.rank_store_path("/s/daser.{rank}.store", 3) == "/s/daser.3.store"
+    monkeypatch.setenv("LOCAL_RANK", "5")
+    assert C.rank_store_path("/s/r{rank}/daser.store") == "/s/r5/daser.store"
+    monkeypatch.delenv("LOCAL_RANK")
+    monkeypatch.setenv("RANK", "2")
+    assert C.rank_store_path("/s/{rank}") == "/s/2"
