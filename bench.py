@@ -25,7 +25,8 @@ cost of the connector's worker hooks on serving-shaped steps; neither is
 `value`.
 
 Usage: python bench.py [--steps K] [--warmup W] [--configs 2,3,4,5,6] [--no-cpu]
-                       [--no-ref-loop] [--io] [--serving] [--patterns] [--calibrate]
+                       [--no-ref-loop] [--io] [--serving] [--patterns] [--shapes]
+                       [--calibrate]
 """
 
 from __future__ import annotations
@@ -641,6 +642,73 @@ def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int 
     return out
 
 
+# Cache shapes of other model families (layers, KV heads, head_dim, block size,
+# element bytes), for --shapes: page sizes from 4 to 96 KiB and head_dim 64
+# to 256, each with its own kernel choices.
+MODEL_SHAPES = [
+    ("qwen2-0.5b", (24, 2, 64, 16, 2)),
+    ("llama-3.2-1b", (16, 8, 64, 16, 2)),
+    ("qwen2.5-7b", (28, 4, 128, 16, 2)),
+    ("llama-3-8b", (32, 8, 128, 16, 2)),
+    ("llama-3-8b bs32", (32, 8, 128, 32, 2)),
+    ("gemma-2-9b", (42, 8, 256, 16, 2)),
+    ("phi-3-mini", (32, 32, 96, 16, 2)),
+    ("llama-3-70b tp8", (80, 1, 128, 16, 2)),
+    ("llama-3-8b e4m3", (32, 8, 128, 16, 1)),
+]
+
+
+def bench_shapes(torch, ops, position, dev, payload: int = 16 << 30, steps: int = 3) -> dict:
+    """Gather, scatter and the fused re-rotating scatter (every request moved
+    by its own delta) at the cache shapes of other model families: ragged
+    requests (U[256, 4096] tokens) on a permuted pool, about ``payload``
+    bytes of records per pass. GB/s = 2P / mean HIP-event kernel time."""
+    from daser_amd import workloads
+
+    out = {}
+    for name, dims in MODEL_SHAPES:
+        shape = workloads.KVShape(*dims)
+        tok_bytes = shape.slot_bytes // shape.block_size
+        n_req = max(1, int(payload // tok_bytes // 2176))
+        wl = workloads.ragged(shape, n_req, 256, 4096, seed=17, pool_slack=1.05)
+        fp8 = shape.elem_bytes == 1
+        full, caches, k_scale = fill_caches(torch, shape, wl.num_blocks,
+                                            "fp8" if fp8 else "bf16", dev, seed=5)
+        table = ops.LayerTable(caches)
+        st = torch.empty(wl.staging_bytes, dtype=torch.uint8, device=dev)
+        g_ids = torch.from_numpy(wl.page_ids.astype(np.int32)).to(dev)
+        g_offs = torch.from_numpy(wl.slot_offsets).to(dev)
+        rng = np.random.default_rng(3)
+        ridx, uniq = position.page_rope_index(wl.req_pages,
+                                              rng.integers(1, 32768, len(wl.req_pages)).tolist())
+        tabs = position.delta_tables(uniq, shape.head_dim, THETA, device=dev)
+        s_ids, s_offs, s_ridx = ops.dest_order(wl.page_ids, wl.slot_offsets, ridx)
+        s_ids = torch.from_numpy(s_ids.astype(np.int32)).to(dev)
+        s_offs = torch.from_numpy(s_offs).to(dev)
+        s_ridx = torch.from_numpy(s_ridx.astype(np.int32)).to(dev)
+        runs = {"gather": lambda: ops.gather(table, g_ids, g_offs, st),
+                "scatter": lambda: ops.scatter(table, s_ids, s_offs, st),
+                "rerotate": lambda: ops.scatter_rerotate(table, s_ids, s_offs, st, tabs, s_ridx,
+                                                         k_scale=k_scale)}
+        P = wl.n_pages * shape.slot_bytes
+        res = {"page_KiB": shape.page_bytes // 1024, "pages": wl.n_pages,
+               "payload_GB": round(P / 1e9, 2)}
+        for k, fn in runs.items():
+            fn()
+            t = Timer(torch)
+            for _ in range(steps):
+                with t:
+                    fn()
+            torch.cuda.synchronize()
+            res[f"{k}_GBps"] = round(2 * P / (t.mean_ms() * 1e-3) / 1e9, 1)
+        res["rerotate_tokens_per_s"] = round(wl.tokens / (2 * P / (res["rerotate_GBps"] * 1e9)))
+        out[name] = res
+        log(f"[bench] shapes: {name}: {json.dumps(res)}")
+        del full, caches, table, st
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_patterns(torch, ops, dev, reps: int = 5) -> dict:
     """The same bytes as config 2 (P = 17,742 pages x 2 MiB records) moved in
     other patterns, for scale: torch's own kernels for a plain sequential
@@ -874,6 +942,9 @@ def main() -> int:
                     help="also time config 2's bytes in other patterns: torch's copy_, "
                          "index_copy_ and index_select, and this library's kernels over "
                          "the identity page list")
+    ap.add_argument("--shapes", action="store_true",
+                    help="also time gather, scatter and re-rotation at the cache shapes "
+                         "of other model families (MODEL_SHAPES)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 4 GiB device copy (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -994,6 +1065,9 @@ def main() -> int:
         log("[bench] patterns: config 2's bytes in other access patterns")
         out["patterns"] = bench_patterns(torch, ops, dev)
         log(f"[bench] patterns: {json.dumps(out['patterns'])}")
+    if args.shapes:
+        log("[bench] shapes: other model families' caches")
+        out["shapes"] = bench_shapes(torch, ops, position, dev)
     if args.io:
         log("[bench] io: PCIe/file-inclusive save and load")
         out["pcie_inclusive"] = bench_io(torch, dev)

@@ -46,7 +46,8 @@ DSR_REROTATE_SHARED_RECORDS = DSR_SHARED_RECORDS
 # dsr_set_tuning knobs (measurements and tests only)
 TUNE = {"units_per_group": 0, "max_wg_per_launch": 1, "rot_kernel": 2, "rot_wg_per_cu": 3,
         "rot_grouped_wg_per_cu": 4, "slots_tpw": 5, "slots_kernel": 6, "slots_unroll": 7,
-        "copy_wg_per_cu": 8, "scatter_kernel": 9, "gather_split": 10}
+        "copy_wg_per_cu": 8, "scatter_kernel": 9, "gather_split": 10,
+        "page_parts": 11}
 ROT_KERNEL_CODES = {"auto": 0, "pairs": 1, "contig": 2, "grouped": 3}
 
 _P = ctypes.c_void_p

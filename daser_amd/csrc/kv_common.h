@@ -67,11 +67,11 @@ struct UnitArgs {
   int32_t hnd_heads = 0;
   int32_t hnd_block = 0;
   int32_t hnd_row_vecs = 0;
-  // log2 of the workgroups per unit of the one-unit gather (0: one; else a
-  // power of two whose share of the page is a whole number of 4 KiB
-  // blocks): launches with too few units to fill the chip split each unit's
-  // runs into equal parts.
-  int32_t split_shift = 0;
+  // Workgroups per unit of the one-unit gather and streaming scatter (1, or
+  // a count whose share of the page is a whole number of 4 KiB blocks):
+  // pages above 32 KiB, and launches with too few units to fill the chip,
+  // split each unit's two runs into equal parts.
+  int32_t parts = 1;
 };
 
 // Workgroup -> unit. Hardware deals consecutive workgroup ids round-robin

@@ -128,7 +128,8 @@ int64_t items_per_launch(int n_layers, int64_t per_wg) {
 // launch error.
 template <class F>
 int launch_page_ranges(const UnitArgs& a, int n_pages, int G, F launch) {
-  const int64_t per = items_per_launch(a.n_layers, G);
+  // a.parts workgroups per unit (the split kernels) count as a.parts units
+  const int64_t per = items_per_launch(a.n_layers * a.parts, G);
   if (per <= 0) return DSR_ERR_ARG;
   for (int64_t p0 = 0; p0 < n_pages; p0 += per) {
     const int64_t n = n_pages - p0 < per ? n_pages - p0 : per;
@@ -136,7 +137,8 @@ int launch_page_ranges(const UnitArgs& a, int n_pages, int G, F launch) {
     b.page_ids += p0;
     b.slot_offsets += p0;
     b.n_units = n * a.n_layers;
-    const unsigned grid = (unsigned)(((b.n_units + G - 1) / G + kXcds - 1) / kXcds * kXcds);
+    const unsigned grid =
+        (unsigned)(((b.n_units * a.parts + G - 1) / G + kXcds - 1) / kXcds * kXcds);
     launch(b, grid);
     const int rc = (int)hipGetLastError();
     if (rc != 0) return rc;
@@ -243,6 +245,18 @@ int gather_split(int64_t page_bytes, int64_t n_units) {
   return (int)(s < 1 ? 1 : s);
 }
 
+// Parts of a page above 32 KiB for the one-unit gather and the streaming
+// scatter: 32 KiB each (the copies' tuned unit; a workgroup's later rounds
+// would wait for its earlier stores, since vmcnt counts both). The
+// DSR_TUNE_PAGE_PARTS override sets it (1: whole pages).
+constexpr int64_t kPartBytes = 32 << 10;
+int page_parts(int64_t page_bytes) {
+  if (const int64_t t = tune(DSR_TUNE_PAGE_PARTS))
+    return page_bytes % (t * kThreads * 16) == 0 ? (int)t : 1;
+  return page_bytes > kPartBytes && page_bytes % kPartBytes == 0 ? (int)(page_bytes / kPartBytes)
+                                                                 : 1;
+}
+
 template <int DT>
 int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipStream_t s,
                     bool kx, unsigned flags, bool hnd = false) {
@@ -276,11 +290,20 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
   // The grouped kernel also serves pages of exactly U vectors per lane
   // (G = 1), for 16-bit K. The DSR_TUNE_ROT_KERNEL override (contig, grouped) changes the
   // choice where both apply, for in-process comparisons.
-  const int64_t nvec = ra.u.page_bytes >> 4;
-  const bool single = contig && nvec % kThreads == 0 &&
-                      nvec == (int64_t)rot_contig_unroll<DT>() * kThreads;
+  // 16-bit token-major pages above 32 KiB run the grouped kernel's single-
+  // unit path on 32 KiB parts, one workgroup each (the DSR_TUNE_PAGE_PARTS
+  // override 1 keeps whole pages on the contig kernel)
+  const int64_t part_vecs = (int64_t)rot_contig_unroll<DT>() * kThreads;
+  const int64_t row_bytes = (int64_t)ra.row_vecs * 16;
+  int parts = 1;
+  if (contig && !kx && !hnd && !is_fp8<DT>() && tune(DSR_TUNE_PAGE_PARTS) != 1 &&
+      (ra.u.page_bytes >> 4) > part_vecs && (ra.u.page_bytes >> 4) % part_vecs == 0 &&
+      (part_vecs * 16) % row_bytes == 0)
+    parts = (int)((ra.u.page_bytes >> 4) / part_vecs);
+  const int64_t nvec = (ra.u.page_bytes >> 4) / parts;
+  const bool single = contig && nvec % kThreads == 0 && nvec == part_vecs;
   bool grouped = G > 1 || (single && !is_fp8<DT>());
-  if (rot_kernel == kRotContig && contig) grouped = false;
+  if (rot_kernel == kRotContig && contig && parts == 1) grouped = false;
   if (rot_kernel == kRotGrouped && (G > 1 || single)) grouped = true;
   if (grouped) {
     wg = G > 1 ? rot_grouped_wg_per_cu<DT>()
@@ -292,7 +315,9 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
   // units per workgroup of the kernel actually launched: the one-unit
   // kernels (an override may pick contig where G > 1) take one
   const int GL = grouped ? G : 1;
-  return launch_page_ranges(ra.u, n_pages, GL, [&](const UnitArgs& b, unsigned grid) {
+  UnitArgs ua = ra.u;
+  ua.parts = grouped ? parts : 1;
+  return launch_page_ranges(ua, n_pages, GL, [&](const UnitArgs& b, unsigned grid) {
     RotArgs rb = ra;
     rb.u = b;
     // one unit per workgroup over distinct records: the whole chip on one
@@ -398,22 +423,26 @@ int dsr_gather(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   // kernel measured faster (6.14 vs 5.57 TB/s at 4 KiB pages; 3-8% at 8, 16
   // and 32 KiB).
   const int G = page_bytes < kThreads * 16 ? units_per_group(page_bytes, kGatherUnroll, kMaxGroup) : 1;
+  int split = 1;
   if (G == 1) {
-    const int split = gather_split(page_bytes, a.n_units);
-    if (split > 1) {
-      a.split_shift = __builtin_ctz((unsigned)split);
-      const unsigned grid = (unsigned)((a.n_units * split + kXcds - 1) / kXcds * kXcds);
-      kv_gather_kernel<true><<<grid, kThreads, occupancy_lds(3, 0), (hipStream_t)stream>>>(a);
-      return (int)hipGetLastError();
-    }
+    const int pp = page_parts(page_bytes);
+    split = gather_split(page_bytes / pp, a.n_units * pp);
+    a.parts = pp * split;
   }
   return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
     const hipStream_t st = (hipStream_t)stream;
     if (G > 1) {
       kv_copy_grouped_kernel<true, kGatherUnroll><<<grid, kThreads, 0, st>>>(b, G);
     } else {
-      const size_t dyn = occupancy_lds(copy_wg_per_cu(page_bytes, b.n_units), 0);
-      kv_gather_kernel<false><<<grid, kThreads, dyn, st>>>(b);
+      // launches split for lack of units keep the registers' three
+      // workgroups per CU (they end before a steady state)
+      const int64_t wus = b.n_units * b.parts;  // workgroup-sized units
+      const size_t dyn =
+          occupancy_lds(split > 1 ? 3 : copy_wg_per_cu(page_bytes / b.parts, wus), 0);
+      if (b.parts > 1)
+        kv_gather_kernel<true><<<grid, kThreads, dyn, st>>>(b);
+      else
+        kv_gather_kernel<false><<<grid, kThreads, dyn, st>>>(b);
     }
   });
 }
@@ -433,6 +462,23 @@ int dsr_scatter_ex(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
   // Grouped up to 4 KiB pages (6.47 vs 5.04 TB/s at 4 KiB); at 8-32 KiB the
   // one-unit kernel measured equal or faster.
   const int G = page_bytes <= kThreads * 16 ? units_per_group(page_bytes, kScatterUnroll, kMaxGroup) : 1;
+  // records read by several pages are partly served by the caches, so
+  // more bytes in flight pay (the 70B share's 64 shared chunks: 50.5 ms at
+  // the registers' 3 workgroups per CU vs 52.6 ms at one)
+  const bool shared = (flags & DSR_SHARED_RECORDS) && !tune(DSR_TUNE_COPY_WG_PER_CU);
+  // the streaming kernel moves pages above 32 KiB as 32 KiB parts, one
+  // workgroup each; U vectors per lane per round (8 for multiples of 32 KiB,
+  // 4 for 16 KiB multiples)
+  const int pp = G == 1 && !shared ? page_parts(page_bytes) : 1;
+  const int64_t part_bytes = page_bytes / pp;
+  const int su = part_bytes % (kThreads * 8 * 16) == 0 ? 8
+                 : part_bytes % (kThreads * 4 * 16) == 0 ? 4 : 0;
+  const int64_t pick = tune(DSR_TUNE_SCATTER_KERNEL);
+  const int wpc_part = shared ? 0 : copy_wg_per_cu(part_bytes, a.n_units * pp);
+  const int64_t kind = pick ? pick : wpc_part == 1 && su == 8 ? 2 : 1;
+  const bool stream_k = G == 1 && (kind == 2 || kind == 3) && su != 0;
+  if (stream_k) a.parts = pp;
+  const int wpc = stream_k ? wpc_part : shared ? 0 : copy_wg_per_cu(page_bytes, a.n_units);
   return launch_page_ranges(a, n_pages, G, [&](const UnitArgs& b, unsigned grid) {
     const hipStream_t st = (hipStream_t)stream;
     if (G > 1) {
@@ -442,28 +488,26 @@ int dsr_scatter_ex(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
       kv_copy_grouped_kernel<false, kScatterUnroll><<<grid, kThreads, occupancy_lds(3, 0), st>>>(b, G);
       return;
     }
-    // records read by several pages are partly served by the caches, so
-    // more bytes in flight pay (the 70B share's 64 shared chunks: 50.5 ms at
-    // the registers' 3 workgroups per CU vs 52.6 ms at one)
-    const int wpc = (flags & DSR_SHARED_RECORDS) && !tune(DSR_TUNE_COPY_WG_PER_CU)
-                        ? 0 : copy_wg_per_cu(page_bytes, b.n_units);
     const size_t dyn = occupancy_lds(wpc, 0);
-    // streaming kernel: U vectors per lane per round (8 for pages of
-    // multiples of 32 KiB, 4 for 16 KiB multiples)
-    const int64_t pick = tune(DSR_TUNE_SCATTER_KERNEL);
-    const int su = page_bytes % (kThreads * 8 * 16) == 0 ? 8
-                   : page_bytes % (kThreads * 4 * 16) == 0 ? 4 : 0;
-    const int64_t kind = pick ? pick : wpc == 1 && su == 8 ? 2 : 1;
-    if (kind == 2 && su == 8)
-      kv_scatter_stream_kernel<8, true><<<grid, kThreads, dyn, st>>>(b);
-    else if (kind == 2 && su == 4)
-      kv_scatter_stream_kernel<4, true><<<grid, kThreads, dyn, st>>>(b);
-    else if (kind == 3 && su == 8)
-      kv_scatter_stream_kernel<8, false><<<grid, kThreads, dyn, st>>>(b);
-    else if (kind == 3 && su == 4)
-      kv_scatter_stream_kernel<4, false><<<grid, kThreads, dyn, st>>>(b);
-    else
+    const bool hw = kind == 2, split = b.parts > 1;
+    if (!stream_k)
       kv_scatter_kernel<<<grid, kThreads, dyn, st>>>(b);
+    else if (su == 8 && hw && split)
+      kv_scatter_stream_kernel<8, true, true><<<grid, kThreads, dyn, st>>>(b);
+    else if (su == 8 && hw)
+      kv_scatter_stream_kernel<8, true><<<grid, kThreads, dyn, st>>>(b);
+    else if (su == 8 && split)
+      kv_scatter_stream_kernel<8, false, true><<<grid, kThreads, dyn, st>>>(b);
+    else if (su == 8)
+      kv_scatter_stream_kernel<8, false><<<grid, kThreads, dyn, st>>>(b);
+    else if (hw && split)
+      kv_scatter_stream_kernel<4, true, true><<<grid, kThreads, dyn, st>>>(b);
+    else if (hw)
+      kv_scatter_stream_kernel<4, true><<<grid, kThreads, dyn, st>>>(b);
+    else if (split)
+      kv_scatter_stream_kernel<4, false, true><<<grid, kThreads, dyn, st>>>(b);
+    else
+      kv_scatter_stream_kernel<4, false><<<grid, kThreads, dyn, st>>>(b);
   });
 }
 

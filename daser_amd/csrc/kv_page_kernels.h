@@ -9,17 +9,16 @@
 namespace {
 
 // Gather: one workgroup per (page, layer) unit, XCD-contiguous order. The
-// kSplit instance (launches of few units) has 2^split_shift consecutive
-// workgroups share a unit, each copying its part of both runs; it is a
-// separate instance because the split arithmetic cost 1.7% at 4 KiB pages.
+// kSplit instance has a.parts consecutive workgroups share a unit, each
+// copying its part of both runs; it is a separate instance because the
+// split arithmetic cost 1.7% at 4 KiB pages.
 template <bool kSplit>
 __global__ __launch_bounds__(kThreads) void kv_gather_kernel(UnitArgs a) {
-  const int sh = kSplit ? a.split_shift : 0;
-  const int64_t w = xcd_unit(a.n_units << sh);
+  const int64_t w = xcd_unit(kSplit ? a.n_units * a.parts : a.n_units);
   if (w < 0) return;
-  const int64_t u = w >> sh;
-  const int64_t bytes = a.page_bytes >> sh;
-  const int64_t part = kSplit ? bytes * (w & ((1 << sh) - 1)) : 0;
+  const int64_t u = kSplit ? udiv32(w, a.parts) : w;
+  const int64_t bytes = kSplit ? a.page_bytes / a.parts : a.page_bytes;
+  const int64_t part = kSplit ? bytes * (w - u * a.parts) : 0;
   uint8_t *cache, *rec;
   int l;
   if (!unit_addresses(a, u, &cache, &rec, &l)) return;
@@ -49,21 +48,32 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_kernel(UnitArgs a) {
 // 12.60 ms, 11.98 vs 12.08, 11.97 vs 12.09 for kv_scatter_kernel at its
 // register-limited 3 workgroups per CU; kv_scatter_kernel itself at one
 // workgroup per CU 12.54-12.56 ms. Units in hardware dispatch order
-// (kHwOrder, layer_major_unit_hw): a further 3.5%. U = 4 serves 16 KiB
+// (kHwOrder): a further 3.5%. Pages above 32 KiB go as 32 KiB parts, one
+// workgroup each (kSplit): a workgroup's second round waits for its first
+// round's stores (vmcnt counts both), and parts measured 13% faster at 64
+// KiB pages (Llama-3-8B with block_size 32: 5.10 vs 5.75 ms). U = 4 serves 16 KiB
 // pages (e4m3) for measurements: at two workgroups per CU it measured
 // 23.0-23.6 ms at config 4 in three processes on one box against
 // 21.8-24.0 ms for kv_scatter_kernel, the spread being the buffers'
 // placement, so the default stays kv_scatter_kernel there.
-template <int U, bool kHwOrder>
+template <int U, bool kHwOrder, bool kSplit = false>
 __global__ __launch_bounds__(kThreads) void kv_scatter_stream_kernel(UnitArgs a) {
   uint8_t *cache, *rec;
   int l;
-  const int64_t u = kHwOrder ? layer_major_unit_hw(a.n_units, a.n_layers)
-                             : layer_major_unit(a.n_units, a.n_layers);
-  if (u < 0 || !unit_addresses(a, u, &cache, &rec, &l)) return;
-  const int64_t pb = a.page_bytes;
-  const rsrc_t sk = make_rsrc(rec, pb), sv = make_rsrc(rec + pb, pb);
-  const rsrc_t dk = make_rsrc(cache, pb), dv = make_rsrc(cache + a.kv_stride, pb);
+  // kSplit: a.parts consecutive workgroups share a unit (pages above 32
+  // KiB: one round of U vectors per lane each), as consecutive units of the
+  // same order
+  const int64_t nw = kSplit ? a.n_units * a.parts : a.n_units;
+  const int64_t b = kHwOrder ? ((int64_t)blockIdx.x < nw ? (int64_t)blockIdx.x : -1)
+                             : xcd_unit(nw);
+  if (b < 0) return;
+  const int64_t v = kSplit ? udiv32(b, a.parts) : b;
+  const int64_t u = layer_major_of(v, a.n_units, a.n_layers);
+  if (!unit_addresses(a, u, &cache, &rec, &l)) return;
+  const int64_t pb = kSplit ? a.page_bytes / a.parts : a.page_bytes;
+  const int64_t part = kSplit ? pb * (b - v * a.parts) : 0;
+  const rsrc_t sk = make_rsrc(rec + part, pb), sv = make_rsrc(rec + a.page_bytes + part, pb);
+  const rsrc_t dk = make_rsrc(cache + part, pb), dv = make_rsrc(cache + a.kv_stride + part, pb);
   const int nvec = (int)(pb >> 4);
   for (int base = threadIdx.x; base < nvec; base += kThreads * U) {
     u32x4 xk[U], xv[U];

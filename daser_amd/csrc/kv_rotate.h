@@ -732,12 +732,17 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
   constexpr int U = rot_contig_unroll<DT>();
   __shared__ float2 tab[kMaxRotHalf];
   const UnitArgs& a = ra.u;
-  const int64_t ng = udiv32(a.n_units + G - 1, G);
-  const int64_t g = ra.hw_order ? ((int64_t)blockIdx.x < ng ? (int64_t)blockIdx.x : -1)
-                                : xcd_unit(ng);
-  if (g < 0) return;
+  // a.parts > 1 (with G = 1, token-major pages): a.parts consecutive
+  // workgroups share a unit, each moving one part of its K and V runs
+  const int64_t ng = udiv32(a.n_units * a.parts + G - 1, G);
+  const int64_t gw = ra.hw_order ? ((int64_t)blockIdx.x < ng ? (int64_t)blockIdx.x : -1)
+                                 : xcd_unit(ng);
+  if (gw < 0) return;
+  const int64_t g = a.parts > 1 ? udiv32(gw, a.parts) : gw;
+  const int64_t pbytes = a.parts > 1 ? a.page_bytes / a.parts : a.page_bytes;
+  const int64_t pofs = a.parts > 1 ? pbytes * (gw - g * a.parts) : 0;
   const int64_t n_pages = udiv32(a.n_units, a.n_layers);
-  const int nvec = (int)(a.page_bytes >> 4);
+  const int nvec = (int)(pbytes >> 4);
   int64_t p0;
   int l0;
   const int64_t n_here = group_start<false>(a, g, G, n_pages, &p0, &l0);
@@ -758,10 +763,11 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_grouped_kernel(R
     koff[k] = KX ? kx_phys(ra, off[k] >> 4) << 4 : off[k];
     coff[k] = HND ? hnd_vec(a, off[k] >> 4) << 4 : koff[k];
     const UnitRsrc u = unit_rsrc<false>(a, n_pages, p0, l0, j, n_here);
-    rk[k] = bload(make_rsrc(u.rec, u.n), koff[k]);
-    rv[k] = bload(make_rsrc(u.rec + a.page_bytes, u.n), off[k]);
-    kd[k] = make_rsrc(u.cache, u.n);
-    vd[k] = make_rsrc(u.cache + a.kv_stride, u.n);
+    const int64_t un = u.n ? pbytes : 0;
+    rk[k] = bload(make_rsrc(u.rec + pofs, un), koff[k]);
+    rv[k] = bload(make_rsrc(u.rec + a.page_bytes + pofs, un), off[k]);
+    kd[k] = make_rsrc(u.cache + pofs, un);
+    vd[k] = make_rsrc(u.cache + a.kv_stride + pofs, un);
     tj[k] = u.n && rope_table(ra, u.p, u.l) >= 0 ? j : -1;
     sc[k] = is_fp8<DT>() && u.n ? ra.k_scale[a.layer0 + u.l] : 1.0f;
   }

@@ -79,6 +79,10 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
  *                                 (streaming: pages of 16 KiB multiples)
  *   DSR_TUNE_GATHER_SPLIT         workgroups per (page, layer) unit of a
  *                                 one-unit page gather (1: no split)
+ *   DSR_TUNE_PAGE_PARTS           parts (one workgroup each) of a page in
+ *                                 the one-unit gather and streaming scatter
+ *                                 (1: whole pages; default: 32 KiB parts of
+ *                                 larger pages)
  */
 #define DSR_TUNE_UNITS_PER_GROUP 0
 #define DSR_TUNE_MAX_WG_PER_LAUNCH 1
@@ -91,7 +95,8 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 #define DSR_TUNE_COPY_WG_PER_CU 8
 #define DSR_TUNE_SCATTER_KERNEL 9
 #define DSR_TUNE_GATHER_SPLIT 10
-#define DSR_TUNE_COUNT_ 11
+#define DSR_TUNE_PAGE_PARTS 11
+#define DSR_TUNE_COUNT_ 12
 
 #define DSR_OK 0
 #define DSR_ERR_ARG (-1)   /* null pointer, negative count, bad enum     */
