@@ -317,6 +317,23 @@ int launch_rerotate(const RotArgs& ra, int n_pages, int style, bool vec_ok, hipS
   const int GL = grouped ? G : 1;
   UnitArgs ua = ra.u;
   ua.parts = grouped ? parts : 1;
+  if (!grouped && !contig && rows_ok) {
+    // the row-aligned kernel on large pages: parts of whole rows near 32 KiB
+    const int64_t pbytes = ra.u.page_bytes;
+    int best = 1;
+    if (const int64_t t = tune(DSR_TUNE_PAGE_PARTS)) {
+      if (pbytes % t == 0 && (pbytes / t) % row_bytes == 0) best = (int)t;
+    } else if (pbytes > kPartBytes) {
+      int64_t bd = pbytes - kPartBytes;
+      for (int q = 2; q <= 8; ++q) {
+        const int64_t pt = pbytes / q;
+        if (pbytes % q || pt % row_bytes || pt < (16 << 10)) continue;
+        const int64_t d = pt > kPartBytes ? pt - kPartBytes : kPartBytes - pt;
+        if (d < bd) bd = d, best = q;
+      }
+    }
+    ua.parts = best;
+  }
   return launch_page_ranges(ua, n_pages, GL, [&](const UnitArgs& b, unsigned grid) {
     RotArgs rb = ra;
     rb.u = b;

@@ -370,17 +370,28 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_kernel(RotArgs r
   __shared__ float2 tab[kMaxRotHalf];
   uint8_t *cache, *rec;
   int l;
-  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
-  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  // ra.u.parts consecutive workgroups share a unit (large pages), each
+  // moving a part of whole rows of both runs
+  const int parts = ra.u.parts;
+  const int64_t w = xcd_unit(ra.u.n_units * parts);
+  if (w < 0) return;
+  const int64_t vu = parts > 1 ? udiv32(w, parts) : w;
+  const int64_t u = layer_major_of(vu, ra.u.n_units, ra.u.n_layers);
+  if (!unit_addresses(ra.u, u, &cache, &rec, &l)) return;
   const int64_t p = udiv32(u, ra.u.n_layers);
   const int ti = rope_table(ra, p, l);
-  const int64_t pb = ra.u.page_bytes;
+  const int64_t pb = ra.u.page_bytes / parts;
+  const int64_t po = pb * (w - vu * parts);
+  uint8_t* const vrec = rec + ra.u.page_bytes + po;
+  uint8_t* const vcache = cache + ra.u.kv_stride + po;
+  rec += po;
+  cache += po;
   if (ti < 0) {
-    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    copy_halves<kRotCopyUnroll>(rec, vrec, cache, vcache, pb);
     return;
   }
   const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
-  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const rsrc_t vs = make_rsrc(vrec, pb), vd = make_rsrc(vcache, pb);
   const int nvec = (int)(pb >> 4);
   const int row_bytes = ra.row_vecs << 4;
   const int ntask = (int)(pb / row_bytes) * ra.tasks_per_row;
@@ -561,17 +572,28 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_rows_kernel(RotA
   __shared__ float2 tab[kMaxRotHalf];
   uint8_t *cache, *rec;
   int l;
-  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
-  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  // ra.u.parts consecutive workgroups share a unit (large pages), each
+  // moving a part of whole rows of both runs
+  const int parts = ra.u.parts;
+  const int64_t w = xcd_unit(ra.u.n_units * parts);
+  if (w < 0) return;
+  const int64_t vu = parts > 1 ? udiv32(w, parts) : w;
+  const int64_t u = layer_major_of(vu, ra.u.n_units, ra.u.n_layers);
+  if (!unit_addresses(ra.u, u, &cache, &rec, &l)) return;
   const int64_t p = udiv32(u, ra.u.n_layers);
   const int ti = rope_table(ra, p, l);
-  const int64_t pb = ra.u.page_bytes;
+  const int64_t pb = ra.u.page_bytes / parts;
+  const int64_t po = pb * (w - vu * parts);
+  uint8_t* const vrec = rec + ra.u.page_bytes + po;
+  uint8_t* const vcache = cache + ra.u.kv_stride + po;
+  rec += po;
+  cache += po;
   if (ti < 0) {
-    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    copy_halves<kRotCopyUnroll>(rec, vrec, cache, vcache, pb);
     return;
   }
   const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
-  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const rsrc_t vs = make_rsrc(vrec, pb), vd = make_rsrc(vcache, pb);
   const int nvec = (int)(pb >> 4);
   const int rv = ra.row_vecs;
   const int rpw = kWave / rv;
@@ -650,17 +672,28 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_rerotate_lds_kernel(RotAr
   __shared__ float2 tab[kMaxRotHalf];
   uint8_t *cache, *rec;
   int l;
-  const int64_t u = layer_major_unit(ra.u.n_units, ra.u.n_layers);
-  if (u < 0 || !unit_addresses(ra.u, u, &cache, &rec, &l)) return;
+  // ra.u.parts consecutive workgroups share a unit (large pages), each
+  // moving a part of whole rows of both runs
+  const int parts = ra.u.parts;
+  const int64_t w = xcd_unit(ra.u.n_units * parts);
+  if (w < 0) return;
+  const int64_t vu = parts > 1 ? udiv32(w, parts) : w;
+  const int64_t u = layer_major_of(vu, ra.u.n_units, ra.u.n_layers);
+  if (!unit_addresses(ra.u, u, &cache, &rec, &l)) return;
   const int64_t p = udiv32(u, ra.u.n_layers);
   const int ti = rope_table(ra, p, l);
-  const int64_t pb = ra.u.page_bytes;
+  const int64_t pb = ra.u.page_bytes / parts;
+  const int64_t po = pb * (w - vu * parts);
+  uint8_t* const vrec = rec + ra.u.page_bytes + po;
+  uint8_t* const vcache = cache + ra.u.kv_stride + po;
+  rec += po;
+  cache += po;
   if (ti < 0) {
-    copy_halves<kRotCopyUnroll>(rec, rec + pb, cache, cache + ra.u.kv_stride, pb);
+    copy_halves<kRotCopyUnroll>(rec, vrec, cache, vcache, pb);
     return;
   }
   const rsrc_t ks = make_rsrc(rec, pb), kd = make_rsrc(cache, pb);
-  const rsrc_t vs = make_rsrc(rec + pb, pb), vd = make_rsrc(cache + ra.u.kv_stride, pb);
+  const rsrc_t vs = make_rsrc(vrec, pb), vd = make_rsrc(vcache, pb);
   const int nvec = (int)(pb >> 4);
   {
     VRound<kRotCopyUnroll> v;  // V: a plain copy

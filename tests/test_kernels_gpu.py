@@ -1608,3 +1608,54 @@ def test_hnd_rerotate_unsupported_width_refused(gpu):
     tabs = position.delta_tables([5], 96, device=gpu)
     with pytest.raises(DaserKVError):  # 96-dim neox rows: partners 6 vectors apart
         ops.scatter_rerotate(ops.LayerTable(caches), [1], [0], st, tabs, [0])
+
+
+@pytest.mark.parametrize("H,D,bs,style,parts", [
+    (8, 128, 32, "neox", 0), (8, 256, 16, "neox", 0), (8, 128, 32, "gptj", 0),
+    (32, 96, 16, "neox", 0), (32, 96, 16, "neox", 2), (8, 128, 32, "neox", 1),
+    (8, 128, 48, "neox", 0)])
+def test_large_pages_in_parts_match_oracle(gpu, tuning, H, D, bs, style, parts):
+    """Pages above 32 KiB move in parts of whole rows, one workgroup each:
+    the gather, the streaming scatter, the grouped re-rotation (64 KiB
+    pages) and the row-aligned re-rotation (head_dim 96, 96 KiB pages) give
+    the oracle's bytes and rotation (parts 0 = the launch policy's choice,
+    1 = whole pages; 96 KiB pages at block_size 48)."""
+    print(f"case: large pages H{H} D{D} bs{bs} {style} parts={parts}", flush=True)
+    if parts:
+        tuning("page_parts", parts)
+    shape = KVShape(3, H, D, bs, 2)
+    wl = workloads.ragged(shape, 5, 30, 900, seed=H + D + bs, pool_slack=1.2)
+    caches = rand_caches(shape, wl.num_blocks, "bf16", gpu, seed=71)
+    table = ops.LayerTable(caches)
+    host = _np_layers(caches, "bf16")
+    ref = np.zeros(wl.staging_bytes, dtype=np.uint8)
+    oracle.gather(host, wl.page_ids, wl.slot_offsets, ref, shape.layer_bytes)
+    st = torch.zeros(wl.staging_bytes, dtype=torch.uint8, device=gpu)
+    ops.gather(table, wl.page_ids, wl.slot_offsets, st)
+    torch.cuda.synchronize()
+    assert np.array_equal(st.cpu().numpy(), ref)
+    rng = np.random.default_rng(5)
+    dst_ids = rng.permutation(wl.num_blocks)[:wl.n_pages].astype(np.int32)
+    deltas = rng.integers(-3000, 30000, size=len(wl.req_pages)) * (rng.random(len(wl.req_pages)) < 0.8)
+    ridx, uniq = position.page_rope_index(wl.req_pages, deltas)
+    tabs = position.delta_tables(uniq or [0], D, 500000.0, device=gpu)
+    dst = [torch.zeros_like(c) for c in caches]
+    rot = [torch.zeros_like(c) for c in caches]
+    ops.scatter(ops.LayerTable(dst), dst_ids, wl.slot_offsets, st)
+    ops.scatter_rerotate(ops.LayerTable(rot), dst_ids, wl.slot_offsets, st, tabs, ridx,
+                         style=style)
+    dref = [np.zeros_like(h) for h in host]
+    oracle.scatter(dref, dst_ids, wl.slot_offsets, ref, shape.layer_bytes)
+    rref = [np.zeros_like(h) for h in host]
+    d = np.repeat(np.asarray(deltas, np.int64), wl.req_pages)
+    oracle.scatter_rerotate(rref, dst_ids, wl.slot_offsets, ref, shape.layer_bytes,
+                            dtype=oracle.BF16, rot_dim=D, style=0 if style == "neox" else 1,
+                            stored_pos=np.zeros(wl.n_pages, np.int64), new_pos=d, rotate=d != 0,
+                            theta=500000.0)
+    torch.cuda.synchronize()
+    for l in range(shape.num_layers):
+        assert np.array_equal(to_bits_np(dst[l], "bf16"), dref[l]), f"scatter layer {l}"
+        got = to_bits_np(rot[l], "bf16")
+        assert np.array_equal(got[1], rref[l][1]), f"V layer {l}"
+        ok, msg = rotation_within_tolerance(got[0], rref[l][0], "bf16")
+        assert ok, f"K layer {l}: {msg}"
