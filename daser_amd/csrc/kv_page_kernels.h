@@ -38,9 +38,9 @@ __global__ __launch_bounds__(kThreads) void kv_scatter_kernel(UnitArgs a) {
                               a.page_bytes);
 }
 
-// Scatter of pages of 32 KiB and up, launched at one workgroup per CU (the
-// launch policy keeps about 64 KiB of each CU's units in flight; see
-// copy_wg_per_cu in kv_move.hip). Each lane keeps U (8 at 32 KiB)
+// Scatter of pages of 32 KiB and up (larger ones in 32 KiB parts),
+// launched at one workgroup per CU (the launch policy keeps about 64 KiB of
+// each CU's units in flight; see copy_wg_per_cu in kv_move.hip). Each lane keeps U (8 at 32 KiB)
 // vectors of K and of V in flight, and every store follows its own load's
 // arrival (no wait for the whole round): at one workgroup per CU the waves
 // stream instead of alternating a load burst with a store burst. Measured
