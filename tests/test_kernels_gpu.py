@@ -1613,16 +1613,19 @@ def test_hnd_rerotate_unsupported_width_refused(gpu):
 @pytest.mark.parametrize("H,D,bs,style,parts", [
     (8, 128, 32, "neox", 0), (8, 256, 16, "neox", 0), (8, 128, 32, "gptj", 0),
     (32, 96, 16, "neox", 0), (32, 96, 16, "neox", 2), (8, 128, 32, "neox", 1),
-    (8, 128, 48, "neox", 0)])
+    (8, 128, 48, "neox", 0), (8, 128, 32, "neox", -64), (32, 96, 16, "neox", -64)])
 def test_large_pages_in_parts_match_oracle(gpu, tuning, H, D, bs, style, parts):
     """Pages above 32 KiB move in parts of whole rows, one workgroup each:
     the gather, the streaming scatter, the grouped re-rotation (64 KiB
     pages) and the row-aligned re-rotation (head_dim 96, 96 KiB pages) give
     the oracle's bytes and rotation (parts 0 = the launch policy's choice,
-    1 = whole pages; 96 KiB pages at block_size 48)."""
+    1 = whole pages; 96 KiB pages at block_size 48; -n: the policy's parts
+    with launches cut to n workgroups, so one call runs as many launches)."""
     print(f"case: large pages H{H} D{D} bs{bs} {style} parts={parts}", flush=True)
-    if parts:
+    if parts > 0:
         tuning("page_parts", parts)
+    elif parts < 0:
+        tuning("max_wg_per_launch", -parts)
     shape = KVShape(3, H, D, bs, 2)
     wl = workloads.ragged(shape, 5, 30, 900, seed=H + D + bs, pool_slack=1.2)
     caches = rand_caches(shape, wl.num_blocks, "bf16", gpu, seed=71)
