@@ -21,10 +21,12 @@
 // Kernel choice, by page and row geometry (all inside the entry points):
 //   gather / scatter: one unit per workgroup; pages of at most 4 KiB
 //     (scatter) or under 4 KiB (gather) take several units per workgroup
-//     (kv_copy_grouped_kernel).
+//     (kv_copy_grouped_kernel); pages above 32 KiB take one workgroup per
+//     32 KiB part, and gathers of few units split their units further.
 //   re-rotation: kv_scatter_rerotate_grouped_kernel for pages below U * 4
-//     KiB and 16-bit pages of exactly U * 4 KiB; kv_scatter_rerotate_contig_
-//     kernel for larger pages with a power-of-two partner distance;
+//     KiB and 16-bit pages of exactly U * 4 KiB (and 16-bit token-major pages
+//     of several such parts, one workgroup each); kv_scatter_rerotate_contig_
+//     kernel for other larger pages with a power-of-two partner distance;
 //     kv_scatter_rerotate_rows_kernel for other neox rows of <= 64 vectors;
 //     the pair-task kv_scatter_rerotate_kernel otherwise; rotary widths that
 //     are not whole 16-byte vectors: kv_scatter_rerotate_lds_kernel.
