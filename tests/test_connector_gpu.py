@@ -716,31 +716,59 @@ def _head_major(caches):
     return out
 
 
-@pytest.mark.parametrize("seed", range(16))
+def _to_split_x(c):
+    """Token-major (2, NB, bs, H, D) caches as vLLM's 3-D PagedAttention caches
+    (2, NB, bs * H * D), K and V pages both in the split-x order
+    [H][D / X][bs][X] (a byte permutation of each page; only K's order
+    matters to the kernels, V is moved as bytes)."""
+    _, nb, bs, h, d = c.shape
+    x = 16 // c.element_size()
+    return (c.view(2, nb, bs, h, d // x, x).permute(0, 1, 3, 4, 2, 5).contiguous()
+            .view(2, nb, bs * h * d))
+
+
+def _from_split_x(c, bs, h, d):
+    x = 16 // c.element_size()
+    nb = c.shape[1]
+    return c.view(2, nb, h, d // x, bs, x).permute(0, 1, 4, 2, 3, 5).reshape(2, nb, bs, h, d)
+
+
+@pytest.mark.parametrize("seed", range(18))
 def test_random_load_plans_match_the_sequential_oracle(gpu, tmp_path, seed):
     """Random loads of one step through the data plane: several requests,
     flat specs and multi-segment ones, segments that reuse ranges read
     earlier in the step, blocks that several loads target, positions
     changed or kept; read in one batch or many, by one ring or several;
-    token-major or head-major caches, bf16 or e4m3 (per-layer K scales).
-    The result equals the reference order applied page by page (request
-    after request, segment after segment: the last load of a block wins),
-    with each page re-rotated by the oracle."""
-    layout, dt = (("nhd", "bf16"), ("hnd", "bf16"), ("nhd", "e4m3"), ("hnd", "e4m3"))[seed % 4]
+    token-major, head-major or 3-D split-x caches, bf16 or e4m3 (per-layer
+    K scales). The result equals the reference order applied page by page
+    (request after request, segment after segment: the last load of a block
+    wins), with each page re-rotated by the oracle."""
+    layout = ("nhd", "hnd", "kx")[seed % 3]
+    dt = ("bf16", "e4m3")[(seed // 3) % 2]
     print(f"case: random load plan seed={seed} {layout} {dt}", flush=True)
     rng = np.random.default_rng(100 + seed)
     shape = SHAPE if dt == "bf16" else KVShape(3, 2, 64, 16, 1)
+    bs, h, d = shape.block_size, shape.num_heads, shape.head_dim
     slot, n_slots, nb, theta = shape.slot_bytes, 40, 48, 500000.0
     gen = torch.Generator().manual_seed(seed)
     if dt == "bf16":
-        recs_all = torch.randn(n_slots * slot // 2, generator=gen).to(torch.bfloat16)
+        recs_t = torch.randn(n_slots * slot // 2, generator=gen).to(torch.bfloat16)
     else:
-        recs_all = (torch.randn(n_slots * slot, generator=gen) * 40).to(torch.float8_e4m3fn)
-    recs_all = recs_all.view(torch.uint8).numpy()
+        recs_t = (torch.randn(n_slots * slot, generator=gen) * 40).to(torch.float8_e4m3fn)
+    # the file holds records of the caches' own layout; the oracle works on
+    # token-major pages, so split-x records are read through the inverse order
+    file_recs = recs_t.view(torch.uint8).numpy()
+    if layout == "kx":
+        x = 16 // recs_t.element_size()
+        recs_all = (recs_t.view(n_slots, shape.num_layers, 2, h, d // x, bs, x)
+                    .permute(0, 1, 2, 5, 3, 4, 6).contiguous().view(torch.uint8).numpy()
+                    .reshape(-1))
+    else:
+        recs_all = file_recs
     store = tmp_path / "daser.store"
     preallocate_store(str(store), n_slots * slot)
     with open(store, "r+b") as f:
-        f.write(recs_all.tobytes())
+        f.write(file_recs.tobytes())
     reqs = random_load_reqs(rng, slot, n_slots, nb)
     init = rand_caches(shape, nb, dt, gpu, seed=200 + seed, scale=1.0 if dt == "bf16" else 40.0)
     ref = [to_bits_np(c, dt) for c in init]
@@ -754,17 +782,21 @@ def test_random_load_plans_match_the_sequential_oracle(gpu, tmp_path, seed):
             oracle.scatter_rerotate(
                 ref, spec.block_ids[sg.block_offset:sg.block_offset + sg.num_slots],
                 np.arange(sg.num_slots) * slot, recs, shape.layer_bytes, dtype=kind,
-                rot_dim=shape.head_dim, style=oracle.NEOX,
+                rot_dim=d, style=oracle.NEOX,
                 stored_pos=np.full(sg.num_slots, sg.pos_offset),
                 new_pos=np.full(sg.num_slots, new),
                 rotate=np.full(sg.num_slots, new != sg.pos_offset), theta=theta,
                 k_scale=scales if dt != "bf16" else None)
     for batch, readers in ((1, 1), (1 << 30, 3), (3 * slot, 2)):
         caches = [c.clone() for c in init]
+        geometry = None
         if layout == "hnd":
             caches = _head_major(caches)
+        elif layout == "kx":
+            caches = [_to_split_x(c) for c in caches]
+            geometry = {"block_size": bs, "head_dim": d}
         p = C.KVDataPlane(str(store), rope_theta=theta, io_readers=readers,
-                          io_slot_bytes=4096, io_slots=2,
+                          io_slot_bytes=4096, io_slots=2, cache_geometry=geometry,
                           k_scales=torch.from_numpy(scales).to(gpu) if dt != "bf16" else None)
         p.register(_named(caches))
         assert p.table.layout.k_layout == layout
@@ -772,6 +804,7 @@ def test_random_load_plans_match_the_sequential_oracle(gpu, tmp_path, seed):
         torch.cuda.synchronize()
         p.close()
         for l, c in enumerate(caches):
+            c = _from_split_x(c, bs, h, d) if layout == "kx" else c
             got = to_bits_np(c.contiguous(), dt)
             assert np.array_equal(got[1], ref[l][1]), f"layer {l} V (batch {batch})"
             ok, msg = oracle.rotation_within_tolerance(got[0], ref[l][0], kind)
