@@ -104,6 +104,12 @@ def test_set_tuning_checks_and_no_environment_reads():
     assert lib.dsr_set_tuning(_lib.TUNE["rot_kernel"], -2) == _lib.DSR_ERR_ARG
     for knob in _lib.TUNE:
         assert lib.dsr_set_tuning(_lib.TUNE[knob], 0) == _lib.DSR_OK
+    # the Python names are exactly the header's knobs
+    text = open(HEADER).read()
+    header = {m.group(1).lower(): int(m.group(2))
+              for m in re.finditer(r"#define DSR_TUNE_(\w+) (\d+)", text) if m.group(1) != "COUNT_"}
+    assert header == _lib.TUNE
+    assert int(re.search(r"#define DSR_TUNE_COUNT_ (\d+)", text).group(1)) == len(_lib.TUNE)
     csrc = os.path.join(ROOT, "daser_amd", "csrc")
     for name in os.listdir(csrc):
         with open(os.path.join(csrc, name)) as f:
