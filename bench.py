@@ -509,7 +509,7 @@ def bench_serving(torch, dev, steps: int = 10, n_req: int = 8, chunk_pages: int 
             asyncio.run(idx.insert(ChunkMeta(chunk_key(t), i * (ct // bs), ct // bs, ct, 0,
                                              "default")))
         cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(
-            kv_connector_extra_config={"block_tokens": bs}))
+            kv_connector_extra_config={"block_tokens": bs, "allow_chunk_assembly": True}))
         sched = C.DaserConnector(cfg, C.KVConnectorRole.SCHEDULER,
                                  ipc_client=_IndexServer(idx, slot))
         sched_ms, load_ms, placed = [], [], []

@@ -30,6 +30,10 @@ wait_for_save), ``io_slot_mb`` / ``io_slots`` (pinned ring geometry), ``io_reade
 (rings reading a load in parallel, default 4), ``io_timeout_s`` (a blocking
 store read or write raises TimeoutError after this long, default 120 as in
 the reference; None: wait forever),
+``allow_chunk_assembly`` (default False: only the first chunk of a lookup
+reply is loaded, the reference's single prefix hit; True: consecutive
+chunks of the reply are assembled, see :func:`place_chunks`; their tokens
+then lack the attention between chunks that a full prefill would have),
 ``store_path`` may hold ``{rank}``, replaced by the worker's tensor-parallel
 rank (one store file per rank; the reference's single path would make ranks
 overwrite each other's records at the same offsets),
@@ -152,10 +156,11 @@ class DaserConnectorMeta(KVConnectorMetadata):
 # placing looked-up chunks in the prompt (scheduler side)
 
 
-def place_chunks(tokens: list[int], chunks: list[dict],
-                 block_tokens: int) -> list[tuple[int, dict]]:
+def place_chunks(tokens: list[int], chunks: list[dict], block_tokens: int,
+                 max_chunks: Optional[int] = None) -> list[tuple[int, dict]]:
     """(first token position, chunk) of each chunk of a lookup reply that the
-    prompt can use, in prompt order.
+    prompt can use, in prompt order, at most ``max_chunks`` of them (None: no
+    limit).
 
     The first chunk goes at position 0, as the reference loads its single
     prefix hit (daser_connector.py:240-258, daser/retrieval/prefix.py:49-72).
@@ -168,6 +173,8 @@ def place_chunks(tokens: list[int], chunks: list[dict],
     placed: list[tuple[int, dict]] = []
     pos = 0
     for i, ch in enumerate(chunks):
+        if max_chunks is not None and i >= max_chunks:
+            break
         n = int(ch.get("token_count", 0))
         if n <= 0 or pos + n > len(tokens) and i > 0:
             break
@@ -179,30 +186,43 @@ def place_chunks(tokens: list[int], chunks: list[dict],
     return placed
 
 
-def load_spec(placed: list[tuple[int, dict]], block_ids: list[int],
-              block_tokens: int) -> Optional[ReqLoadSpec]:
-    """The worker's load of placed chunks into the request's first blocks:
-    chunk i's records go to the blocks from ``position_i / block_size``, as
-    far as the blocks reach, each with ``new_pos`` = its position. A single
-    chunk keeps the reference's flat fields; several become segments."""
+def load_spec(placed: list[tuple[int, dict]], block_ids: list[int], block_tokens: int,
+              first_block: int = 0) -> Optional[ReqLoadSpec]:
+    """The worker's load of placed chunks into the request's blocks: chunk
+    i's records go to the blocks from ``position_i / block_size``, as far as
+    the blocks reach, each with ``new_pos`` = its position. ``block_ids``
+    are all of the request's blocks from token 0; those below
+    ``first_block`` already hold vLLM's own KV (its local prefix cache hit,
+    ``num_computed_tokens``) and receive nothing. A single chunk keeps the
+    reference's flat fields; several become segments, indexing the returned
+    ``block_ids``, which start at ``first_block``."""
     segs = []
+    end = 0  # token after the last one loaded
     for pos, ch in placed:
         first = pos // block_tokens
         n = min(int(ch["num_slots"]), len(block_ids) - first)
         if n <= 0:
             break
-        segs.append(LoadSegment(start_slot=int(ch["start_slot"]), num_slots=n, block_offset=first,
-                                pos_offset=int(ch.get("pos_offset", 0)), new_pos=pos))
+        end = min(pos + int(ch["token_count"]), (first + n) * block_tokens)
+        skip = max(0, first_block - first)  # pages vLLM computed itself
+        if skip >= n:
+            continue
+        # the segment's first page moves by `skip`, both positions with it:
+        # the rotation delta new_pos - pos_offset is unchanged
+        segs.append(LoadSegment(start_slot=int(ch["start_slot"]) + skip, num_slots=n - skip,
+                                block_offset=first + skip - first_block,
+                                pos_offset=int(ch.get("pos_offset", 0)) + skip * block_tokens,
+                                new_pos=pos + skip * block_tokens))
     if not segs:
         return None
     head = placed[0][1]
-    used = block_ids[:segs[-1].block_offset + segs[-1].num_slots]
+    used = block_ids[first_block:first_block + segs[-1].block_offset + segs[-1].num_slots]
     return ReqLoadSpec(
         chunk_key=head["chunk_key"], start_slot=segs[0].start_slot, num_slots=segs[0].num_slots,
+        # file_offset stays the head chunk's: loads read start_slot * slot_size
         block_ids=used, file_offset=int(head["file_offset"]),
-        token_count=placed[len(segs) - 1][0] + int(placed[len(segs) - 1][1]["token_count"]),
-        pos_offset=segs[0].pos_offset, new_pos=segs[0].new_pos,
-        segments=segs if len(segs) > 1 else [])
+        token_count=end, pos_offset=segs[0].pos_offset, new_pos=segs[0].new_pos,
+        segments=segs if len(segs) > 1 or segs[0].block_offset else [])
 
 
 # ---------------------------------------------------------------------------
@@ -279,6 +299,10 @@ class DaserConnector(KVConnectorBase_V1):
         self._slot_size: int = int(extra.get("slot_size", 0))
         self._block_tokens: int = int(extra.get("block_tokens", 16))
         self._model_id: str = extra.get("model_id", "default")
+        # several separately prefilled chunks in one prompt skip the
+        # attention between them: opt in, else only the first (the
+        # reference's single prefix hit) is loaded
+        self._allow_assembly = bool(extra.get("allow_chunk_assembly", False))
         self._role_kind = role
         if role == KVConnectorRole.SCHEDULER:
             self._ipc_sync = ipc_client if ipc_client is not None else _default_ipc(
@@ -358,7 +382,8 @@ class DaserConnector(KVConnectorBase_V1):
             return 0, False
         if reply.get("alloc") is not None:
             self._pending_alloc[rid] = reply["alloc"]
-        placed = place_chunks(tokens[:lookup_len], reply.get("chunks") or [], bs)
+        placed = place_chunks(tokens[:lookup_len], reply.get("chunks") or [], bs,
+                              None if self._allow_assembly else 1)
         if not placed:
             return 0, False
         matched = placed[-1][0] + int(placed[-1][1]["token_count"])
@@ -369,19 +394,26 @@ class DaserConnector(KVConnectorBase_V1):
         new_tokens = min(matched, len(tokens) - 1) - num_computed_tokens
         if new_tokens <= 0:
             return 0, False
-        self._pending_loads[rid] = {"placed": placed}
+        self._pending_loads[rid] = {"placed": placed, "computed": num_computed_tokens}
         return new_tokens, False
 
     def update_state_after_alloc(self, request: Any, blocks: Any, num_external_tokens: int) -> None:
-        """Records the blocks vLLM gave the request: the first
-        ceil(num_external_tokens / block_size) receive a load (reference
-        :260-298), or those of the aligned prompt receive its store."""
+        """Records the blocks vLLM gave the request: those of tokens
+        [num_computed_tokens, num_computed_tokens + num_external_tokens)
+        receive a load, or those of the aligned prompt receive its store
+        (reference :260-298, which counts the load's blocks from block 0
+        and so assumes num_computed_tokens == 0)."""
         rid = request.request_id
         block_ids = [blk.block_id for blk in blocks.blocks[0]]
         bs = self._block_tokens
         pending = self._pending_loads.get(rid)
         if num_external_tokens > 0 and pending is not None:
-            pending["block_ids"] = block_ids[:-(-num_external_tokens // bs)]
+            # vLLM's blocks start at token 0; its own prefix-cache hit (the
+            # first num_computed_tokens, whole blocks) keeps its KV and the
+            # external tokens follow it
+            computed = pending["computed"]
+            pending["block_ids"] = block_ids[:-(-(computed + num_external_tokens) // bs)]
+            pending["first_block"] = computed // bs
             return
         alloc = self._pending_alloc.pop(rid, None)
         if alloc is not None:
@@ -399,7 +431,8 @@ class DaserConnector(KVConnectorBase_V1):
         for rid in [r for r, p in self._pending_loads.items()
                     if r in scheduled and "block_ids" in p]:
             pending = self._pending_loads.pop(rid)
-            spec = load_spec(pending["placed"], pending["block_ids"], self._block_tokens)
+            spec = load_spec(pending["placed"], pending["block_ids"], self._block_tokens,
+                             pending["first_block"])
             if spec is not None:
                 meta.reqs_to_load[rid] = spec
         for rid in [r for r, a in self._pending_stores.items()

@@ -107,6 +107,28 @@ def test_two_chunks_assembled_at_0_and_528(gpu, tmp_path):
     w.shutdown()
 
 
+def test_vllm_prefix_hit_keeps_its_blocks(gpu, tmp_path):
+    """vLLM computed the first 80 tokens itself (its local prefix cache):
+    the load leaves those 5 blocks alone and fills the rest, the second chunk
+    re-rotated from its stored position 1000 to 528."""
+    print("case: positions num_computed_tokens=80, chunks at 0 and 528", flush=True)
+    rng = np.random.default_rng(12)
+    a = rng.integers(0, 30000, size=528).tolist()
+    b = rng.integers(0, 30000, size=256).tolist()
+    w = _store_chunks(tmp_path, gpu, [(a, 40), (b, 200)], seed=43)
+    idx = ChunkAssemblyIndex(BS)
+    asyncio.run(idx.insert(meta_for(a, 40, model_id="m", pos_offset=0)))
+    asyncio.run(idx.insert(meta_for(b, 200, model_id="m", pos_offset=1000)))
+    blocks = rng.permutation(NB)
+    n, spec = _schedule(_scheduler(ServerWithIndex(idx, SHAPE.slot_bytes)), "r",
+                        a + b + [3] * 30, 60, blocks, computed=80)
+    assert n == 784 - 80 and spec.block_ids == blocks[5:49].tolist()
+    # _load_and_check also holds every page it does not load (blocks[:5]) to
+    # its old bytes
+    _load_and_check(tmp_path, gpu, spec, [(45, 28, 0, 80, 80), (200, 16, 28, 1000, 528)])
+    w.shutdown()
+
+
 def test_duplicate_destination_blocks_keep_the_last_load(gpu, tmp_path):
     """Loads of one step that target the same block leave the last one's
     bytes, as the reference's sequential copies do (daser_connector.py:

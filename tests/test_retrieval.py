@@ -121,17 +121,19 @@ class ServerWithIndex:
                 "alloc": None}
 
 
-def _scheduler(server):
+def _scheduler(server, assemble=True):
     cfg = SimpleNamespace(kv_transfer_config=SimpleNamespace(
-        kv_connector_extra_config={"block_tokens": BS, "model_id": "m"}))
+        kv_connector_extra_config={"block_tokens": BS, "model_id": "m",
+                                   "allow_chunk_assembly": assemble}))
     return C.DaserConnector(cfg, C.KVConnectorRole.SCHEDULER, ipc_client=server)
 
 
-def _schedule(conn, rid, prompt, n_blocks, block_ids=None):
+def _schedule(conn, rid, prompt, n_blocks, block_ids=None, computed=0):
     """One request through the scheduler hooks; vLLM's blocks are
-    ``block_ids`` (default 1000, 1001, ...)."""
+    ``block_ids`` (default 1000, 1001, ...), of which the first
+    ``computed`` tokens hit vLLM's own prefix cache."""
     req = SimpleNamespace(request_id=rid, prompt_token_ids=prompt)
-    n, _ = conn.get_num_new_matched_tokens(req, 0)
+    n, _ = conn.get_num_new_matched_tokens(req, computed)
     ids = list(block_ids) if block_ids is not None else [1000 + i for i in range(n_blocks)]
     blocks = SimpleNamespace(blocks=[[SimpleNamespace(block_id=i) for i in ids[:n_blocks]]])
     conn.update_state_after_alloc(req, blocks, n)
@@ -197,10 +199,75 @@ def test_load_spec_clips_to_the_blocks_given():
     spec = C.load_spec(placed, [9, 8, 7, 6, 5], BS)
     assert [(s.num_slots, s.block_offset, s.new_pos) for s in spec.segments] == \
         [(3, 0, 0), (2, 3, 48)]
-    assert spec.block_ids == [9, 8, 7, 6, 5] and spec.token_count == 112
+    # the second chunk is cut to 2 of its 4 pages: 80 tokens are loaded
+    assert spec.block_ids == [9, 8, 7, 6, 5] and spec.token_count == 80
     one = C.load_spec(placed, [9, 8], BS)
     assert one.segments == [] and one.num_slots == 2 and one.block_ids == [9, 8]
     assert C.load_spec(placed, [], BS) is None
+
+
+def test_load_spec_skips_the_blocks_vllm_computed():
+    """Blocks below first_block hold vLLM's own prefix-cache KV: nothing is
+    loaded there, and a cut segment keeps its rotation delta."""
+    placed = [(0, {"chunk_key": "x", "start_slot": 4, "num_slots": 3, "token_count": 48,
+                   "pos_offset": 0, "file_offset": 4 * SLOT}),
+              (48, {"chunk_key": "y", "start_slot": 20, "num_slots": 4, "token_count": 64,
+                    "pos_offset": 100, "file_offset": 20 * SLOT})]
+    ids = [9, 8, 7, 6, 5, 4, 3]
+    spec = C.load_spec(placed, ids, BS, first_block=2)
+    assert spec.block_ids == [7, 6, 5, 4, 3] and spec.token_count == 112
+    assert [(s.start_slot, s.num_slots, s.block_offset, s.pos_offset, s.new_pos)
+            for s in spec.segments] == [(6, 1, 0, 32, 32), (20, 4, 1, 100, 48)]
+    # the whole first chunk computed, and one page of the second
+    spec = C.load_spec(placed, ids, BS, first_block=4)
+    assert spec.block_ids == [5, 4, 3] and spec.segments == []
+    assert (spec.start_slot, spec.num_slots, spec.pos_offset, spec.new_pos) == (21, 3, 116, 64)
+    plan = C.plan_load({"r": spec}, SLOT)
+    assert plan.deltas == [48 - 100] and plan.page_ids.tolist() == [5, 4, 3]
+    assert C.load_spec(placed, ids, BS, first_block=7) is None
+
+
+def test_scheduler_with_vllm_prefix_hit_loads_only_the_rest():
+    """num_computed_tokens > 0 (vLLM's local prefix cache): the load fills
+    the blocks from there on, and none of the computed ones."""
+    rng = np.random.default_rng(6)
+    a = rng.integers(0, 30000, size=528).tolist()  # 33 pages
+    b = rng.integers(0, 30000, size=256).tolist()  # 16 pages
+    idx = ChunkAssemblyIndex(BS)
+    run(idx.insert(meta_for(a, 40, pos_offset=0)))
+    run(idx.insert(meta_for(b, 7, pos_offset=3000)))
+    prompt = a + b + [5] * 20
+    n, spec = _schedule(_scheduler(ServerWithIndex(idx)), "r", prompt, 60, computed=80)
+    assert n == 784 - 80
+    assert spec.block_ids == list(range(1005, 1049))
+    assert [(s.start_slot, s.num_slots, s.block_offset, s.pos_offset, s.new_pos)
+            for s in spec.segments] == [(45, 28, 0, 80, 80), (7, 16, 28, 3000, 528)]
+    plan = C.plan_load({"r": spec}, SLOT)
+    assert plan.page_ids.tolist() == list(range(1005, 1049))
+    assert plan.rope_idx.tolist() == [-1] * 28 + [0] * 16
+    # vLLM computed past the first chunk: only the rest of the second loads
+    n, spec = _schedule(_scheduler(ServerWithIndex(idx)), "s", prompt, 60, computed=560)
+    assert n == 784 - 560 and spec.block_ids == list(range(1035, 1049))
+    assert (spec.start_slot, spec.num_slots, spec.pos_offset, spec.new_pos) == \
+        (9, 14, 3032, 560)
+    # vLLM computed everything a hit would give: nothing to load
+    n, spec = _schedule(_scheduler(ServerWithIndex(idx)), "t", prompt, 60, computed=784)
+    assert n == 0 and spec is None
+
+
+def test_chunk_assembly_is_opt_in():
+    """Without allow_chunk_assembly only the first chunk of a reply loads,
+    as the reference's single prefix hit."""
+    rng = np.random.default_rng(7)
+    a = rng.integers(0, 30000, size=64).tolist()
+    b = rng.integers(0, 30000, size=64).tolist()
+    idx = ChunkAssemblyIndex(BS)
+    run(idx.insert(meta_for(a, 1, pos_offset=0)))
+    run(idx.insert(meta_for(b, 9, pos_offset=0)))
+    n, spec = _schedule(_scheduler(ServerWithIndex(idx), assemble=False), "r", a + b + [1], 9)
+    assert n == 64 and spec.segments == [] and spec.block_ids == list(range(1000, 1004))
+    n, spec = _schedule(_scheduler(ServerWithIndex(idx)), "r", a + b + [1], 9)
+    assert n == 128 and len(spec.segments) == 2
 
 
 def test_whole_prompt_hit_leaves_one_token_to_compute():
