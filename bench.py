@@ -153,40 +153,60 @@ def bench_copy(torch, ops, wl, dtype, dev, steps, warmup, position=None):
         ro_np = ops.token_row_offsets(wl.req_tokens, shape.slot_bytes, shape.block_size, row)
         sm = torch.from_numpy(sm_np).to(dev)
         ro = torch.from_numpy(ro_np).to(dev)
-        order = np.argsort(sm_np, kind="stable")  # scatter in destination order
-        sm_s = torch.from_numpy(sm_np[order]).to(dev)
-        ro_s = torch.from_numpy(ro_np[order]).to(dev)
-        tsg, tss = Timer(torch), Timer(torch)
-        for i in range(warmup + steps):
-            if i < warmup:
-                ops.gather_slots(table, sm, ro, staging)
-                ops.scatter_slots(table, sm_s, ro_s, staging)
-                continue
-            with tsg:
-                ops.gather_slots(table, sm, ro, staging)
-            with tss:
-                ops.scatter_slots(table, sm_s, ro_s, staging)
-        # the token-form load with every request re-rotated (a delta each)
+        # the token-form load as ops.scatter_slots runs host tables: in
+        # destination-slot order, whole pages through the page scatter and
+        # the ragged rows through the token kernel; the split is made once,
+        # as by a caller whose tables stay resident
         from daser_amd import position as _position
 
         rng = np.random.default_rng(11)
         deltas = rng.integers(1, 32768, size=len(wl.req_tokens)).tolist()
         req_idx, uniq = _position.page_rope_index([1] * len(deltas), deltas)
         tabs = _position.delta_tables(uniq, shape.head_dim, THETA, device=dev)
-        tok_idx = np.repeat(np.asarray(req_idx, np.int64), wl.req_tokens)[order]
-        ridx_s = torch.from_numpy(tok_idx.astype(np.int32)).to(dev)
+        tok_idx = np.repeat(np.asarray(req_idx, np.int64), wl.req_tokens)
+        sm_o, ro_o, ri_o = ops.slot_order(sm_np, ro_np, tok_idx)
+        pg, pg_offs, pg_ri, rest = ops.whole_pages(sm_o, ro_o, shape.block_size, row, ri_o)
+
+        def dev_t(x, dt=torch.int64):
+            return torch.from_numpy(np.ascontiguousarray(x)).to(dt).to(dev)
+
+        pg_d, pg_offs_d, pg_ri_d = dev_t(pg, torch.int32), dev_t(pg_offs), dev_t(pg_ri, torch.int32)
+        sm_r, ro_r, ri_r = dev_t(sm_o[rest]), dev_t(ro_o[rest]), dev_t(ri_o[rest], torch.int32)
+        has_rest = bool(np.any(sm_o[rest] >= 0))
+
+        def scatter_tokens():
+            ops.scatter(table, pg_d, pg_offs_d, staging)
+            if has_rest:
+                ops.scatter_slots(table, sm_r, ro_r, staging)
+
+        def rerotate_tokens():
+            ops.scatter_rerotate(table, pg_d, pg_offs_d, staging, tabs, pg_ri_d)
+            if has_rest:
+                ops.scatter_slots_rerotate(table, sm_r, ro_r, staging, tabs, ri_r)
+
+        tsg, tss = Timer(torch), Timer(torch)
+        for i in range(warmup + steps):
+            if i < warmup:
+                ops.gather_slots(table, sm, ro, staging)
+                scatter_tokens()
+                continue
+            with tsg:
+                ops.gather_slots(table, sm, ro, staging)
+            with tss:
+                scatter_tokens()
         tsr = Timer(torch)
         for i in range(warmup + steps):
             if i < warmup:
-                ops.scatter_slots_rerotate(table, sm_s, ro_s, staging, tabs, ridx_s)
+                rerotate_tokens()
                 continue
             with tsr:
-                ops.scatter_slots_rerotate(table, sm_s, ro_s, staging, tabs, ridx_s)
+                rerotate_tokens()
         torch.cuda.synchronize()
         tokP = wl.tokens * row * 2 * shape.num_layers
         rot = {"slots_gather_ms": tsg.mean_ms(), "slots_scatter_ms": tss.mean_ms(),
                "slots_rerotate_ms": tsr.mean_ms(),
                "slots_payload_bytes": tokP,
+               "slots_whole_pages": int(pg.size), "slots_ragged_tokens": int(np.sum(sm_o[rest] >= 0)),
                "slots_gather_GBps": 2 * tokP / (tsg.mean_ms() * 1e-3) / 1e9,
                "slots_scatter_GBps": 2 * tokP / (tss.mean_ms() * 1e-3) / 1e9,
                "slots_rerotate_GBps": 2 * tokP / (tsr.mean_ms() * 1e-3) / 1e9}
@@ -773,14 +793,22 @@ def bench_patterns(torch, ops, dev, reps: int = 5) -> dict:
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (/proc/cpuinfo)."""
+    """The host CPU as /proc/cpuinfo names it: model name verbatim, with its
+    family / model / stepping numbers and the logical CPUs listed there."""
+    fields, n = {}, 0
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key == "processor":
+                n += 1
+            elif key in ("model name", "cpu family", "model", "stepping") and key not in fields:
+                fields[key] = val.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    return (f"{fields.get('model name', 'unknown')} (family {fields.get('cpu family', '?')}, "
+            f"model {fields.get('model', '?')}, stepping {fields.get('stepping', '?')}; "
+            f"{n} logical CPUs in /proc/cpuinfo)")
 
 
 def reference_loop(torch, dev, budget_s: float = 6.0) -> dict:
@@ -836,6 +864,16 @@ def reference_loop(torch, dev, budget_s: float = 6.0) -> dict:
 # the re-rotation kernel each configuration's launch selects (by page size)
 ROT_KERNEL = {3: "kv_scatter_rerotate_grouped_kernel", 5: "kv_scatter_rerotate_grouped_kernel",
               6: "kv_scatter_rerotate_grouped_kernel"}
+
+
+def frac_hbm(traffic, ms):
+    """HBM fraction on counter bytes: recorded traffic per launch (FETCH_SIZE
+    + WRITE_SIZE, scaled) / this run's kernel time / 8 TB/s. Below the
+    algorithmic fraction where caches (the memory-side cache) serve part of
+    the reads. None if the traffic is not recorded."""
+    if traffic is None or not ms:
+        return None
+    return round(traffic / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
 
 
 def pmc_traffic(kernel: str, config: int, pages: int):
@@ -1017,12 +1055,16 @@ def main() -> int:
         out["kernels"]["gather_slots"] = {
             "ms": round(r["slots_gather_ms"], 4), "GBps": round(r["slots_gather_GBps"], 1),
             "frac": round(r["slots_gather_GBps"] / HBM_PEAK_GBS, 4)}
+        split = (f"{r['slots_whole_pages']} whole pages through the page kernel, "
+                 f"{r['slots_ragged_tokens']} ragged-edge tokens through the token kernel")
         out["kernels"]["scatter_slots"] = {
             "ms": round(r["slots_scatter_ms"], 4), "GBps": round(r["slots_scatter_GBps"], 1),
-            "frac": round(r["slots_scatter_GBps"] / HBM_PEAK_GBS, 4)}
+            "frac": round(r["slots_scatter_GBps"] / HBM_PEAK_GBS, 4),
+            "path": "kv_scatter_stream_kernel + kv_slots_kernel: " + split}
         out["kernels"]["scatter_slots_rerotate"] = {
             "ms": round(r["slots_rerotate_ms"], 4), "GBps": round(r["slots_rerotate_GBps"], 1),
-            "frac": round(r["slots_rerotate_GBps"] / HBM_PEAK_GBS, 4)}
+            "frac": round(r["slots_rerotate_GBps"] / HBM_PEAK_GBS, 4),
+            "path": "kv_scatter_rerotate_grouped_kernel + kv_slots_rerotate_kernel: " + split}
         out["check"] = {"round_trip_probe": r["probe_ok"]}
     for c in (3, 5, 6):
         if c in res:
@@ -1042,6 +1084,8 @@ def main() -> int:
                 "kernel": ROT_KERNEL[c],
                 "traffic": pmc_traffic(ROT_KERNEL[c], c, r["pages"]),
                 "algorithmic_bytes": 2 * r["payload_bytes"]}
+            out[f"rerotate_cfg{c}"]["frac_hbm"] = frac_hbm(
+                out[f"rerotate_cfg{c}"]["traffic"], r["kernel_ms"])
     if 4 in res:
         r = res[4]
         out["fp8_cfg4"] = {"workload": workloads.CONFIG_NAMES[4],
@@ -1056,6 +1100,13 @@ def main() -> int:
                            "tokens": r["tokens"], "payload_bytes": r["payload_bytes"],
                            "traffic_rerotate": pmc_traffic("kv_scatter_rerotate_contig_kernel", 4,
                                                            r["pages"])}
+        f8 = out["fp8_cfg4"]
+        f8["frac"] = {k: round(r[f"{k}_GBps"] / HBM_PEAK_GBS, 4)
+                      for k in ("gather", "scatter", "rerotate") if r.get(f"{k}_GBps")}
+        f8["frac_hbm"] = {
+            "gather": frac_hbm(pmc_traffic("kv_gather_kernel", 4, r["pages"]), r["gather_ms"]),
+            "scatter": frac_hbm(pmc_traffic("kv_scatter_kernel", 4, r["pages"]), r["scatter_ms"]),
+            "rerotate": frac_hbm(f8["traffic_rerotate"], r.get("rerotate_ms"))}
     if "value" not in out and configs:
         r = res[configs[0]]
         out.update({"value": round(r.get("tokens_per_s", 0.0)), "unit": "tokens/s",
@@ -1086,7 +1137,7 @@ def main() -> int:
             f"({ncpu} threads)")
         r = reference_loop(torch, torch.device("cpu"), budget_s=12.0)
         out["cpu_baseline"] = {
-            "value": r["GBps"], "unit": "GB/s", "cores": ncpu, "kind": "port",
+            "value": r["GBps"], "unit": "GB/s", "cores": ncpu, "kind": "reference torch loop",
             "cpu_model": cpu_model(),
             "sample": "torch restatement of daser_connector.py:625-632 (save: reshape + copy_ "
                       "per page and layer) and :536-551 (load: copy_ per page and layer) on "

@@ -47,7 +47,7 @@ DSR_REROTATE_SHARED_RECORDS = DSR_SHARED_RECORDS
 TUNE = {"units_per_group": 0, "max_wg_per_launch": 1, "rot_kernel": 2, "rot_wg_per_cu": 3,
         "rot_grouped_wg_per_cu": 4, "slots_tpw": 5, "slots_kernel": 6, "slots_unroll": 7,
         "copy_wg_per_cu": 8, "scatter_kernel": 9, "gather_split": 10,
-        "page_parts": 11}
+        "page_parts": 11, "slots_order": 12, "slots_wg_per_cu": 13}
 ROT_KERNEL_CODES = {"auto": 0, "pairs": 1, "contig": 2, "grouped": 3}
 
 _P = ctypes.c_void_p

@@ -829,6 +829,16 @@ int dsr_scatter_hnd(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
 
 namespace {
 
+// Unit order and workgroups per CU of the large-row token scatters
+// (kv_slots_kernel, kv_slots_rerotate_kernel); DSR_TUNE_SLOTS_ORDER (1 per-XCD
+// layer-major, 2 hardware dispatch order) and DSR_TUNE_SLOTS_WG_PER_CU
+// override them.
+bool slots_hw_order() { return tune(DSR_TUNE_SLOTS_ORDER) == 2; }
+int slots_wg_per_cu(int dflt) {
+  const int64_t t = tune(DSR_TUNE_SLOTS_WG_PER_CU);
+  return t > 0 ? (int)t : dflt;
+}
+
 int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t kv_stride,
                  int64_t page_stride, int64_t page_bytes, int64_t num_blocks, int block_size,
                  int64_t row_bytes, const int64_t* slot_mapping, const int64_t* row_offsets,
@@ -918,8 +928,10 @@ int slots_launch(bool gather, const uint64_t* layer_base, int n_layers, int64_t 
         kv_slots_small_kernel<false, 4><<<grid, kThreads, 0, s>>>(b);
     } else if (gather) {
       kv_slots_kernel<true><<<grid, kThreads, occupancy_lds(3, 0), s>>>(b);
+    } else if (slots_hw_order()) {
+      kv_slots_kernel<false, true><<<grid, kThreads, occupancy_lds(slots_wg_per_cu(3), 0), s>>>(b);
     } else {
-      kv_slots_kernel<false><<<grid, kThreads, occupancy_lds(3, 0), s>>>(b);
+      kv_slots_kernel<false><<<grid, kThreads, occupancy_lds(slots_wg_per_cu(3), 0), s>>>(b);
     }
     const int rc = (int)hipGetLastError();
     if (rc != 0) return rc;
@@ -1008,11 +1020,14 @@ int slots_rerotate_launch(const uint64_t* layer_base, int n_layers, int64_t kv_s
     rb.rope_idx = rope_idx + t0;
     const int64_t units = ((int64_t)b.n_tokens + kTokPerWg - 1) / kTokPerWg * n_layers;
     const unsigned grid = (unsigned)((units + kXcds - 1) / kXcds * kXcds);
-    const size_t dyn = occupancy_lds(3, sizeof(float2) * kTokPerWg * kSlotRotMaxHalf);
-    const bool neox = rope_style == DSR_ROPE_NEOX;
-#define DSR_SLOT_ROT(DT)                                                                  \
-  (neox ? kv_slots_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(b, rb) \
-        : kv_slots_rerotate_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(b, rb))
+    const size_t dyn =
+        occupancy_lds(slots_wg_per_cu(3), sizeof(float2) * kTokPerWg * kSlotRotMaxHalf);
+    const bool neox = rope_style == DSR_ROPE_NEOX, hw = slots_hw_order();
+#define DSR_SLOT_ROT(DT)                                                                      \
+  (hw ? (neox ? kv_slots_rerotate_kernel<DT, DSR_ROPE_NEOX, true><<<grid, kThreads, dyn, s>>>(b, rb) \
+              : kv_slots_rerotate_kernel<DT, DSR_ROPE_GPTJ, true><<<grid, kThreads, dyn, s>>>(b, rb)) \
+      : (neox ? kv_slots_rerotate_kernel<DT, DSR_ROPE_NEOX><<<grid, kThreads, dyn, s>>>(b, rb)       \
+              : kv_slots_rerotate_kernel<DT, DSR_ROPE_GPTJ><<<grid, kThreads, dyn, s>>>(b, rb)))
     switch (dtype) {
       case DSR_DTYPE_BF16: DSR_SLOT_ROT(DSR_DTYPE_BF16); break;
       case DSR_DTYPE_FP16: DSR_SLOT_ROT(DSR_DTYPE_FP16); break;

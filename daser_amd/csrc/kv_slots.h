@@ -54,14 +54,15 @@ constexpr int kRowUnroll = 2;   // 64-vector slices of a row per round
 // 11.58 ms and scatter 12.63 -> 12.38 ms against the branching kernel
 // without LDS (the branch-free kernel without LDS: 12.38 / 12.55; at one or
 // two workgroups per CU: 13.8-14.3 ms).
-template <bool kGather>
+template <bool kGather, bool kHwOrder = false>
 __global__ __launch_bounds__(kThreads) void kv_slots_kernel(SlotArgs a) {
   // the scatter writes the paged cache: layer-major per XCD, as the page
-  // scatter (-2.4% in-process); the gather keeps the identity order
+  // scatter (-2.4% in-process), or layer-major in hardware dispatch order
+  // (kHwOrder); the gather keeps the identity order
   int64_t unit = blockIdx.x;
   if (!kGather) {
     const int64_t nu = ((int64_t)a.n_tokens + kTokPerWg - 1) / kTokPerWg * a.n_layers;
-    unit = layer_major_unit(nu, a.n_layers);
+    unit = kHwOrder ? layer_major_unit_hw(nu, a.n_layers) : layer_major_unit(nu, a.n_layers);
     if (unit < 0) return;
   }
   const int64_t tb = udiv32(unit, a.n_layers);
@@ -261,12 +262,13 @@ constexpr int kSlotRotMaxHalf = 128;  // rot_dim <= 256
 // s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima
 constexpr int kWaitVmcnt0 = 0x0F70;
 
-template <int DT, int STYLE>
+template <int DT, int STYLE, bool kHwOrder = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void kv_slots_rerotate_kernel(SlotArgs a, RotArgs ra) {
   __shared__ float2 tab[kTokPerWg][kSlotRotMaxHalf];
   const int64_t nu = ((int64_t)a.n_tokens + kTokPerWg - 1) / kTokPerWg * a.n_layers;
-  const int64_t unit = layer_major_unit(nu, a.n_layers);
+  const int64_t unit =
+      kHwOrder ? layer_major_unit_hw(nu, a.n_layers) : layer_major_unit(nu, a.n_layers);
   if (unit < 0) return;
   const int64_t tb = udiv32(unit, a.n_layers);
   const int l = (int)(unit - tb * a.n_layers);

@@ -540,15 +540,17 @@ def _slots_args(table: LayerTable, slot_mapping, row_offsets, staging, layer0, l
             # slot (scatter) would race inside the launch; as the reference's
             # sequential copies leave the last one's bytes, the earlier ones
             # become padding (slot -1) in a copy of the host table.
-            dest = r if records_written else sm[valid]
-            if np.unique(dest).size != dest.size:
-                idx = np.nonzero(valid)[0]
-                _, last_rev = np.unique(dest[::-1], return_index=True)
-                keep = np.zeros(idx.size, bool)
-                keep[idx.size - 1 - last_rev] = True
-                sm = sm.copy()
-                sm[idx[~keep]] = -1
-                slot_mapping = sm
+            if records_written:
+                if np.unique(r).size != r.size:
+                    idx = np.nonzero(valid)[0]
+                    _, last_rev = np.unique(r[::-1], return_index=True)
+                    keep = np.zeros(idx.size, bool)
+                    keep[idx.size - 1 - last_rev] = True
+                    sm = sm.copy()
+                    sm[idx[~keep]] = -1
+                    slot_mapping = sm
+            else:
+                slot_mapping = _last_per_slot(sm)
     sm_d = _as_device_table(slot_mapping, torch.int64, lay.device, "slot_mapping")
     ro_d = _as_device_table(row_offsets, torch.int64, lay.device, "row_offsets")
     if sm_d.numel() != ro_d.numel():
@@ -569,15 +571,93 @@ def gather_slots(table: LayerTable, slot_mapping, row_offsets, staging: torch.Te
     _lib.check("dsr_gather_slots", rc)
 
 
+def _last_per_slot(sm: np.ndarray) -> np.ndarray:
+    """slot_mapping with every entry but the last of a repeated slot turned
+    into padding (-1): the reference's sequential copies leave the last
+    one's bytes, while copies inside one launch would race."""
+    valid = np.nonzero(sm >= 0)[0]
+    dest = sm[valid]
+    if np.unique(dest).size == dest.size:
+        return sm
+    _, last_rev = np.unique(dest[::-1], return_index=True)
+    keep = np.zeros(valid.size, bool)
+    keep[valid.size - 1 - last_rev] = True
+    sm = sm.copy()
+    sm[valid[~keep]] = -1
+    return sm
+
+
+def whole_pages(slot_mapping: np.ndarray, row_offsets: np.ndarray, block_size: int,
+                row_bytes: int, rope_idx: Optional[np.ndarray] = None):
+    """Splits the host tables of a token-form scatter into whole pages and
+    the rest. The entries must be in slot order with no slot listed twice
+    (padding, -1, anywhere). A block is whole when its block_size slots sit
+    in consecutive entries, in order, with consecutive record rows
+    (row_offsets stepping by row_bytes: the block's K rows form one record
+    page, its V rows the page after) and, with rope_idx, one table index.
+
+    Returns (page_ids, page_offsets, page_rope or None, rest): the whole
+    blocks, the record offset of each one's first row (its slot record
+    offset in the page form), their table indices, and a mask of the entries
+    left for the token kernels."""
+    sm = np.asarray(slot_mapping, np.int64)
+    ro = np.asarray(row_offsets, np.int64)
+    n, bs = sm.size, int(block_size)
+    rest = np.ones(n, bool)
+    empty = np.zeros(0, np.int64)
+    if n < bs:
+        return empty, empty, None if rope_idx is None else empty, rest
+    step = np.zeros(n, bool)  # entry i continues entry i - 1 inside one record page
+    step[1:] = (sm[1:] == sm[:-1] + 1) & (ro[1:] == ro[:-1] + row_bytes) & (sm[:-1] >= 0)
+    ri = None
+    if rope_idx is not None:
+        ri = np.asarray(rope_idx, np.int64)
+        step[1:] &= ri[1:] == ri[:-1]
+    breaks = np.cumsum(~step)
+    i = np.arange(n - bs + 1)
+    start = (sm[i] >= 0) & (sm[i] % bs == 0) & (breaks[i + bs - 1] == breaks[i])
+    starts = i[start]
+    rest[(starts[:, None] + np.arange(bs)).ravel()] = False
+    return (sm[starts] // bs, ro[starts], None if ri is None else ri[starts], rest)
+
+
+def slot_order(slot_mapping, row_offsets, rope_idx=None):
+    """Host tables in slot order, repeated slots padded but the last; None
+    for device tables."""
+    sm = _host_array(slot_mapping, np.int64)
+    ro = _host_array(row_offsets, np.int64)
+    ri = None if rope_idx is None else _host_array(rope_idx, np.int64)
+    if sm is None or ro is None or (rope_idx is not None and ri is None) or not sm.size:
+        return None
+    if sm.shape != ro.shape or (ri is not None and ri.shape != sm.shape):
+        raise ValueError("slot_mapping, row_offsets and rope_idx differ in length")
+    order = np.argsort(sm, kind="stable")
+    # within a run of equal slots the stable order keeps list order
+    return _last_per_slot(sm[order]), ro[order], None if ri is None else ri[order]
+
+
 def scatter_slots(table: LayerTable, slot_mapping, row_offsets, staging: torch.Tensor, *,
                   layer0: int = 0, layers: Optional[tuple[int, int]] = None) -> None:
     """Inverse of :func:`gather_slots`. Host tables are processed in
-    destination-slot order (near-sequential writes), like :func:`scatter`."""
-    sm = _host_array(slot_mapping, np.int64)
-    ro = _host_array(row_offsets, np.int64)
-    if sm is not None and ro is not None and sm.size:
-        order = np.argsort(sm, kind="stable")
-        slot_mapping, row_offsets = sm[order], ro[order]
+    destination-slot order (near-sequential writes), like :func:`scatter`,
+    and blocks whose every slot is listed with consecutive record rows go
+    as whole pages through the page scatter (:func:`whole_pages`); the other
+    tokens (the ragged edges of requests) go through the token kernel.
+    Device tables go to the token kernel as given."""
+    host = slot_order(slot_mapping, row_offsets)
+    if host is not None:
+        sm, ro, _ = host
+        lay = table.layout
+        if lay.has_geometry and lay.k_layout == "nhd":
+            row = lay.num_heads * lay.head_dim * lay.elem_bytes
+            pages, offs, _, rest = whole_pages(sm, ro, lay.block_size, row)
+            if pages.size:
+                scatter(table, pages, offs, staging, layer0=layer0, layers=layers,
+                        shared_records=False)
+                sm, ro = sm[rest], ro[rest]
+                if not np.any(sm >= 0):
+                    return
+        slot_mapping, row_offsets = sm, ro
     args, _tables = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, False)
     rc = _lib.lib().dsr_scatter_slots(*args, _stream_handle(table.layout.device))
     _lib.check("dsr_scatter_slots", rc)
@@ -592,18 +672,25 @@ def scatter_slots_rerotate(table: LayerTable, slot_mapping, row_offsets,
     """:func:`scatter_slots` with each valid token's K rotated by
     ``cos_sin[rope_idx[t]]`` (-1 = copy), as :func:`scatter_rerotate` rotates
     a page row (same tables, scales and layer groups). Host tables are
-    processed in destination-slot order."""
+    processed in destination-slot order, whole pages with one table index
+    through :func:`scatter_rerotate`."""
     lay = table.layout
     rot_dim, n_tables, n_groups, lg_d, ks_ptr = _rope_args(
         lay, cos_sin, rope_idx, rot_dim, k_scale, layer0, layer_group)
-    sm = _host_array(slot_mapping, np.int64)
-    ro = _host_array(row_offsets, np.int64)
-    ri = _host_array(rope_idx, np.int64)
-    if sm is not None and ro is not None and ri is not None and sm.size:
-        if ri.shape != sm.shape:
-            raise ValueError("rope_idx and slot_mapping differ in length")
-        order = np.argsort(sm, kind="stable")
-        slot_mapping, row_offsets, rope_idx = sm[order], ro[order], ri[order]
+    host = slot_order(slot_mapping, row_offsets, rope_idx)
+    if host is not None:
+        sm, ro, ri = host
+        if lay.has_geometry and lay.k_layout == "nhd":
+            row = lay.num_heads * lay.head_dim * lay.elem_bytes
+            pages, offs, pri, rest = whole_pages(sm, ro, lay.block_size, row, ri)
+            if pages.size:
+                scatter_rerotate(table, pages, offs, staging, cos_sin, pri, rot_dim=rot_dim,
+                                 style=style, k_scale=k_scale, layer0=layer0, layers=layers,
+                                 layer_group=layer_group, shared_records=False)
+                sm, ro, ri = sm[rest], ro[rest], ri[rest]
+                if not np.any(sm >= 0):
+                    return
+        slot_mapping, row_offsets, rope_idx = sm, ro, ri
     args, _tables = _slots_args(table, slot_mapping, row_offsets, staging, layer0, layers, False)
     ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")
     if ridx_d.numel() != _tables[0].numel():

@@ -83,6 +83,11 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
  *                                 the one-unit gather and streaming scatter
  *                                 (1: whole pages; default: 32 KiB parts of
  *                                 larger pages)
+ *   DSR_TUNE_SLOTS_ORDER          unit order of the large-row token scatters
+ *                                 (plain and re-rotating): 1 per-XCD
+ *                                 layer-major, 2 layer-major in hardware
+ *                                 dispatch order
+ *   DSR_TUNE_SLOTS_WG_PER_CU      workgroups per CU of those kernels
  */
 #define DSR_TUNE_UNITS_PER_GROUP 0
 #define DSR_TUNE_MAX_WG_PER_LAUNCH 1
@@ -96,7 +101,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 #define DSR_TUNE_SCATTER_KERNEL 9
 #define DSR_TUNE_GATHER_SPLIT 10
 #define DSR_TUNE_PAGE_PARTS 11
-#define DSR_TUNE_COUNT_ 12
+#define DSR_TUNE_SLOTS_ORDER 12
+#define DSR_TUNE_SLOTS_WG_PER_CU 13
+#define DSR_TUNE_COUNT_ 14
 
 #define DSR_OK 0
 #define DSR_ERR_ARG (-1)   /* null pointer, negative count, bad enum     */

@@ -596,12 +596,15 @@ def test_rerotate_special_values(gpu, dt):
     KVShape(3, 1, 64, 12, 2),      # 128-byte rows, block size 12 (not a power of two)
 ], ids=["cfg1", "row128", "row512", "row1k", "e4m3_row128", "row64_bs32", "row16",
         "row128_bs12"])
-@pytest.mark.parametrize("unroll", ["default", "4"])
-def test_slots_gather_scatter_match_oracle(gpu, tuning, shape, unroll):
+@pytest.mark.parametrize("unroll,form", [("default", "host"), ("4", "host"),
+                                          ("default", "device")])
+def test_slots_gather_scatter_match_oracle(gpu, tuning, shape, unroll, form):
     """slot_mapping-driven token gather/scatter with ragged requests, partial
     last pages and padding tokens, at each row-size class of the kernels
-    (rows of <= 8 vectors: the packed kernel, at both unrolls)."""
-    print(f"case: slots gather/scatter {shape} unroll {unroll}", flush=True)
+    (rows of <= 8 vectors: the packed kernel, at both unrolls). Host tables
+    scatter whole pages through the page kernel and the rest through the
+    token kernel; device tables take the token kernel for every token."""
+    print(f"case: slots gather/scatter {shape} unroll {unroll} {form}", flush=True)
     if unroll != "default":
         tuning("slots_unroll", int(unroll))
     wl = workloads.config(1) if shape is None else workloads.ragged(
@@ -626,7 +629,11 @@ def test_slots_gather_scatter_match_oracle(gpu, tuning, shape, unroll):
     torch.cuda.synchronize()
     assert np.array_equal(st.cpu().numpy(), ref)
     dst = [torch.zeros_like(c) for c in caches]
-    ops.scatter_slots(ops.LayerTable(dst), sm, ro, st)
+    if form == "device":
+        ops.scatter_slots(ops.LayerTable(dst), torch.from_numpy(sm).to(gpu),
+                          torch.from_numpy(ro).to(gpu), st)
+    else:
+        ops.scatter_slots(ops.LayerTable(dst), sm, ro, st)
     dref = [np.zeros_like(h) for h in host]
     oracle.scatter_slots(dref, sm, ro, ref, shape.layer_bytes)
     torch.cuda.synchronize()
@@ -1120,6 +1127,7 @@ def _token_tables(deltas, rot_dim, gpu, theta=500000.0):
     return idx, position.delta_tables(uniq or [0], rot_dim, theta, device=gpu)
 
 
+@pytest.mark.parametrize("form", ["host", "device"])
 @pytest.mark.parametrize("dt,style,D,R,H,bs", [
     ("bf16", "neox", 128, 128, 8, 16),
     ("bf16", "neox", 128, 96, 2, 16),   # partial rotary, half of 6 vectors
@@ -1131,11 +1139,13 @@ def _token_tables(deltas, rot_dim, gpu, theta=500000.0):
     ("e5m2", "neox", 128, 64, 8, 16),
     ("e5m2", "gptj", 256, 256, 2, 16),
 ])
-def test_slots_rerotate_matches_oracle(gpu, dt, style, D, R, H, bs):
+def test_slots_rerotate_matches_oracle(gpu, dt, style, D, R, H, bs, form):
     """Token-form load with per-request deltas (ragged requests, partial
     pages, padding, requests kept at their position) against the oracle:
-    V bit-exact, K within the rotation tolerance."""
-    print(f"case: slots rerotate {dt} {style} D{D} R{R} H{H} bs{bs}", flush=True)
+    V bit-exact, K within the rotation tolerance. Host tables send whole
+    pages through the page re-rotation; device tables take the token kernel
+    for every token."""
+    print(f"case: slots rerotate {dt} {style} D{D} R{R} H{H} bs{bs} {form}", flush=True)
     L = 3
     shape = KVShape(L, H, D, bs, 1 if dt in FP8 else 2)
     rng = np.random.default_rng(D * 7 + R + H)
@@ -1161,8 +1171,14 @@ def test_slots_rerotate_matches_oracle(gpu, dt, style, D, R, H, bs):
     ks = torch.from_numpy(ks_np).to(gpu) if ks_np is not None else None
     dst = rand_caches(shape, nb, dt, gpu, seed=12)
     dref = [to_bits_np(c, dt) for c in dst]
-    ops.scatter_slots_rerotate(ops.LayerTable(dst), sm, ro, st, tabs, ridx, rot_dim=R,
-                               style=style, k_scale=ks)
+    if form == "device":
+        ops.scatter_slots_rerotate(ops.LayerTable(dst), torch.from_numpy(sm).to(gpu),
+                                   torch.from_numpy(ro).to(gpu), st, tabs,
+                                   torch.as_tensor(np.asarray(ridx, np.int32), device=gpu), rot_dim=R,
+                                   style=style, k_scale=ks)
+    else:
+        ops.scatter_slots_rerotate(ops.LayerTable(dst), sm, ro, st, tabs, ridx, rot_dim=R,
+                                   style=style, k_scale=ks)
     oracle.scatter_slots_rerotate(
         dref, sm, ro, st.cpu().numpy(), shape.layer_bytes, dtype=ORC_DT[dt], rot_dim=R,
         style=0 if style == "neox" else 1, stored_pos=np.zeros(sm.size, np.int64),
@@ -1204,8 +1220,12 @@ def test_slots_rerotate_equals_page_rerotate(gpu, dt, style, R):
     row = shape.num_heads * shape.head_dim * shape.elem_bytes
     ro = (offs[:, None] + np.arange(bs)[None, :] * row).reshape(-1)
     ridx_t = np.repeat(np.asarray(ridx_p, np.int64), bs)
+    # device tables: the token kernel on every token (host tables would send
+    # these whole pages to the page kernel)
     tk = [torch.zeros_like(c) for c in src]
-    ops.scatter_slots_rerotate(ops.LayerTable(tk), sm, ro, st, tabs, ridx_t, rot_dim=R,
+    ops.scatter_slots_rerotate(ops.LayerTable(tk), torch.from_numpy(sm).to(gpu),
+                               torch.from_numpy(ro).to(gpu), st, tabs,
+                               torch.from_numpy(ridx_t.astype(np.int32)).to(gpu), rot_dim=R,
                                style=style, k_scale=ks, layer_group=group)
     torch.cuda.synchronize()
     for l in range(L):
