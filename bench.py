@@ -375,11 +375,27 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
     }
 
 
-def bench_io(torch, dev, budget_bytes: int = 2 << 30, reps: int = 3) -> dict:
+def store_fs(path: str) -> str:
+    """File system type and device of the mount holding ``path``
+    (/proc/mounts, longest matching mount point)."""
+    best, out = "", "unknown"
+    try:
+        for line in open("/proc/mounts"):
+            dev, mnt, fstype = line.split()[:3]
+            if (path == mnt or path.startswith(mnt.rstrip("/") + "/")) and len(mnt) > len(best):
+                best, out = mnt, f"{fstype} on {dev} (mounted at {mnt})"
+    except OSError:
+        pass
+    return out
+
+
+def bench_io(torch, dev, budget_bytes: int = 2 << 30, reps: int = 3,
+             backends=("native", "mmap", "direct")) -> dict:
     """PCIe- and file-inclusive rates of the connector's data plane on a
     sample of config 2's shape: save = gather + device->pinned ring->file,
-    load = file->pinned ring->device + scatter, through KVDataPlane with the
-    native ring, into a store file under $TMPDIR. Not the headline value."""
+    load = file->pinned ring->device + scatter, through KVDataPlane with
+    each ring backend (default ring geometry: 8 x 4 MiB slots), into a store
+    file under $TMPDIR. Not the headline value."""
     import shutil
     import tempfile
 
@@ -391,44 +407,55 @@ def bench_io(torch, dev, budget_bytes: int = 2 << 30, reps: int = 3) -> dict:
     nb = n_pages + 64
     full, caches, _ = fill_caches(torch, shape, nb, "bf16", dev, seed=9)
     named = {f"layer.{i}": c for i, c in enumerate(caches)}
-    d = tempfile.mkdtemp(prefix="daser_bench_")
-    try:
-        plane = KVDataPlane(os.path.join(d, "daser.store"))  # default ring: 8 x 4 MiB
-        plane.register(named)
-        rng = np.random.default_rng(3)
-        blocks = rng.permutation(nb)[:n_pages].tolist()
-        per = 16  # 256-token chunks, one transfer each
-        store = {f"r{i}": ReqStoreSpec(f"k{i}", i, min(per, n_pages - i), blocks[i:i + per],
-                                       i * shape.slot_bytes, per * 16)
-                 for i in range(0, n_pages, per)}
-        sp = plan_store(store, shape.slot_bytes)
-        arena = plane.new_store_arena(sp)
-        load = {k: ReqLoadSpec(v.chunk_key, v.start_slot, v.num_slots, v.block_ids,
-                               v.file_offset, v.token_count) for k, v in store.items()}
-        lp = plan_load(load, shape.slot_bytes)
-        ts, tl = [], []
-        for _ in range(reps):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            plane.save_all(sp, arena)
-            plane.flush(sp, arena)
-            torch.cuda.synchronize()
-            ts.append(time.perf_counter() - t0)
-            t0 = time.perf_counter()
-            plane.load(lp)
-            torch.cuda.synchronize()
-            tl.append(time.perf_counter() - t0)
-        uring = plane.io.uses_io_uring
-        plane.close()
-    finally:
-        shutil.rmtree(d, ignore_errors=True)
-        del full, caches
-        torch.cuda.empty_cache()
+    rng = np.random.default_rng(3)
+    blocks = rng.permutation(nb)[:n_pages].tolist()
+    per = 16  # 256-token chunks, one transfer each
+    store = {f"r{i}": ReqStoreSpec(f"k{i}", i, min(per, n_pages - i), blocks[i:i + per],
+                                   i * shape.slot_bytes, per * 16)
+             for i in range(0, n_pages, per)}
+    sp = plan_store(store, shape.slot_bytes)
+    load = {k: ReqLoadSpec(v.chunk_key, v.start_slot, v.num_slots, v.block_ids,
+                           v.file_offset, v.token_count) for k, v in store.items()}
+    lp = plan_load(load, shape.slot_bytes)
     P = n_pages * shape.slot_bytes
-    return {"payload_bytes": P, "save_GBps": round(P / min(ts) / 1e9, 2),
-            "load_GBps": round(P / min(tl) / 1e9, 2), "io_uring": bool(uring),
-            "sample": f"{n_pages} Llama-3-8B pages ({P / 1e9:.2f} GB) in 256-token chunks, "
-                      f"best of {reps}, store file under {tempfile.gettempdir()}"}
+    out = {"payload_bytes": P, "backends": {},
+           "store_fs": store_fs(os.path.realpath(tempfile.gettempdir())),
+           "sample": f"{n_pages} Llama-3-8B pages ({P / 1e9:.2f} GB) in 256-token chunks "
+                     f"(one {per * shape.slot_bytes >> 20} MiB transfer each), best of {reps}, "
+                     f"store file under {tempfile.gettempdir()}"}
+    for backend in backends:
+        d = tempfile.mkdtemp(prefix="daser_bench_")
+        try:
+            plane = KVDataPlane(os.path.join(d, "daser.store"), io_backend=backend)
+            plane.register(named)
+            arena = plane.new_store_arena(sp)
+            ts, tl = [], []
+            for _ in range(reps):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                plane.save_all(sp, arena)
+                plane.flush(sp, arena)
+                torch.cuda.synchronize()
+                ts.append(time.perf_counter() - t0)
+                t0 = time.perf_counter()
+                plane.load(lp)
+                torch.cuda.synchronize()
+                tl.append(time.perf_counter() - t0)
+            out["backends"][backend] = {"save_GBps": round(P / min(ts) / 1e9, 2),
+                                        "load_GBps": round(P / min(tl) / 1e9, 2),
+                                        "ring": plane.io.backend}
+            plane.close()
+            del arena
+        except Exception as e:  # a backend the file system refuses (O_DIRECT)
+            out["backends"][backend] = {"error": f"{type(e).__name__}: {e}"}
+        finally:
+            shutil.rmtree(d, ignore_errors=True)
+    del full, caches
+    torch.cuda.empty_cache()
+    dflt = out["backends"].get("mmap", {})  # the connector's default backend
+    out["save_GBps"], out["load_GBps"] = dflt.get("save_GBps"), dflt.get("load_GBps")
+    out["default_backend"] = "mmap"
+    return out
 
 
 class _BenchIPC:

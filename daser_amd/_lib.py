@@ -20,7 +20,7 @@ LIB_PATH = os.environ.get("DASER_KV_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so"
 )
 
-DSR_ABI_VERSION = 8
+DSR_ABI_VERSION = 9
 DSR_OK = 0
 DSR_ERR_ARG = -1
 DSR_ERR_ALIGN = -2
@@ -31,6 +31,7 @@ DSR_ERR_NOFILE = -5
 DSR_RING_HOST = 1
 DSR_RING_DIRECT = 2
 DSR_RING_NO_URING = 4
+DSR_RING_MMAP = 8
 
 DSR_DTYPE_BF16 = 0
 DSR_DTYPE_FP16 = 1
@@ -72,6 +73,7 @@ SIGNATURES = {
     "dsr_ring_write": ([_P, _P, _I64, _I64, _P], _I),
     "dsr_ring_read": ([_P, _P, _I64, _I64, _P], _I),
     "dsr_ring_uses_io_uring": ([_P], _I),
+    "dsr_ring_is_mapped": ([_P], _I),
     "dsr_ring_last_errno": ([_P], _I),
     "dsr_ring_close": ([_P], _I),
     "dsr_scatter_rerotate": (

@@ -37,7 +37,12 @@ then lack the attention between chunks that a full prefill would have),
 ``store_path`` may hold ``{rank}``, replaced by the worker's tensor-parallel
 rank (one store file per rank; the reference's single path would make ranks
 overwrite each other's records at the same offsets),
-``io_backend`` ("native": the C++ io_uring ring of libdaser_kv, default;
+``io_backend`` ("mmap", default: the C++ ring of libdaser_kv copying
+between its pinned slots and a shared mapping of the store file on worker
+threads: buffered writes to one file serialise in the kernel, page faults
+on a mapping do not; a disk read error or an outside truncation of the
+store file then faults the process instead of failing the call;
+"native": the same ring with io_uring (pread/pwrite) file calls;
 "direct": the same ring with the store file opened O_DIRECT;
 "python": the threaded ring of store_io.PinnedRingIO), ``k_scale`` (one K
 scale for every layer of an fp8 cache, when the attention modules' own
@@ -341,7 +346,7 @@ class DaserConnector(KVConnectorBase_V1):
                 io_slots=int(extra.get("io_slots", 8)),
                 io_readers=int(extra.get("io_readers", 4)),
                 io_timeout=extra.get("io_timeout_s", 120.0),
-                io_backend=extra.get("io_backend", "native"),
+                io_backend=extra.get("io_backend", "mmap"),
                 save_stream=extra.get("save_stream", "auto"),
                 cache_geometry=geometry,
             )

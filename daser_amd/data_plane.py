@@ -72,6 +72,22 @@ def plan_store(reqs: dict[str, ReqStoreSpec], slot_bytes: int) -> StorePlan:
     return StorePlan(np.asarray(ids, np.int32), offs, transfers, base)
 
 
+def coalesce_transfers(transfers) -> list[tuple[list[str], int, int, int]]:
+    """The step's store transfers with neighbours merged: consecutive
+    requests whose records follow each other in the arena and in the file
+    become one ring call ((keys, arena_off, nbytes, file_off) each), so the
+    ring's pipeline does not drain between them."""
+    out: list[tuple[list[str], int, int, int]] = []
+    for key, off, nbytes, file_off in transfers:
+        if out:
+            keys, o, n, f = out[-1]
+            if o + n == off and f + n == file_off:
+                out[-1] = (keys + [key], o, n + nbytes, f)
+                continue
+        out.append(([key], off, nbytes, file_off))
+    return out
+
+
 def plan_load(reqs: dict[str, ReqLoadSpec], slot_bytes: int) -> LoadPlan:
     """Each segment's records are read once into the arena; page j of a
     segment scatters record j into block_ids[block_offset + j]. A segment
@@ -157,15 +173,15 @@ class KVDataPlane:
                  inv_freq: Optional[np.ndarray] = None, rope_scaling: Optional[dict] = None,
                  save_mode: str = "per_layer",
                  io_slot_bytes: int = 4 << 20, io_slots: int = 8,
-                 io_backend: str = "native", save_stream: str = "auto",
+                 io_backend: str = "mmap", save_stream: str = "auto",
                  k_scales: Optional[torch.Tensor] = None, io_readers: int = 4,
                  layer_rope: Optional[list] = None,
                  io_timeout: Optional[float] = 120.0,
                  cache_geometry: Optional[dict] = None) -> None:
         if save_mode not in ("per_layer", "deferred"):
             raise ValueError("save_mode must be 'per_layer' or 'deferred'")
-        if io_backend not in ("native", "direct", "python"):
-            raise ValueError("io_backend must be 'native', 'direct' or 'python'")
+        if io_backend not in ("native", "mmap", "direct", "python"):
+            raise ValueError("io_backend must be 'native', 'mmap', 'direct' or 'python'")
         if save_stream not in ("side", "current", "auto"):
             raise ValueError("save_stream must be 'side', 'current' or 'auto'")
         self.io_backend = io_backend
@@ -281,7 +297,8 @@ class KVDataPlane:
             return PinnedRingIO(self.store_path, device, slot_bytes=self._io_slot_bytes,
                                 n_slots=self._io_slots)
         return NativeRingIO(self.store_path, device, slot_bytes=self._io_slot_bytes,
-                            n_slots=self._io_slots, direct=self.io_backend == "direct")
+                            n_slots=self._io_slots, direct=self.io_backend == "direct",
+                            mapped=self.io_backend == "mmap")
 
     @property
     def device(self) -> torch.device:
@@ -384,10 +401,10 @@ class KVDataPlane:
             err: Optional[BaseException] = None
             try:
                 ev.synchronize()  # the gathers into this arena have run
-                for key, off, nbytes, file_off in plan.transfers:
+                for group, off, nbytes, file_off in coalesce_transfers(plan.transfers):
                     self._wio.write_from_device(arena[off:off + nbytes], file_off,
                                                 self._idle_stream)
-                    keys.append(key)
+                    keys.extend(group)
             except BaseException as e:  # reported, never lost on the thread
                 err = e
             done(keys, err)
@@ -409,9 +426,9 @@ class KVDataPlane:
             producer = torch.cuda.current_stream(self.device)  # resolved on this thread
 
         def run() -> None:
-            for key, off, nbytes, file_off in plan.transfers:
+            for group, off, nbytes, file_off in coalesce_transfers(plan.transfers):
                 self.io.write_from_device(arena[off:off + nbytes], file_off, producer)
-                keys.append(key)
+                keys.extend(group)
 
         self._io_call(run, "store write")
         return keys

@@ -300,7 +300,7 @@ class NativeRingIO:
 
     def __init__(self, path: str, device: torch.device | str = "cuda",
                  slot_bytes: int = 4 << 20, n_slots: int = 8, use_io_uring: bool = True,
-                 direct: bool = False) -> None:
+                 direct: bool = False, mapped: bool = False) -> None:
         import ctypes
 
         from daser_amd import _lib
@@ -315,6 +315,8 @@ class NativeRingIO:
             flags |= _lib.DSR_RING_NO_URING
         if direct:
             flags |= _lib.DSR_RING_DIRECT
+        if mapped:
+            flags |= _lib.DSR_RING_MMAP
         h = ctypes.c_void_p()
         rc = _lib.lib().dsr_ring_open(path.encode(), int(slot_bytes), int(n_slots), flags,
                                       ctypes.byref(h))
@@ -335,8 +337,12 @@ class NativeRingIO:
 
     @property
     def backend(self) -> str:
-        """How file I/O is done ("io_uring" or "posix", "+O_DIRECT"); the
-        counterpart of GDSTransferLayer.backend (gds_transfer.py:37-60)."""
+        """How file I/O is done ("mmap", "io_uring" or "posix", "+O_DIRECT");
+        the counterpart of GDSTransferLayer.backend (gds_transfer.py:37-60).
+        A mapped ring writes past the end of the file through io_uring or
+        posix calls."""
+        if self._lib.lib().dsr_ring_is_mapped(self._handle()):
+            return "mmap"
         return ("io_uring" if self.uses_io_uring else "posix") + ("+O_DIRECT" if self._direct
                                                                   else "")
 

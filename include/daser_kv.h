@@ -49,9 +49,10 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 /* Bumped whenever an entry point's signature changes or one is added:
  * 2 layer_group on the re-rotation, 3 dsr_scatter_rerotate_kx, 4 the
  * re-rotations' flags, 5 the head-major (_hnd) entry points, 6
- * dsr_set_tuning, 7 dsr_scatter_ex, 8 dsr_scatter_slots_rerotate. Callers check
- * dsr_abi_version() against it. */
-#define DSR_ABI_VERSION 8
+ * dsr_set_tuning, 7 dsr_scatter_ex, 8 dsr_scatter_slots_rerotate, 9
+ * DSR_RING_MMAP and dsr_ring_is_mapped. Callers check dsr_abi_version()
+ * against it. */
+#define DSR_ABI_VERSION 9
 
 /*
  * Kernel choice and launch shape follow from the geometry. dsr_set_tuning()
@@ -408,6 +409,18 @@ typedef struct dsr_ring dsr_ring;
                                then 4 KiB-aligned pageable memory (O_DIRECT
                                cannot use hipHostMalloc'd pages)            */
 #define DSR_RING_NO_URING 4 /* use pread/pwrite even if io_uring works       */
+#define DSR_RING_MMAP 8     /* copy between the pinned slots and a shared
+                               mapping of the file on worker threads (up to
+                               8, one per slot) instead of read/write calls:
+                               buffered writes to one file serialise in the
+                               kernel, page faults on a mapping do not. A
+                               write first allocates the blocks of its range
+                               (fallocate: ENOSPC is DSR_ERR_IO, not a fault);
+                               a write past the end of the file goes through
+                               pwrite/io_uring.
+                               Not with DSR_RING_DIRECT (DSR_ERR_ARG). The
+                               file must not be truncated while the ring is
+                               open (a mapped access past its end faults)  */
 
 /* Opens `path` (must exist: DSR_ERR_NOFILE otherwise) and allocates the
  * ring. slot_bytes <= 2^31 - 1, 1 <= n_slots <= 65535. */
@@ -430,6 +443,10 @@ int dsr_ring_read(dsr_ring* ring, void* dst, int64_t nbytes, int64_t file_offset
 
 /* 1 if transfers go through io_uring, 0 if through pread/pwrite. */
 int dsr_ring_uses_io_uring(const dsr_ring* ring);
+
+/* 1 if the ring was opened with DSR_RING_MMAP. No counterpart in the
+ * reference (its GDSTransferLayer.backend names kvikio's mode). */
+int dsr_ring_is_mapped(const dsr_ring* ring);
 
 /* errno of the last failed file operation on this ring (0 if none). */
 int dsr_ring_last_errno(const dsr_ring* ring);

@@ -1,6 +1,7 @@
 // The staging ring (store_ring.cpp) in host mode, built with AddressSanitizer
 // and UndefinedBehaviorSanitizer (host code only; no GPU): random transfer
-// sizes and offsets through every slot geometry, io_uring and pread/pwrite,
+// sizes and offsets through every slot geometry, io_uring, pread/pwrite and
+// the mapped mode's worker threads,
 // each read checked against what was written, and a read past the end of the
 // file. Exit 0 and "ring sanitize ok" when clean; a sanitizer report aborts.
 #include <fcntl.h>
@@ -15,7 +16,7 @@ int main() {
   char path[] = "/tmp/dsr_ring_san_XXXXXX";
   int fd = mkstemp(path); ftruncate(fd, 8 << 20); close(fd);
   std::mt19937 rng(1);
-  for (int flags : {DSR_RING_HOST, DSR_RING_HOST | DSR_RING_NO_URING}) {
+  for (int flags : {DSR_RING_HOST, DSR_RING_HOST | DSR_RING_NO_URING, DSR_RING_HOST | DSR_RING_MMAP}) {
     for (long slot : {4096L, 8192L, 65536L, 80000L}) {
       for (int ns : {1, 2, 3, 8}) {
         dsr_ring* r = nullptr;

@@ -68,7 +68,8 @@ def _file_records(path, start_slot, n):
     ("per_layer", "native", "side"), ("deferred", "native", "side"),
     ("per_layer", "python", "side"), ("per_layer", "native", "current"),
     ("deferred", "python", "current"), ("per_layer", "direct", "side"),
-    ("per_layer", "native", "auto-side"), ("per_layer", "native", "auto-current")])
+    ("per_layer", "native", "auto-side"), ("per_layer", "native", "auto-current"),
+    ("per_layer", "mmap", "side"), ("deferred", "mmap", "current")])
 def test_save_writes_reference_layout(gpu, tmp_path, monkeypatch, mode, backend, stream):
     print(f"case: connector save {mode} {backend} {stream}", flush=True)
     if stream.startswith("auto"):
@@ -101,16 +102,17 @@ def test_save_writes_reference_layout(gpu, tmp_path, monkeypatch, mode, backend,
     w.shutdown()
 
 
-def test_load_round_trip_into_other_blocks(gpu, tmp_path):
-    print("case: connector load", flush=True)
-    w, _ = _worker(tmp_path)
+@pytest.mark.parametrize("backend", ["native", "mmap"])
+def test_load_round_trip_into_other_blocks(gpu, tmp_path, backend):
+    print(f"case: connector load {backend}", flush=True)
+    w, _ = _worker(tmp_path, io_backend=backend)
     caches = rand_caches(SHAPE, 16, "bf16", gpu, seed=32)
     named = _named(caches)
     w.register_kv_caches(named)
     _save(w, named, _store_reqs())
     w.shutdown()
 
-    r, _ = _worker(tmp_path)
+    r, _ = _worker(tmp_path, io_backend=backend)
     fresh = [torch.zeros_like(c) for c in caches]
     r.register_kv_caches(_named(fresh))
     slot = SHAPE.slot_bytes
@@ -363,7 +365,7 @@ def test_fp8_load_rerotates_with_module_scales(gpu, tmp_path):
     w2.shutdown()
 
 
-@pytest.mark.parametrize("backend", ["native", "python"])
+@pytest.mark.parametrize("backend", ["native", "python", "mmap"])
 def test_async_save_survives_immediate_block_reuse(gpu, tmp_path, backend):
     """async_save: wait_for_save returns before the file writes; the next
     step's KV writes to the same blocks (enqueued at once on the current

@@ -36,6 +36,18 @@ def test_plan_store_layout_matches_reference_offsets():
     assert p.arena_bytes == 4 * SLOT
 
 
+def test_coalesce_transfers_merges_file_neighbours():
+    from daser_amd.data_plane import coalesce_transfers
+
+    t = [("a", 0, 3 * SLOT, 10 * SLOT), ("b", 3 * SLOT, SLOT, 13 * SLOT),
+         ("c", 4 * SLOT, 2 * SLOT, 2 * SLOT), ("d", 6 * SLOT, SLOT, 4 * SLOT),
+         ("e", 7 * SLOT, SLOT, 20 * SLOT)]
+    assert coalesce_transfers(t) == [(["a", "b"], 0, 4 * SLOT, 10 * SLOT),
+                                     (["c", "d"], 4 * SLOT, 3 * SLOT, 2 * SLOT),
+                                     (["e"], 7 * SLOT, SLOT, 20 * SLOT)]
+    assert coalesce_transfers([]) == []
+
+
 def test_plan_load_without_positions_is_plain_scatter():
     reqs = {"r": C.ReqLoadSpec("k", start_slot=4, num_slots=2, block_ids=[11, 3],
                                file_offset=4 * SLOT, token_count=20)}

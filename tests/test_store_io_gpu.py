@@ -1,7 +1,8 @@
 """The staging rings against the reference's own transfer-layer tests
 (reference tests/connector/test_gds_transfer.py:31-90: backend set, 1 MB
 round trip with byte counts, two regions at different offsets, context
-manager, missing file), run on device tensors for both rings."""
+manager, missing file), run on device tensors for each ring (the native
+ring also in its mapped mode)."""
 
 import asyncio
 
@@ -12,7 +13,8 @@ from daser_amd.store_io import NativeRingIO, PinnedRingIO, preallocate_store
 
 pytestmark = pytest.mark.gpu
 
-RINGS = {"native": NativeRingIO, "python": PinnedRingIO}
+RINGS = {"native": NativeRingIO, "python": PinnedRingIO,
+         "mmap": lambda path, dev, **kw: NativeRingIO(path, dev, mapped=True, **kw)}
 
 
 @pytest.fixture()
@@ -30,7 +32,7 @@ def _run(coro):
 def test_backend_is_set(gpu, store_file, ring):
     print(f"case: ring backend {ring}", flush=True)
     io = RINGS[ring](store_file, gpu)
-    assert io.backend in ("io_uring", "posix", "threads")
+    assert io.backend in ("io_uring", "posix", "threads", "mmap")
     io.close()
 
 

@@ -20,13 +20,18 @@ def store(tmp_path):
     return path
 
 
-@pytest.mark.parametrize("uring", [True, False])
-def test_round_trip_many_pieces(store, uring):
-    rng = np.random.default_rng(uring)
+MODES = {"io_uring": dict(use_io_uring=True), "posix": dict(use_io_uring=False),
+         "mmap": dict(mapped=True)}
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_round_trip_many_pieces(store, mode):
+    rng = np.random.default_rng(len(mode))
     src = torch.from_numpy(rng.integers(0, 256, 1_000_003, dtype=np.uint8))
-    with NativeRingIO(store, "cpu", slot_bytes=65536, n_slots=3, use_io_uring=uring) as io:
-        if uring:
+    with NativeRingIO(store, "cpu", slot_bytes=65536, n_slots=3, **MODES[mode]) as io:
+        if mode == "io_uring":
             assert io.uses_io_uring
+        assert io.backend == ("mmap" if mode == "mmap" else io.backend)
         assert io.write_from_device(src, 8192) == src.numel()
         dst = torch.zeros_like(src)
         io.read_into_device(dst, 8192)
@@ -53,8 +58,9 @@ def test_missing_file(tmp_path):
         NativeRingIO(str(tmp_path / "absent"), "cpu")
 
 
-def test_read_past_end_is_an_error(store):
-    with NativeRingIO(store, "cpu", slot_bytes=8192, n_slots=2) as io:
+@pytest.mark.parametrize("mode", list(MODES))
+def test_read_past_end_is_an_error(store, mode):
+    with NativeRingIO(store, "cpu", slot_bytes=8192, n_slots=2, **MODES[mode]) as io:
         with pytest.raises(StoreIOError):
             io.read_into_device(torch.zeros(100_000, dtype=torch.uint8), (4 << 20) - 5000)
         # the ring keeps working afterwards
@@ -114,8 +120,52 @@ def test_direct_io_round_trip_and_alignment(store, uring):
     assert e.value.code == DSR_ERR_ALIGN
 
 
-@pytest.mark.parametrize("uring", [True, False])
-def test_randomized_transfers_from_several_threads(tmp_path, uring):
+def test_mapped_write_past_the_end_extends_the_file(store):
+    """A mapped ring writes beyond the end of the file through pwrite (the
+    mapping cannot grow the file); later reads there are mapped."""
+    rng = np.random.default_rng(8)
+    data = torch.from_numpy(rng.integers(0, 256, 300_000, dtype=np.uint8))
+    end = 4 << 20
+    with NativeRingIO(store, "cpu", slot_bytes=65536, n_slots=4, mapped=True) as io:
+        io.write_from_device(data, end - 1000)
+        assert os.path.getsize(store) == end - 1000 + data.numel()
+        back = torch.zeros_like(data)
+        io.read_into_device(back, end - 1000)
+        assert torch.equal(back, data)
+        # inside the file again: overwrite part of it through the mapping
+        io.write_from_device(data[:5000], 0)
+        io.read_into_device(back[:5000], 0)
+        assert torch.equal(back[:5000], data[:5000])
+
+
+def test_mapped_write_keeps_neighbour_bytes(store):
+    """A mapped write changes exactly its range: bytes of the pages at its
+    ends that lie outside it keep their values."""
+    rng = np.random.default_rng(9)
+    base = torch.from_numpy(rng.integers(1, 256, 3 * 4096, dtype=np.uint8))
+    with NativeRingIO(store, "cpu", slot_bytes=8192, n_slots=2) as plain:
+        plain.write_from_device(base, 40960)
+    patch = torch.zeros(4096 + 100, dtype=torch.uint8)
+    with NativeRingIO(store, "cpu", slot_bytes=8192, n_slots=2, mapped=True) as io:
+        io.write_from_device(patch, 40960 + 2000)
+    want = base.clone()
+    want[2000:2000 + patch.numel()] = 0
+    with open(store, "rb") as f:
+        f.seek(40960)
+        got = np.frombuffer(f.read(want.numel()), np.uint8)
+    assert np.array_equal(got, want.numpy())
+
+
+def test_mapped_and_direct_are_exclusive(store):
+    from daser_amd._lib import DSR_ERR_ARG, DaserKVError
+
+    with pytest.raises(DaserKVError) as e:
+        NativeRingIO(store, "cpu", slot_bytes=8192, mapped=True, direct=True)
+    assert e.value.code == DSR_ERR_ARG
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_randomized_transfers_from_several_threads(tmp_path, mode):
     """Random sizes and offsets (pieces shorter and longer than a slot, odd
     lengths) from four threads, each with its own ring on one file over
     disjoint regions, and a shared ring used by two threads at once (its
@@ -126,7 +176,7 @@ def test_randomized_transfers_from_several_threads(tmp_path, uring):
     size = 8 << 20
     preallocate_store(path, size)
     model = np.zeros(size, np.uint8)
-    shared = NativeRingIO(path, "cpu", slot_bytes=8192, n_slots=3, use_io_uring=uring)
+    shared = NativeRingIO(path, "cpu", slot_bytes=8192, n_slots=3, **MODES[mode])
     errors = []
 
     def worker(t: int, ring) -> None:
@@ -145,7 +195,7 @@ def test_randomized_transfers_from_several_threads(tmp_path, uring):
         except BaseException as e:  # reported on the main thread
             errors.append(e)
 
-    own = [NativeRingIO(path, "cpu", slot_bytes=int(s), n_slots=int(k), use_io_uring=uring)
+    own = [NativeRingIO(path, "cpu", slot_bytes=int(s), n_slots=int(k), **MODES[mode])
            for s, k in ((4096, 1), (16384, 2), (65536, 4), (5000 * 16, 3))]
     threads = [threading.Thread(target=worker, args=(t, r)) for t, r in enumerate(own)]
     threads += [threading.Thread(target=worker, args=(4 + t, shared)) for t in range(2)]
