@@ -20,13 +20,15 @@ LIB_PATH = os.environ.get("DASER_KV_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so"
 )
 
-DSR_ABI_VERSION = 9
+DSR_ABI_VERSION = 10
 DSR_OK = 0
 DSR_ERR_ARG = -1
 DSR_ERR_ALIGN = -2
 DSR_ERR_SHAPE = -3
 DSR_ERR_IO = -4
 DSR_ERR_NOFILE = -5
+DSR_ERR_TOO_LARGE = -6
+DSR_STATIC_TABLE_BYTES = 4 << 20
 
 DSR_RING_HOST = 1
 DSR_RING_DIRECT = 2
@@ -77,6 +79,10 @@ SIGNATURES = {
     "dsr_ring_last_errno": ([_P], _I),
     "dsr_ring_close": ([_P], _I),
     "dsr_scatter_rerotate": (
+        _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, ctypes.c_uint, _P],
+        _I,
+    ),
+    "dsr_scatter_rerotate_static": (
         _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, ctypes.c_uint, _P],
         _I,
     ),

@@ -49,6 +49,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "daser_kv.h"
 
 #include "kv_common.h"
@@ -421,6 +423,8 @@ const char* dsr_error_string(int code) {
       return "store file read or write failed (see dsr_ring_last_errno)";
     case DSR_ERR_NOFILE:
       return "store file not found";
+    case DSR_ERR_TOO_LARGE:
+      return "tables exceed the library's static table area (DSR_STATIC_TABLE_BYTES)";
     default:
       return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
@@ -1081,6 +1085,125 @@ int dsr_scatter_slots_rerotate(const uint64_t* layer_base, int n_layers, int64_t
                                n_tokens, staging, staging_bytes, layer_bytes, layer0, cos_sin,
                                rope_idx, n_tables, layer_group, n_groups, head_dim, rot_dim,
                                rope_style, dtype, k_scale, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free load with re-rotation (dsr_scatter_rerotate_static).
+//
+// dsr_scatter_rerotate reads its tables (layer addresses, page ids, record
+// offsets, table indices, angle tables, layer groups, scales) from device
+// memory that the caller allocates per call. This variant takes them in host
+// memory and stages them in `scratch`, a fixed device array of the library,
+// then runs the same kernels on the staged copies. Each GPU holds its own
+// copy of the array; its device address comes from hipGetSymbolAddress on
+// the first call on that device (the array's name is a host-side stand-in
+// and is never passed to a kernel or a copy).
+
+namespace {
+
+static __device__ __align__(256) uint8_t scratch[DSR_STATIC_TABLE_BYTES];
+
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices];  // per device, set once
+
+// Device address of `scratch` on the current device (nullptr and *rc set
+// on failure).
+uint8_t* scratch_on_current_device(int* rc) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *rc = (int)e;
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *rc = DSR_ERR_ARG;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *rc = e != hipSuccess ? (int)e : DSR_ERR_ARG;
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+int64_t round256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+}  // namespace
+
+extern "C" {
+
+int dsr_scatter_rerotate_static(const uint64_t* layer_base, int n_layers,
+                                int64_t kv_stride, int64_t page_stride,
+                                int64_t page_bytes, int64_t num_blocks,
+                                const int32_t* page_ids, const int64_t* slot_offsets,
+                                int n_pages, const void* staging,
+                                int64_t staging_bytes, int64_t layer_bytes,
+                                int layer0, const float* cos_sin,
+                                const int32_t* rope_idx, int n_tables,
+                                const int32_t* layer_group, int n_groups, int head_dim,
+                                int rot_dim, int rope_style, int dtype,
+                                const float* k_scale, unsigned flags, dsr_stream_t stream) {
+  if (n_pages < 0 || n_layers < 0 || layer0 < 0 || n_tables < 0 ||
+      (layer_group && n_groups < 1))
+    return DSR_ERR_ARG;
+  if (n_pages == 0 || n_layers == 0) return DSR_OK;
+  if (!layer_base || !page_ids || !slot_offsets || !rope_idx || (n_tables > 0 && !cos_sin))
+    return DSR_ERR_ARG;
+  if (rot_dim <= 0 || (rot_dim & 1) || rot_dim / 2 > kMaxRotHalf) return DSR_ERR_SHAPE;
+  const int64_t rec_layers = (int64_t)layer0 + n_layers;  // entries of per-layer tables
+  const int64_t groups = layer_group ? n_groups : 1;
+  // packed sections of the staged tables, each 256-byte aligned
+  const int64_t sz_base = (int64_t)n_layers * 8;
+  const int64_t sz_ids = (int64_t)n_pages * 4;
+  const int64_t sz_off = (int64_t)n_pages * 8;
+  const int64_t sz_idx = (int64_t)n_pages * 4;
+  const int64_t sz_cs = groups * n_tables * (rot_dim / 2) * 8;
+  const int64_t sz_grp = layer_group ? rec_layers * 4 : 0;
+  const int64_t sz_scl = k_scale ? rec_layers * 4 : 0;
+  const int64_t o_base = 0, o_ids = o_base + round256(sz_base), o_off = o_ids + round256(sz_ids),
+                o_idx = o_off + round256(sz_off), o_cs = o_idx + round256(sz_idx),
+                o_grp = o_cs + round256(sz_cs), o_scl = o_grp + round256(sz_grp),
+                total = o_scl + round256(sz_scl);
+  if (total > DSR_STATIC_TABLE_BYTES) return DSR_ERR_TOO_LARGE;
+
+  hipStream_t s = (hipStream_t)stream;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cap);
+  if (e != hipSuccess) return (int)e;
+  if (cap != hipStreamCaptureStatusNone) return DSR_ERR_ARG;  // host-to-device copies
+
+  int rc = DSR_OK;
+  uint8_t* base = scratch_on_current_device(&rc);
+  if (!base) return rc;
+  struct Piece {
+    int64_t off, bytes;
+    const void* src;
+  } pieces[] = {{o_base, sz_base, layer_base}, {o_ids, sz_ids, page_ids},
+                {o_off, sz_off, slot_offsets}, {o_idx, sz_idx, rope_idx},
+                {o_cs, sz_cs, cos_sin},       {o_grp, sz_grp, layer_group},
+                {o_scl, sz_scl, k_scale}};
+  for (const Piece& p : pieces) {
+    if (p.bytes == 0) continue;
+    e = hipMemcpyAsync(base + p.off, p.src, (size_t)p.bytes, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return (int)e;
+  }
+  return scatter_rerotate_any(
+      reinterpret_cast<const uint64_t*>(base + o_base), n_layers, kv_stride, page_stride,
+      page_bytes, num_blocks, reinterpret_cast<const int32_t*>(base + o_ids),
+      reinterpret_cast<const int64_t*>(base + o_off), n_pages, staging, staging_bytes,
+      layer_bytes, layer0, sz_cs ? reinterpret_cast<const float*>(base + o_cs) : nullptr,
+      reinterpret_cast<const int32_t*>(base + o_idx), n_tables,
+      layer_group ? reinterpret_cast<const int32_t*>(base + o_grp) : nullptr, n_groups,
+      head_dim, rot_dim, rope_style, dtype,
+      k_scale ? reinterpret_cast<const float*>(base + o_scl) : nullptr, 0, 0, flags, stream);
 }
 
 }  // extern "C"

@@ -50,9 +50,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
  * 2 layer_group on the re-rotation, 3 dsr_scatter_rerotate_kx, 4 the
  * re-rotations' flags, 5 the head-major (_hnd) entry points, 6
  * dsr_set_tuning, 7 dsr_scatter_ex, 8 dsr_scatter_slots_rerotate, 9
- * DSR_RING_MMAP and dsr_ring_is_mapped. Callers check dsr_abi_version()
- * against it. */
-#define DSR_ABI_VERSION 9
+ * DSR_RING_MMAP and dsr_ring_is_mapped, 10 dsr_scatter_rerotate_static.
+ * Callers check dsr_abi_version() against it. */
+#define DSR_ABI_VERSION 10
 
 /*
  * Kernel choice and launch shape follow from the geometry. dsr_set_tuning()
@@ -112,6 +112,7 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 #define DSR_ERR_SHAPE (-3) /* rot_dim/head_dim/page geometry inconsistent */
 #define DSR_ERR_IO (-4)    /* store-file read/write failed or came up short */
 #define DSR_ERR_NOFILE (-5) /* store file does not exist                  */
+#define DSR_ERR_TOO_LARGE (-6) /* tables exceed DSR_STATIC_TABLE_BYTES      */
 
 /* Element types understood by the re-rotation kernel. Plain gather/scatter
  * is dtype-agnostic (raw bytes, bit-exact for every dtype incl. fp8). */
@@ -253,6 +254,45 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
                          const float* k_scale, unsigned flags, dsr_stream_t stream);
+
+/*
+ * Allocation-free form of dsr_scatter_rerotate. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, kernels and bytes as dsr_scatter_rerotate,
+ * except that layer_base, page_ids, slot_offsets, cos_sin, rope_idx,
+ * layer_group and k_scale are HOST arrays: the call copies them
+ * (hipMemcpyAsync on `stream`) into a fixed device array of the library
+ * (DSR_STATIC_TABLE_BYTES per GPU, held until the process ends) and launches
+ * on those copies. It calls no allocating routine.
+ *
+ * Limits and contracts:
+ *   - the staged tables, each section rounded up to 256 bytes (layer_base 8 B
+ *     per layer; page_ids 4, slot_offsets 8 and rope_idx 4 B per page;
+ *     cos_sin n_groups * n_tables * rot_dim / 2 * 8 B; layer_group and
+ *     k_scale 4 B per record layer), must fit in DSR_STATIC_TABLE_BYTES,
+ *     else DSR_ERR_TOO_LARGE without any copy or launch (4 MiB holds e.g.
+ *     130,000 pages of one layer group with 64 angle tables);
+ *   - the host arrays must stay unchanged until `stream` has completed the
+ *     call's work;
+ *   - calls share the GPU's one array: calls on one stream are ordered, but
+ *     calls that overlap on one GPU from different streams (or threads on
+ *     different streams) race and must be serialised by the caller;
+ *   - the device current on the calling thread must be the stream's device;
+ *   - a stream under graph capture returns DSR_ERR_ARG (the host-to-device
+ *     table copies cannot be captured).
+ */
+#define DSR_STATIC_TABLE_BYTES (4 << 20)
+int dsr_scatter_rerotate_static(const uint64_t* layer_base, int n_layers,
+                                int64_t kv_stride, int64_t page_stride,
+                                int64_t page_bytes, int64_t num_blocks,
+                                const int32_t* page_ids, const int64_t* slot_offsets,
+                                int n_pages, const void* staging,
+                                int64_t staging_bytes, int64_t layer_bytes,
+                                int layer0, const float* cos_sin,
+                                const int32_t* rope_idx, int n_tables,
+                                const int32_t* layer_group, int n_groups, int head_dim,
+                                int rot_dim, int rope_style, int dtype,
+                                const float* k_scale, unsigned flags, dsr_stream_t stream);
 
 /*
  * dsr_scatter_rerotate for caches whose K page uses the split-x layout of
