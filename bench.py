@@ -1013,6 +1013,10 @@ def main() -> int:
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 4 GiB device copy (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--tune", default="",
+                    help="launch-shape overrides for a measurement, as knob=value pairs "
+                         "separated by commas (daser_amd._lib.TUNE names); the bytes moved "
+                         "are the same")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the KV path shards per rank with no "
@@ -1025,6 +1029,13 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.tune:
+        from daser_amd import _lib
+
+        for kv in args.tune.split(","):
+            k, v = kv.split("=")
+            _lib.set_tuning(k.strip(), v.strip() if k.strip() == "rot_kernel" else int(v))
+        log(f"[bench] tuning overrides: {args.tune}")
     configs = [int(c) for c in args.configs.split(",") if c]
     res = {}
     if args.calibrate:
