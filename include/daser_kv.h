@@ -212,8 +212,10 @@ int dsr_scatter_ex(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
  *
  * fp8 (DSR_DTYPE_FP8_E4M3): x = e4m3(q) * k_scale[layer0 + l], rotate,
  * q' = e4m3_rne(clamp(y / k_scale, -448, 448)); NaN stays NaN (0x7F).
- * fp8 (DSR_DTYPE_FP8_E5M2): the same with e5m2 and +-57344 (infinities
- * saturate too); NaN -> 0x7F.
+ * fp8 (DSR_DTYPE_FP8_E5M2): the same with e5m2 and +-57344; infinities
+ * saturate too (a saturate-to-finite encode, the mode vLLM's fp8 cache
+ * writes use, not torch's float8_e5m2 cast, which keeps infinities); NaN
+ * -> 0x7F.
  * bf16/fp16: round-to-nearest-even from fp32; NaN -> canonical quiet NaN.
  *
  * The reference has no re-rotation (daser/position/fixed_offset.py:11-50
