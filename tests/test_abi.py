@@ -114,3 +114,24 @@ def test_set_tuning_checks_and_no_environment_reads():
     for name in os.listdir(csrc):
         with open(os.path.join(csrc, name)) as f:
             assert "getenv" not in f.read(), name
+
+
+def test_static_rerotate_argument_errors():
+    """dsr_scatter_rerotate_static checks its host tables' sizes against the
+    library's fixed table area before any copy or launch."""
+    lib = _lib.lib()
+
+    def call(n_pages=1, page_ids=32, rot_dim=128, n_tables=1, layer_group=None, n_groups=0):
+        return lib.dsr_scatter_rerotate_static(
+            16, 1, 4096, 4096, 4096, 8, page_ids, 48, n_pages, 64, 1 << 20, 8192, 0, 96, 112,
+            n_tables, layer_group, n_groups, 128, rot_dim, 0, 0, None, 0, None)
+
+    n_max = _lib.DSR_STATIC_TABLE_BYTES // 16  # 16 table bytes per page
+    assert call(n_pages=n_max + 1) == _lib.DSR_ERR_TOO_LARGE
+    assert call(n_tables=_lib.DSR_STATIC_TABLE_BYTES // (64 * 8) + 1) == _lib.DSR_ERR_TOO_LARGE
+    assert call(n_pages=0) == _lib.DSR_OK
+    assert call(page_ids=None) == _lib.DSR_ERR_ARG
+    assert call(n_pages=-1) == _lib.DSR_ERR_ARG
+    assert call(rot_dim=127) == _lib.DSR_ERR_SHAPE
+    assert call(layer_group=128, n_groups=0) == _lib.DSR_ERR_ARG
+    assert b"static table" in lib.dsr_error_string(_lib.DSR_ERR_TOO_LARGE)

@@ -99,11 +99,3 @@ def test_static_matches_device_table_entry_point(dt):
         v_want = rec[torch.from_numpy(slot_offsets // slot).to(dev), 3, 1]
         assert torch.equal(v_got.reshape(n_pages, -1), v_want)
 
-
-def test_static_rejects_tables_beyond_the_limit():
-    lib = _lib.lib()
-    n = _lib.DSR_STATIC_TABLE_BYTES // 16 + 1  # 16 table bytes per page
-    rc = lib.dsr_scatter_rerotate_static(16, 1, 4096, 4096, 4096, 8, 32, 48, n, 64, 1 << 20,
-                                         8192, 0, 96, 112, 1, None, 0, 128, 128, 0, 0, None,
-                                         0, None)
-    assert rc == _lib.DSR_ERR_TOO_LARGE
