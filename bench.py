@@ -819,6 +819,55 @@ def bench_patterns(torch, ops, dev, reps: int = 5) -> dict:
     return out
 
 
+def bench_ceilings(torch, dev, nbytes: int = 16 << 30, reps: int = 5) -> dict:
+    """Plain streams over `nbytes` buffers (daser_amd/csrc/bw_probe.hip):
+    read-only, write-only and copy, one workgroup per unit of 16, 32 or 64
+    KiB at 1, 2, 4 or 8 workgroups per CU; best HIP-event time of `reps`
+    launches each. Bytes counted: read or written once (copy: both). The
+    harmonic mean of the best read and write rates is what a copy that
+    alternates the two directions at those rates would sustain."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "daser_amd", "libdaser_bwprobe.so"))
+    fn = lib.dsr_bw_probe
+    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                   ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(2)
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = {}
+    for op, name in ((0, "read"), (1, "write"), (2, "copy")):
+        moved = nbytes * (2 if op == 2 else 1)
+        sweep = []
+        for unit in (16 << 10, 32 << 10, 64 << 10):
+            for wpc in (1, 2, 4, 8):
+                def launch():
+                    rc = fn(op, a.data_ptr(), b.data_ptr(), nbytes, unit, wpc, sink.data_ptr(),
+                            stream)
+                    if rc:
+                        raise RuntimeError(f"dsr_bw_probe failed with {rc}")
+                launch()
+                t = Timer(torch)
+                for _ in range(reps):
+                    with t:
+                        launch()
+                torch.cuda.synchronize()
+                ms = min(s_.elapsed_time(e_) for s_, e_ in t.pairs)
+                sweep.append({"unit_kib": unit >> 10, "wg_per_cu": wpc, "ms": round(ms, 4),
+                              "GBps": round(moved / (ms * 1e-3) / 1e9, 1)})
+        best = max(sweep, key=lambda r: r["GBps"])
+        out[name] = {"best_GBps": best["GBps"], "frac": round(best["GBps"] / HBM_PEAK_GBS, 4),
+                     "unit_kib": best["unit_kib"], "wg_per_cu": best["wg_per_cu"],
+                     "sweep": sweep}
+    r, w = out["read"]["best_GBps"], out["write"]["best_GBps"]
+    out["read_write_harmonic_GBps"] = round(2 / (1 / r + 1 / w), 1)
+    del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_model() -> str:
     """The host CPU as /proc/cpuinfo names it: model name verbatim, with its
     family / model / stepping numbers and the logical CPUs listed there."""
@@ -1013,6 +1062,10 @@ def main() -> int:
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a plain 4 GiB device copy (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="also time plain read-only, write-only and copy streams of 16 GiB "
+                         "(libdaser_bwprobe.so) over unit sizes and workgroups per CU: what "
+                         "the memory system sustains per direction of traffic")
     ap.add_argument("--tune", default="",
                     help="launch-shape overrides for a measurement, as knob=value pairs "
                          "separated by commas (daser_amd._lib.TUNE names); the bytes moved "
@@ -1150,6 +1203,10 @@ def main() -> int:
         out.update({"value": round(r.get("tokens_per_s", 0.0)), "unit": "tokens/s",
                     "ms_per_step": round(r.get("kernel_ms", 0.0), 3), "dtype": "bf16",
                     "config": {"workload": workloads.CONFIG_NAMES[configs[0]]}})
+    if args.ceilings:
+        log("[bench] ceilings: plain read, write and copy streams")
+        out["ceilings"] = bench_ceilings(torch, dev)
+        log(f"[bench] ceilings: {json.dumps(out['ceilings'])}")
     if args.patterns:
         log("[bench] patterns: config 2's bytes in other access patterns")
         out["patterns"] = bench_patterns(torch, ops, dev)

@@ -21,6 +21,8 @@ ABI_TEST_SRC = os.path.join(ROOT, "tests", "c", "abi_roundtrip.cpp")
 ABI_TEST_OUT = os.path.join(ROOT, "tests", "c", "abi_roundtrip")
 RING_SAN_SRC = os.path.join(ROOT, "tests", "c", "ring_sanitize.cpp")
 RING_SAN_OUT = os.path.join(ROOT, "tests", "c", "ring_sanitize")
+PROBE_SRC = os.path.join(HERE, "csrc", "bw_probe.hip")
+PROBE_OUT = os.path.join(HERE, "libdaser_bwprobe.so")
 
 ARCH = "gfx950"
 
@@ -65,6 +67,14 @@ def build(verbose: bool = False) -> str:
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
     os.replace(ABI_TEST_OUT + ".tmp", ABI_TEST_OUT)
+    # the HBM ceiling probes of bench.py --ceilings (not part of the KV path)
+    cmd = [hipcc(), *HIPCC_FLAGS, PROBE_SRC, "-o", PROBE_OUT + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(PROBE_OUT + ".tmp", PROBE_OUT)
     build_ring_sanitize(verbose)
     return OUT
 
