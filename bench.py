@@ -1066,6 +1066,9 @@ def main() -> int:
                     help="also time plain read-only, write-only and copy streams of 16 GiB "
                          "(libdaser_bwprobe.so) over unit sizes and workgroups per CU: what "
                          "the memory system sustains per direction of traffic")
+    ap.add_argument("--no-ceilings", action="store_true",
+                    help="skip the short read/write/copy stream measurement that the default "
+                         "run adds beside the roofline (hbm_ceilings)")
     ap.add_argument("--tune", default="",
                     help="launch-shape overrides for a measurement, as knob=value pairs "
                          "separated by commas (daser_amd._lib.TUNE names); the bytes moved "
@@ -1203,10 +1206,21 @@ def main() -> int:
         out.update({"value": round(r.get("tokens_per_s", 0.0)), "unit": "tokens/s",
                     "ms_per_step": round(r.get("kernel_ms", 0.0), 3), "dtype": "bf16",
                     "config": {"workload": workloads.CONFIG_NAMES[configs[0]]}})
-    if args.ceilings:
+    if args.ceilings or (2 in res and not args.no_ceilings):
         log("[bench] ceilings: plain read, write and copy streams")
-        out["ceilings"] = bench_ceilings(torch, dev)
-        log(f"[bench] ceilings: {json.dumps(out['ceilings'])}")
+        ceil = bench_ceilings(torch, dev)
+        if args.ceilings:
+            out["ceilings"] = ceil
+            log(f"[bench] ceilings: {json.dumps(ceil)}")
+        bound = ceil["read_write_harmonic_GBps"]
+        out["hbm_ceilings"] = {
+            "read_GBps": ceil["read"]["best_GBps"], "write_GBps": ceil["write"]["best_GBps"],
+            "copy_bound_GBps": bound, "plain_copy_GBps": ceil["copy"]["best_GBps"],
+            "note": "measured on this GPU in this run (libdaser_bwprobe.so streams); a copy "
+                    "moves as many bytes each way, so it is bounded near the harmonic mean "
+                    "of the read and write rates"}
+        if "roofline" in out:
+            out["roofline"]["frac_of_copy_bound"] = round(out["roofline"]["achieved"] / bound, 4)
     if args.patterns:
         log("[bench] patterns: config 2's bytes in other access patterns")
         out["patterns"] = bench_patterns(torch, ops, dev)
