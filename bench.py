@@ -24,9 +24,15 @@ file-inclusive save/load of the connector's data plane, --serving the host
 cost of the connector's worker hooks on serving-shaped steps; neither is
 `value`.
 
+roofline prices the slower kernel of the step against the published 8 TB/s;
+hbm_ceilings measures plain read-only, write-only and copy streams on the
+same GPU in the same run, and roofline.frac_of_copy_bound prices the kernel
+against the harmonic mean of the read and write rates, the most a copy can
+sustain there.
+
 Usage: python bench.py [--steps K] [--warmup W] [--configs 2,3,4,5,6] [--no-cpu]
                        [--no-ref-loop] [--io] [--serving] [--patterns] [--shapes]
-                       [--calibrate]
+                       [--calibrate] [--ceilings | --no-ceilings] [--tune k=v,...]
 """
 
 from __future__ import annotations
