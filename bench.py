@@ -306,6 +306,30 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = t.mean_ms()
+    fan = {}
+    if shared and ops.fanout_supported(table.layout, shape.head_dim):
+        # what ops.scatter_rerotate runs for host tables with shared records:
+        # each distinct record read once and written to all of its pages
+        # (dsr_scatter_fanout), tables grouped and uploaded once
+        prep = ops.PreparedFanout(table, s_ids, s_offs, src,
+                                  rope=(s_ridx, tabs, None, "neox", k_scale, None))
+        tf = Timer(torch)
+        for _ in range(warmup):
+            prep()
+        for _ in range(steps):
+            with tf:
+                prep()
+        plain = ops.PreparedFanout(table, s_ids, s_offs, src)
+        tp = Timer(torch)
+        for _ in range(warmup):
+            plain()
+        for _ in range(steps):
+            with tp:
+                plain()
+        torch.cuda.synchronize()
+        fan = {"fanout_ms": tf.mean_ms(), "fanout_plain_ms": tp.mean_ms(),
+               "fanout_sources": prep.n_src,
+               "fanout_read_bytes": prep.n_src * shape.slot_bytes}
     # the same page list as a plain scatter: the copy ceiling of this layout
     tc = Timer(torch)
     for _ in range(steps):
@@ -367,7 +391,7 @@ def bench_rerotate(torch, ops, position, wl, dtype, dev, steps, warmup):
         src = recs
     del full, caches, table, src
     torch.cuda.empty_cache()
-    return {**extra,
+    return {**extra, **fan,
         "payload_bytes": P,
         "pages": wl.n_pages,
         "tokens": wl.tokens,
@@ -1186,6 +1210,27 @@ def main() -> int:
                 "algorithmic_bytes": 2 * r["payload_bytes"]}
             out[f"rerotate_cfg{c}"]["frac_hbm"] = frac_hbm(
                 out[f"rerotate_cfg{c}"]["traffic"], r["kernel_ms"])
+            if "fanout_ms" in r:
+                # the load the library runs for these host tables: each shared
+                # record read once (reads: the distinct records; writes: P)
+                per_page = {k: out[f"rerotate_cfg{c}"].pop(k) for k in
+                            ("tokens_per_s", "GBps", "frac", "kernel_ms", "kernel", "traffic",
+                             "algorithmic_bytes", "frac_hbm")}
+                alg = r["fanout_read_bytes"] + r["payload_bytes"]
+                fms = r["fanout_ms"]
+                out[f"rerotate_cfg{c}"].update({
+                    "tokens_per_s": round(r["tokens"] / (fms * 1e-3)),
+                    "GBps": round(alg / (fms * 1e-3) / 1e9, 1),
+                    "frac": round(alg / (fms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "kernel_ms": round(fms, 4), "kernel": "kv_fanout_kernel",
+                    "algorithmic_bytes": alg,
+                    "traffic": pmc_traffic("kv_fanout_kernel", c, r["pages"]),
+                    "distinct_records": r["fanout_sources"],
+                    "same_pages_plain_fanout_GBps": round(
+                        alg / (r["fanout_plain_ms"] * 1e-3) / 1e9, 1),
+                    "per_page_path": per_page})
+                out[f"rerotate_cfg{c}"]["frac_hbm"] = frac_hbm(
+                    out[f"rerotate_cfg{c}"]["traffic"], fms)
     if 4 in res:
         r = res[4]
         out["fp8_cfg4"] = {"workload": workloads.CONFIG_NAMES[4],

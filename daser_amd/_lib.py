@@ -20,7 +20,7 @@ LIB_PATH = os.environ.get("DASER_KV_LIB") or os.path.join(
     os.path.dirname(os.path.abspath(__file__)), "libdaser_kv.so"
 )
 
-DSR_ABI_VERSION = 10
+DSR_ABI_VERSION = 11
 DSR_OK = 0
 DSR_ERR_ARG = -1
 DSR_ERR_ALIGN = -2
@@ -50,7 +50,8 @@ DSR_REROTATE_SHARED_RECORDS = DSR_SHARED_RECORDS
 TUNE = {"units_per_group": 0, "max_wg_per_launch": 1, "rot_kernel": 2, "rot_wg_per_cu": 3,
         "rot_grouped_wg_per_cu": 4, "slots_tpw": 5, "slots_kernel": 6, "slots_unroll": 7,
         "copy_wg_per_cu": 8, "scatter_kernel": 9, "gather_split": 10,
-        "page_parts": 11, "slots_order": 12, "slots_wg_per_cu": 13}
+        "page_parts": 11, "slots_order": 12, "slots_wg_per_cu": 13,
+        "fanout_wg_per_cu": 14, "fanout_parts": 15}
 ROT_KERNEL_CODES = {"auto": 0, "pairs": 1, "contig": 2, "grouped": 3}
 
 _P = ctypes.c_void_p
@@ -82,6 +83,9 @@ SIGNATURES = {
         _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, ctypes.c_uint, _P],
         _I,
     ),
+    "dsr_scatter_fanout": (
+        [_P, _I, _I64, _I64, _I64, _I64, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I,
+         _P, _I, _P, _I, _I, _I, _I, _I, _P, _P], _I),
     "dsr_scatter_rerotate_static": (
         _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, ctypes.c_uint, _P],
         _I,

@@ -57,6 +57,7 @@
 #include "kv_page_kernels.h"
 #include "kv_rotate.h"
 #include "kv_slots.h"
+#include "kv_fanout.h"
 
 namespace {
 
@@ -1204,6 +1205,166 @@ int dsr_scatter_rerotate_static(const uint64_t* layer_base, int n_layers,
       layer_group ? reinterpret_cast<const int32_t*>(base + o_grp) : nullptr, n_groups,
       head_dim, rot_dim, rope_style, dtype,
       k_scale ? reinterpret_cast<const float*>(base + o_scl) : nullptr, 0, 0, flags, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Loads of shared records (dsr_scatter_fanout): one workgroup per (source
+// record, layer), written to all of that record's destination pages.
+
+namespace {
+
+// Workgroups per CU of the fan-out kernel (DSR_TUNE_FANOUT_WG_PER_CU
+// overrides): pages of 16 KiB and up at 2 (config 5's 32 KiB pages measured
+// 33.58-33.64 ms from 2 to 8 per CU, 34.23 at 1), smaller ones at 8 (config
+// 6's 4 KiB pages: 4.53 ms at 8, 4.55 at 4, 4.74 at 2, 6.54 at 1).
+int fanout_wg_per_cu(int U) { return U >= 4 ? 2 : 8; }
+
+template <int DT, int STYLE>
+int launch_fanout_u(FanArgs fa, int U, int64_t n_src, hipStream_t s) {
+  int wpc = fanout_wg_per_cu(U);
+  if (const int64_t t = tune(DSR_TUNE_FANOUT_WG_PER_CU)) wpc = (int)t;
+  const size_t dyn = occupancy_lds(
+      wpc, (int64_t)sizeof(float2) * kFanLdsFloat2 + 2 * sizeof(int32_t) * kFanMaxBatch);
+  // source ranges of at most max_wg_per_launch() workgroups each
+  // (one source's layers and parts always fit HIP's limit; a tuning limit
+  // below them still launches one source at a time)
+  int64_t per = (max_wg_per_launch() - kXcds) / (fa.ra.u.n_layers * fa.parts);
+  if (per <= 0) per = 1;
+  for (int64_t s0 = 0; s0 < n_src; s0 += per) {
+    FanArgs f = fa;
+    const int64_t n = n_src - s0 < per ? n_src - s0 : per;
+    f.src_offsets += s0;
+    f.dst_start += s0;
+    f.n_src = (int32_t)n;
+    f.ra.u.n_units = n * fa.ra.u.n_layers;
+    const unsigned grid = (unsigned)(f.ra.u.n_units * fa.parts);
+    switch (U) {
+      case 1: kv_fanout_kernel<DT, STYLE, 1><<<grid, kThreads, dyn, s>>>(f); break;
+      case 2: kv_fanout_kernel<DT, STYLE, 2><<<grid, kThreads, dyn, s>>>(f); break;
+      case 4: kv_fanout_kernel<DT, STYLE, 4><<<grid, kThreads, dyn, s>>>(f); break;
+      default: kv_fanout_kernel<DT, STYLE, 8><<<grid, kThreads, dyn, s>>>(f); break;
+    }
+    const int rc = (int)hipGetLastError();
+    if (rc != 0) return rc;
+  }
+  return DSR_OK;
+}
+
+template <int DT>
+int launch_fanout(const FanArgs& fa, int U, int64_t n_src, int style, hipStream_t s) {
+  return style == DSR_ROPE_GPTJ ? launch_fanout_u<DT, DSR_ROPE_GPTJ>(fa, U, n_src, s)
+                                : launch_fanout_u<DT, DSR_ROPE_NEOX>(fa, U, n_src, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsr_scatter_fanout(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                       int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                       const int64_t* src_offsets, int n_src, const int32_t* dst_start,
+                       const int32_t* dst_page_ids, const int32_t* dst_rope_idx, int n_dst,
+                       const void* staging, int64_t staging_bytes, int64_t layer_bytes,
+                       int layer0, const float* cos_sin, int n_tables,
+                       const int32_t* layer_group, int n_groups, int head_dim, int rot_dim,
+                       int rope_style, int dtype, const float* k_scale, dsr_stream_t stream) {
+  if (n_src < 0 || n_dst < 0) return DSR_ERR_ARG;
+  // the page-table checks of the copies, with the destination ids and the
+  // source offsets in the tables' places
+  int rc = check_common(layer_base, n_layers, kv_stride, page_stride, page_bytes, num_blocks,
+                        dst_page_ids, src_offsets, n_dst, staging, staging_bytes, layer_bytes,
+                        layer0);
+  if (rc != DSR_OK) return rc;
+  if (n_src == 0 || n_dst == 0 || n_layers == 0) return DSR_OK;
+  if (!dst_start) return DSR_ERR_ARG;
+  // the page (or its part) in registers: at most 8 vectors per lane
+  const int64_t nvec = page_bytes >> 4;
+  if (nvec > 8 * kThreads) return DSR_ERR_SHAPE;
+  int parts = 1;
+  if (const int64_t t = tune(DSR_TUNE_FANOUT_PARTS)) parts = (int)t;
+  const int64_t row_vecs_all = dst_rope_idx && head_dim > 0
+                                   ? (int64_t)head_dim * (dtype >= DSR_DTYPE_FP8_E4M3 ? 1 : 2) / 16
+                                   : 1;
+  // parts of whole rows of at least one vector per lane
+  while (parts > 1 && (nvec % parts || (nvec / parts) % (row_vecs_all > 0 ? row_vecs_all : 1) ||
+                       nvec / parts < kThreads))
+    parts /= 2;
+  if (parts < 1) parts = 1;
+  const int64_t pv = nvec / parts;
+  const int U = pv <= kThreads ? 1 : pv <= 2 * kThreads ? 2 : pv <= 4 * kThreads ? 4 : 8;
+  if ((int64_t)n_src * n_layers * parts > 0x7fffffffLL) return DSR_ERR_ARG;
+  RotArgs ra{};
+  ra.u = make_unit(layer_base, n_layers, kv_stride, page_stride, page_bytes, num_blocks,
+                   nullptr, nullptr, 0, staging, staging_bytes, layer_bytes, layer0);
+  ra.n_groups = 1;
+  ra.rot_half = 1;
+  int dt = DSR_DTYPE_BF16, style = DSR_ROPE_NEOX;
+  if (dst_rope_idx) {
+    if (rope_style != DSR_ROPE_NEOX && rope_style != DSR_ROPE_GPTJ) return DSR_ERR_ARG;
+    int esize, ve;
+    switch (dtype) {
+      case DSR_DTYPE_BF16:
+      case DSR_DTYPE_FP16:
+        esize = 2;
+        ve = 8;
+        break;
+      case DSR_DTYPE_FP8_E4M3:
+      case DSR_DTYPE_FP8_E5M2:
+        esize = 1;
+        ve = 16;
+        break;
+      default:
+        return DSR_ERR_ARG;
+    }
+    if (n_tables < 0 || (layer_group && n_groups < 1)) return DSR_ERR_ARG;
+    if (n_tables > 0 && !cos_sin) return DSR_ERR_ARG;
+    if (esize == 1 && !k_scale) return DSR_ERR_ARG;
+    if (head_dim <= 0 || rot_dim <= 0 || rot_dim > head_dim || (rot_dim & 1) ||
+        rot_dim / 2 > kMaxRotHalf)
+      return DSR_ERR_SHAPE;
+    const int64_t row_bytes = (int64_t)head_dim * esize;
+    if (row_bytes % 16 || page_bytes % row_bytes) return DSR_ERR_SHAPE;
+    // the contig kernel's vector geometry: whole-vector rotary widths, neox
+    // partners a power of two <= 32 vectors apart inside a row
+    const bool vec_ok = ((int64_t)(head_dim - rot_dim) * esize) % 16 == 0 &&
+                        (rope_style == DSR_ROPE_NEOX ? (rot_dim / 2) % ve == 0 : rot_dim % ve == 0);
+    const int row_vecs = (int)(row_bytes / 16);
+    const int h = rope_style == DSR_ROPE_NEOX && vec_ok ? rot_dim / 2 * esize / 16 : 0;
+    const bool contig = vec_ok && (rope_style == DSR_ROPE_GPTJ ||
+                                   (h > 0 && h <= 32 && (h & (h - 1)) == 0 &&
+                                    row_vecs % (2 * h) == 0));
+    if (!contig) return DSR_ERR_SHAPE;
+    ra.cos_sin = reinterpret_cast<const float2*>(cos_sin);
+    ra.n_tables = n_tables;
+    ra.layer_group = layer_group;
+    ra.n_groups = layer_group ? n_groups : 1;
+    ra.row_vecs = row_vecs;
+    ra.rot_half = rot_dim / 2;
+    ra.rot_vecs = rot_dim * esize / 16;
+    ra.half_vecs = h;
+    ra.k_scale = k_scale;
+    dt = dtype;
+    style = rope_style;
+  }
+  FanArgs fa{};
+  fa.ra = ra;
+  fa.src_offsets = src_offsets;
+  fa.dst_start = dst_start;
+  fa.dst_pages = dst_page_ids;
+  fa.dst_rope = dst_rope_idx;
+  fa.n_src = n_src;
+  fa.parts = parts;
+  const int b = kFanLdsFloat2 / ra.rot_half;
+  fa.batch = b < kFanMaxBatch ? b : kFanMaxBatch;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dt) {
+    case DSR_DTYPE_BF16: return launch_fanout<DSR_DTYPE_BF16>(fa, U, n_src, style, s);
+    case DSR_DTYPE_FP16: return launch_fanout<DSR_DTYPE_FP16>(fa, U, n_src, style, s);
+    case DSR_DTYPE_FP8_E4M3: return launch_fanout<DSR_DTYPE_FP8_E4M3>(fa, U, n_src, style, s);
+    default: return launch_fanout<DSR_DTYPE_FP8_E5M2>(fa, U, n_src, style, s);
+  }
 }
 
 }  // extern "C"

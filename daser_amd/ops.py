@@ -393,6 +393,9 @@ def scatter(
     if shared_records is None:
         shared_records = _shared_offsets(slot_offsets)
     page_ids, slot_offsets, _ = dest_order(page_ids, slot_offsets)
+    if shared_records and _scatter_fanout(table, page_ids, slot_offsets, staging, layer0,
+                                          layers):
+        return
     args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
     stream = _stream_handle(table.layout.device)
     if shared_records and table.layout.k_layout != "hnd":
@@ -408,6 +411,136 @@ def _shared_offsets(slot_offsets) -> bool:
     """At most half of the host record offsets are distinct."""
     offs_h = _host_array(slot_offsets, np.int64)
     return offs_h is not None and offs_h.size > 1 and 2 * np.unique(offs_h).size <= offs_h.size
+
+
+def fanout_tables(page_ids: np.ndarray, slot_offsets: np.ndarray,
+                  rope_idx: Optional[np.ndarray] = None):
+    """Host tables of a scatter (destination order, one entry per block)
+    grouped by source record: (src_offsets, dst_start, dst_pages, dst_rope),
+    where the destinations of source s are entries dst_start[s] to
+    dst_start[s + 1] - 1, in block order."""
+    ids = np.asarray(page_ids, np.int64)
+    offs = np.asarray(slot_offsets, np.int64)
+    order = np.argsort(offs, kind="stable")  # keeps block order inside a source
+    so = offs[order]
+    first = np.ones(so.size, bool)
+    first[1:] = so[1:] != so[:-1]
+    starts = np.nonzero(first)[0]
+    dst_start = np.append(starts, so.size).astype(np.int32)
+    dst_rope = None if rope_idx is None else np.asarray(rope_idx, np.int64)[order]
+    return so[starts], dst_start, ids[order], dst_rope
+
+
+def fanout_supported(lay: PagedKVLayout, rot_dim: Optional[int] = None,
+                     style: str = "neox") -> bool:
+    """Whether dsr_scatter_fanout takes these pages (``rot_dim`` None: a
+    plain copy): pages of at most 32 KiB in record order (not head-major);
+    with rotation, token-major K rows with whole-vector rotary widths and a
+    neox partner a power of two of at most 32 vectors away, or gptj."""
+    if lay.k_layout == "hnd" or lay.page_bytes > 32 << 10 or lay.page_bytes % 16:
+        return False
+    if rot_dim is None:
+        return True
+    if lay.k_layout != "nhd" or not lay.has_geometry or lay.dtype not in _DTYPE_CODES:
+        return False
+    e = lay.elem_bytes
+    ve = 16 // e
+    if (lay.head_dim - rot_dim) * e % 16 or lay.head_dim * e % 16:
+        return False
+    if style == "gptj":
+        return rot_dim % ve == 0
+    h = rot_dim // 2 * e // 16
+    row_vecs = lay.head_dim * e // 16
+    return (rot_dim // 2) % ve == 0 and 0 < h <= 32 and h & (h - 1) == 0 and \
+        row_vecs % (2 * h) == 0
+
+
+class PreparedFanout:
+    """A load of host tables whose pages share records (a cached chunk
+    placed in several requests), through dsr_scatter_fanout: each record is
+    read once and written to all of its pages. The tables are checked,
+    grouped by record (:func:`fanout_tables`) and uploaded once; each call
+    launches the load on the current stream. ``rope``: None for a plain
+    copy, else (rope_idx, cos_sin, rot_dim, style, k_scale, layer_group) as
+    for :func:`scatter_rerotate`. Pages must satisfy
+    :func:`fanout_supported`; a block listed twice keeps its last entry."""
+
+    def __init__(self, table: LayerTable, page_ids, slot_offsets, staging: torch.Tensor, *,
+                 rope=None, layer0: int = 0, layers: Optional[tuple[int, int]] = None) -> None:
+        lay = table.layout
+        ids = _host_array(page_ids, np.int64)
+        offs = _host_array(slot_offsets, np.int64)
+        if ids is None or offs is None:
+            raise ValueError("PreparedFanout takes host tables")
+        first, count = (0, lay.num_layers) if layers is None else layers
+        if first < 0 or count < 0 or first + count > lay.num_layers:
+            raise IndexError("layer range outside the registered caches")
+        if staging.device != lay.device or not staging.is_contiguous():
+            raise ValueError("staging must be a contiguous tensor on the KV caches' device")
+        tail = (None, 0, None, 0, 0, 0, 0, 0, None)
+        ridx = None
+        keep = []
+        if rope is not None:
+            rope_idx, cos_sin, rot_dim, style, k_scale, layer_group = rope
+            rot_dim, n_tables, n_groups, lg_d, ks_ptr = _rope_args(
+                lay, cos_sin, rope_idx, rot_dim, k_scale, layer0, layer_group)
+            ridx = _host_array(rope_idx, np.int64)
+            if ridx is None:
+                raise ValueError("PreparedFanout takes host tables")
+            if ridx.shape != ids.shape:
+                raise ValueError("rope_idx and page_ids differ in length")
+            if not fanout_supported(lay, rot_dim, style):
+                raise ValueError("these pages need the per-page re-rotation kernels")
+            tail = (cos_sin.data_ptr(), n_tables, None if lg_d is None else lg_d.data_ptr(),
+                    n_groups, lay.head_dim, rot_dim, ROPE_STYLES[style],
+                    _DTYPE_CODES[lay.dtype], ks_ptr)
+            keep += [cos_sin, lg_d, k_scale]
+        elif not fanout_supported(lay):
+            raise ValueError("these pages need the per-page scatter kernels")
+        ids, offs, ridx = dest_order(ids, offs, ridx)
+        _validate(lay, ids, offs, staging, layer0 + first, count, False)
+        src, start, dpages, drope = fanout_tables(ids, offs, ridx)
+        dev = lay.device
+        self._tables = [_upload(torch.from_numpy(src), dev),
+                        _upload(torch.from_numpy(start), dev),
+                        _upload(torch.from_numpy(dpages.astype(np.int32)), dev),
+                        None if drope is None else
+                        _upload(torch.from_numpy(drope.astype(np.int32)), dev)]
+        self._keep = keep + [table, staging]
+        self.n_src, self.n_dst = int(src.size), int(dpages.size)
+        src_d, start_d, pages_d, rope_d = self._tables
+        self._args = (table.ptr(first), count, lay.kv_stride, lay.page_stride, lay.page_bytes,
+                      lay.num_blocks, src_d.data_ptr(), self.n_src, start_d.data_ptr(),
+                      pages_d.data_ptr(), None if rope_d is None else rope_d.data_ptr(),
+                      self.n_dst, staging.data_ptr(), staging.numel() * staging.element_size(),
+                      lay.layer_bytes, layer0 + first, *tail)
+        self._device = dev
+
+    def __call__(self) -> None:
+        rc = _lib.lib().dsr_scatter_fanout(*self._args, _stream_handle(self._device))
+        _lib.check("dsr_scatter_fanout", rc)
+
+
+def _scatter_fanout(table: LayerTable, page_ids, slot_offsets, staging: torch.Tensor,
+                    layer0: int, layers, rope=None) -> bool:
+    """The load of host tables whose pages share records, each record read
+    once (:class:`PreparedFanout`, prepared and launched once). Returns
+    False, having launched nothing, for device tables and for pages that
+    need the per-page kernels (:func:`fanout_supported`)."""
+    lay = table.layout
+    if _host_array(page_ids, np.int64) is None or _host_array(slot_offsets, np.int64) is None:
+        return False
+    if rope is not None:
+        if _host_array(rope[0], np.int64) is None:
+            return False
+        rot_dim = lay.head_dim if rope[2] is None else rope[2]
+        if not fanout_supported(lay, rot_dim, rope[3]):
+            return False
+    elif not fanout_supported(lay):
+        return False
+    PreparedFanout(table, page_ids, slot_offsets, staging, rope=rope, layer0=layer0,
+                   layers=layers)()
+    return True
 
 
 def _rope_args(lay: PagedKVLayout, cos_sin: torch.Tensor, rope_idx, rot_dim, k_scale,
@@ -490,6 +623,10 @@ def scatter_rerotate(
     if shared_records is None:
         shared_records = _shared_offsets(slot_offsets)
     page_ids, slot_offsets, rope_idx = dest_order(page_ids, slot_offsets, rope_idx)
+    if shared_records and _scatter_fanout(
+            table, page_ids, slot_offsets, staging, layer0, layers,
+            (rope_idx, cos_sin, rot_dim, style, k_scale, layer_group)):
+        return
     args, _tables = _copy_args(table, page_ids, slot_offsets, staging, layer0, layers)
     ridx_d = _as_device_table(rope_idx, torch.int32, lay.device, "rope_idx")
     if ridx_d.numel() != _tables[0].numel():

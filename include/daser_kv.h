@@ -50,9 +50,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
  * 2 layer_group on the re-rotation, 3 dsr_scatter_rerotate_kx, 4 the
  * re-rotations' flags, 5 the head-major (_hnd) entry points, 6
  * dsr_set_tuning, 7 dsr_scatter_ex, 8 dsr_scatter_slots_rerotate, 9
- * DSR_RING_MMAP and dsr_ring_is_mapped, 10 dsr_scatter_rerotate_static.
- * Callers check dsr_abi_version() against it. */
-#define DSR_ABI_VERSION 10
+ * DSR_RING_MMAP and dsr_ring_is_mapped, 10 dsr_scatter_rerotate_static, 11
+ * dsr_scatter_fanout. Callers check dsr_abi_version() against it. */
+#define DSR_ABI_VERSION 11
 
 /*
  * Kernel choice and launch shape follow from the geometry. dsr_set_tuning()
@@ -89,6 +89,10 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
  *                                 layer-major, 2 layer-major in hardware
  *                                 dispatch order
  *   DSR_TUNE_SLOTS_WG_PER_CU      workgroups per CU of those kernels
+ *   DSR_TUNE_FANOUT_WG_PER_CU     workgroups per CU of dsr_scatter_fanout
+ *   DSR_TUNE_FANOUT_PARTS         workgroups per (record, layer) unit of
+ *                                 dsr_scatter_fanout (1, 2, 4: parts of
+ *                                 whole rows)
  */
 #define DSR_TUNE_UNITS_PER_GROUP 0
 #define DSR_TUNE_MAX_WG_PER_LAUNCH 1
@@ -104,7 +108,9 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 #define DSR_TUNE_PAGE_PARTS 11
 #define DSR_TUNE_SLOTS_ORDER 12
 #define DSR_TUNE_SLOTS_WG_PER_CU 13
-#define DSR_TUNE_COUNT_ 14
+#define DSR_TUNE_FANOUT_WG_PER_CU 14
+#define DSR_TUNE_FANOUT_PARTS 15
+#define DSR_TUNE_COUNT_ 16
 
 #define DSR_OK 0
 #define DSR_ERR_ARG (-1)   /* null pointer, negative count, bad enum     */
@@ -256,6 +262,44 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
                          const int32_t* layer_group, int n_groups, int head_dim,
                          int rot_dim, int rope_style, int dtype,
                          const float* k_scale, unsigned flags, dsr_stream_t stream);
+
+/*
+ * Load of shared records: the bytes of dsr_scatter_rerotate (or, with
+ * dst_rope_idx null, of dsr_scatter) for loads in which several pages read
+ * the same record, with each record read once. Source s (record offset
+ * src_offsets[s], layer l's part at + (layer0 + l) * layer_bytes) goes to
+ * the destination blocks dst_page_ids[d] for d in [dst_start[s],
+ * dst_start[s + 1]); destination d's K is rotated by table dst_rope_idx[d]
+ * (-1: copied), exactly as dsr_scatter_rerotate rotates a page with that
+ * table (same arithmetic, scales, layer groups and rounding). A block may
+ * appear once per call (duplicates race). Out-of-range blocks and records
+ * are skipped.
+ *
+ * The same loop of daser/connector/daser_connector.py:536-551 (each
+ * request's pages copied from its staged chunk), for requests that share
+ * cached chunks; the reference reads a shared chunk once per request.
+ *
+ * Geometry: pages of at most 32 KiB (8 vectors per lane), token-major K
+ * rows; with rotation, whole-vector rotary widths and neox partners a
+ * power of two <= 32 vectors apart dividing the row, or gptj. Other shapes
+ * return DSR_ERR_SHAPE (dsr_scatter_rerotate covers them).
+ *
+ *   src_offsets   [device] n_src int64 record offsets
+ *   dst_start     [device] n_src + 1 int32, non-decreasing, dst_start[0] = 0,
+ *                 dst_start[n_src] = n_dst
+ *   dst_page_ids  [device] n_dst int32 block ids
+ *   dst_rope_idx  [device] n_dst int32 table indices, or null (plain copy:
+ *                 cos_sin, n_tables, layer_group, head_dim, rot_dim,
+ *                 rope_style, dtype and k_scale are then ignored)
+ */
+int dsr_scatter_fanout(const uint64_t* layer_base, int n_layers, int64_t kv_stride,
+                       int64_t page_stride, int64_t page_bytes, int64_t num_blocks,
+                       const int64_t* src_offsets, int n_src, const int32_t* dst_start,
+                       const int32_t* dst_page_ids, const int32_t* dst_rope_idx, int n_dst,
+                       const void* staging, int64_t staging_bytes, int64_t layer_bytes,
+                       int layer0, const float* cos_sin, int n_tables,
+                       const int32_t* layer_group, int n_groups, int head_dim, int rot_dim,
+                       int rope_style, int dtype, const float* k_scale, dsr_stream_t stream);
 
 /*
  * Allocation-free form of dsr_scatter_rerotate. No counterpart in the

@@ -135,3 +135,17 @@ def test_static_rerotate_argument_errors():
     assert call(rot_dim=127) == _lib.DSR_ERR_SHAPE
     assert call(layer_group=128, n_groups=0) == _lib.DSR_ERR_ARG
     assert b"static table" in lib.dsr_error_string(_lib.DSR_ERR_TOO_LARGE)
+
+
+def test_fanout_refuses_shapes_it_does_not_take():
+    """Geometries the fan-out kernel does not take are refused before any
+    launch, so that callers fall back to the per-page entry points."""
+    lib = _lib.lib()
+    base = [16, 1, 1 << 20, 1 << 20, 64 << 10, 8, 32, 1, 48, 64, 80, 1, 96, 1 << 24, 128 << 10,
+            0, 112, 1, None, 0]
+    # 64 KiB pages: more than 8 vectors per lane
+    assert lib.dsr_scatter_fanout(*base, 128, 128, 0, 0, None, None) == _lib.DSR_ERR_SHAPE
+    # neox partner 6 vectors away (head_dim 96): not a power of two
+    base[4] = 24 << 10
+    base[14] = 48 << 10
+    assert lib.dsr_scatter_fanout(*base, 96, 96, 0, 0, None, None) == _lib.DSR_ERR_SHAPE

@@ -1,0 +1,174 @@
+"""dsr_scatter_fanout (each shared record read once, written to all of its
+destination pages) writes the bytes of the per-page entry points on the
+same loads: dsr_scatter_rerotate for the re-rotating form, dsr_scatter for
+the plain copy. Called through the C ABI over random geometries; the
+per-page entry points are themselves oracle-checked (test_kernels_gpu.py),
+and ops' shared-record loads, which take this path, are checked against the
+oracle there too."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from daser_amd import _lib, ops, position
+from daser_amd.workloads import KVShape
+from tests.helpers import TORCH_DT, rand_caches
+
+pytestmark = pytest.mark.gpu
+
+DCODE = {"bf16": 0, "fp16": 1, "e4m3": 2, "e5m2": 3}
+
+
+def _dev(x, dt=torch.int32):
+    return torch.as_tensor(np.ascontiguousarray(x)).to(dt).cuda()
+
+
+def _case(heads, head_dim, dt, style, rot_dim, groups, n_src, n, seed):
+    """Caches (two identical copies), records, per-page tables and the
+    fan-out tables of one random load."""
+    esize = 1 if dt in ("e4m3", "e5m2") else 2
+    shape = KVShape(4, heads, head_dim, 16, esize)
+    rng = np.random.default_rng(seed)
+    nb = n + 8
+    recs = torch.from_numpy(rng.integers(0, 256, n_src * shape.slot_bytes, dtype=np.uint8))
+    if esize == 1:  # no NaN codes: NaN bytes are canonicalised, which the test is not about
+        recs[(recs & 0x7F) == 0x7F] = 0x11
+        if dt == "e5m2":
+            recs[(recs & 0x7C) == 0x7C] = 0x21
+    else:  # finite 16-bit values
+        w = recs.view(torch.int16)
+        exp = (w >> (10 if dt == "fp16" else 7)) & (0x1F if dt == "fp16" else 0xFF)
+        w[exp == (0x1F if dt == "fp16" else 0xFF)] = 0x3C00 if dt == "fp16" else 0x3F80
+    recs = recs.cuda()
+    a = rand_caches(shape, nb, dt, "cuda", seed=seed + 1)
+    b = [c.clone() for c in a]
+    page_ids = rng.permutation(nb)[:n].astype(np.int32)
+    src_of = rng.integers(0, n_src, n)
+    offs = (src_of * shape.slot_bytes).astype(np.int64)
+    n_tables = 5
+    ridx = rng.integers(-1, n_tables, n).astype(np.int32)
+    tabs = position.delta_tables(list(rng.integers(1, 30000, n_tables)), rot_dim, 500000.0,
+                                 device="cuda")
+    if groups:
+        tabs = torch.stack([tabs, position.delta_tables(list(rng.integers(1, 30000, n_tables)),
+                                                        rot_dim, 10000.0, device="cuda")])
+        lg = np.array([0, 1, -1, 1], np.int32)
+    else:
+        lg = None
+    ks = torch.tensor([0.03, 0.011, 0.05, 0.02], device="cuda") if esize == 1 else None
+    return shape, nb, recs, a, b, page_ids, offs, ridx, tabs, lg, ks, n_tables
+
+
+def _geometry(shape, cache):
+    e = cache.element_size()
+    return cache.stride(0) * e, cache.stride(1) * e
+
+
+@pytest.mark.parametrize("heads,head_dim,dt,style,rot_dim,groups", [
+    (8, 128, "bf16", 0, 128, False),   # 32 KiB pages, U = 8
+    (4, 128, "bf16", 0, 128, True),    # 16 KiB, layer groups
+    (2, 128, "fp16", 1, 128, False),   # 8 KiB, gptj
+    (1, 128, "bf16", 0, 64, False),    # 4 KiB, partial rotary
+    (8, 128, "e4m3", 0, 128, False),   # 16 KiB e4m3 with scales
+    (1, 128, "e5m2", 0, 128, True),    # 2 KiB e5m2, layer groups
+    (2, 64, "bf16", 0, 64, False),     # 4 KiB, partner 4 vectors away
+    (16, 128, "e4m3", 1, 96, False),   # 32 KiB e4m3, gptj, partial rotary
+])
+@pytest.mark.parametrize("parts", [1, 2])
+def test_fanout_matches_per_page_rerotate(tuning, parts, heads, head_dim, dt, style, rot_dim,
+                                          groups):
+    print(f"case: fanout H{heads} D{head_dim} {dt} style{style} rot{rot_dim} groups{groups} "
+          f"parts{parts}", flush=True)
+    tuning("fanout_parts", parts)
+    shape, nb, recs, a, b, page_ids, offs, ridx, tabs, lg, ks, n_tables = _case(
+        heads, head_dim, dt, style, rot_dim, groups, n_src=7, n=60, seed=heads * 7 + head_dim)
+    kv_stride, page_stride = _geometry(shape, a[0])
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    n_groups = 2 if groups else 0
+    lg_d = None if lg is None else _dev(lg)
+    ks_p = None if ks is None else ks.data_ptr()
+    # per-page entry point on copy a
+    base_a = _dev([c.data_ptr() for c in a], torch.int64)
+    ids_d, offs_d, ridx_d = _dev(page_ids), _dev(offs, torch.int64), _dev(ridx)
+    rc = lib.dsr_scatter_rerotate(
+        base_a.data_ptr(), 4, kv_stride, page_stride, shape.page_bytes, nb, ids_d.data_ptr(),
+        offs_d.data_ptr(), len(page_ids), recs.data_ptr(), recs.numel(), shape.layer_bytes, 0,
+        tabs.data_ptr(), ridx_d.data_ptr(), n_tables, None if lg_d is None else lg_d.data_ptr(),
+        n_groups, head_dim, rot_dim, style, DCODE[dt], ks_p, 0, stream)
+    _lib.check("dsr_scatter_rerotate", rc)
+    # fan-out on copy b
+    src, start, dpages, drope = ops.fanout_tables(page_ids, offs, ridx)
+    assert start[-1] == len(page_ids) and np.all(np.diff(start) > 0)
+    base_b = _dev([c.data_ptr() for c in b], torch.int64)
+    src_d, start_d, dp_d, dr_d = (_dev(src, torch.int64), _dev(start), _dev(dpages),
+                                  _dev(drope))
+    rc = lib.dsr_scatter_fanout(
+        base_b.data_ptr(), 4, kv_stride, page_stride, shape.page_bytes, nb, src_d.data_ptr(),
+        len(src), start_d.data_ptr(), dp_d.data_ptr(), dr_d.data_ptr(), len(dpages),
+        recs.data_ptr(), recs.numel(), shape.layer_bytes, 0, tabs.data_ptr(), n_tables,
+        None if lg_d is None else lg_d.data_ptr(), n_groups, head_dim, rot_dim, style,
+        DCODE[dt], ks_p, stream)
+    _lib.check("dsr_scatter_fanout", rc)
+    torch.cuda.synchronize()
+    for l in range(4):
+        assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), f"layer {l}"
+    # the loads did happen: V of a loaded page is its record's V
+    rec = recs.view(-1, 4, 2, shape.page_bytes)
+    p = 3
+    got = b[1][1, int(page_ids[p])].contiguous().view(torch.uint8).reshape(-1)
+    assert torch.equal(got, rec[int(offs[p] // shape.slot_bytes), 1, 1])
+
+
+@pytest.mark.parametrize("max_wg,parts", [(0, 1), (16, 1), (0, 2), (16, 4)])
+def test_fanout_plain_copy_matches_scatter(tuning, max_wg, parts):
+    """dst_rope_idx null: the plain load, bit-exact to dsr_scatter, also when
+    the sources are split over several launches and units over several
+    workgroups."""
+    print(f"case: fanout copy max_wg={max_wg} parts={parts}", flush=True)
+    if max_wg:
+        tuning("max_wg_per_launch", max_wg)
+    tuning("fanout_parts", parts)
+    shape, nb, recs, a, b, page_ids, offs, *_ = _case(8, 128, "bf16", 0, 128, False,
+                                                      n_src=9, n=70, seed=5)
+    kv_stride, page_stride = _geometry(shape, a[0])
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    base_a = _dev([c.data_ptr() for c in a], torch.int64)
+    ids_d, offs_d = _dev(page_ids), _dev(offs, torch.int64)
+    _lib.check("dsr_scatter", lib.dsr_scatter(
+        base_a.data_ptr(), 4, kv_stride, page_stride, shape.page_bytes, nb, ids_d.data_ptr(),
+        offs_d.data_ptr(), len(page_ids), recs.data_ptr(), recs.numel(), shape.layer_bytes, 0,
+        stream))
+    src, start, dpages, _ = ops.fanout_tables(page_ids, offs)
+    base_b = _dev([c.data_ptr() for c in b], torch.int64)
+    src_d, start_d, dp_d = _dev(src, torch.int64), _dev(start), _dev(dpages)
+    _lib.check("dsr_scatter_fanout", lib.dsr_scatter_fanout(
+        base_b.data_ptr(), 4, kv_stride, page_stride, shape.page_bytes, nb, src_d.data_ptr(),
+        len(src), start_d.data_ptr(), dp_d.data_ptr(), None, len(dpages), recs.data_ptr(),
+        recs.numel(), shape.layer_bytes, 0, None, 0, None, 0, 0, 0, 0, 0, None, stream))
+    torch.cuda.synchronize()
+    for l in range(4):
+        assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), f"layer {l}"
+
+
+def test_fanout_through_ops_matches_per_page_path():
+    """ops.scatter_rerotate on host tables with shared records takes the
+    fan-out path; with the hint off it takes the per-page kernels: same
+    bits, including a block listed twice (the last entry kept) and layer
+    ranges."""
+    print("case: fanout through ops", flush=True)
+    shape, nb, recs, a, b, page_ids, offs, ridx, tabs, lg, ks, n_tables = _case(
+        8, 128, "bf16", 0, 128, False, n_src=4, n=40, seed=9)
+    page_ids = np.append(page_ids, page_ids[5]).astype(np.int32)  # block 5 loaded twice
+    offs = np.append(offs, offs[0])
+    ridx = np.append(ridx, 2).astype(np.int32)
+    for caches, hint in ((a, False), (b, True)):
+        ops.scatter_rerotate(ops.LayerTable(caches), page_ids, offs, recs, tabs, ridx,
+                             shared_records=hint, layers=(1, 3))
+    torch.cuda.synchronize()
+    for l in range(4):
+        assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), f"layer {l}"
+
