@@ -1239,7 +1239,7 @@ int launch_fanout_u(FanArgs fa, int U, int64_t n_src, hipStream_t s) {
     f.dst_start += s0;
     f.n_src = (int32_t)n;
     f.ra.u.n_units = n * fa.ra.u.n_layers;
-    const unsigned grid = (unsigned)(f.ra.u.n_units * fa.parts);
+    const unsigned grid = (unsigned)((f.ra.u.n_units * fa.parts + kXcds - 1) / kXcds * kXcds);
     switch (U) {
       case 1: kv_fanout_kernel<DT, STYLE, 1><<<grid, kThreads, dyn, s>>>(f); break;
       case 2: kv_fanout_kernel<DT, STYLE, 2><<<grid, kThreads, dyn, s>>>(f); break;
