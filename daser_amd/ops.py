@@ -779,8 +779,9 @@ def scatter_slots(table: LayerTable, slot_mapping, row_offsets, staging: torch.T
     destination-slot order (near-sequential writes), like :func:`scatter`,
     and blocks whose every slot is listed with consecutive record rows go
     as whole pages through the page scatter (:func:`whole_pages`); the other
-    tokens (the ragged edges of requests) go through the token kernel.
-    Device tables go to the token kernel as given."""
+    tokens (the ragged edges of requests) go through the token kernel;
+    whole pages that share records load through :class:`PreparedFanout`,
+    as in :func:`scatter`. Device tables go to the token kernel as given."""
     host = slot_order(slot_mapping, row_offsets)
     if host is not None:
         sm, ro, _ = host
@@ -790,7 +791,7 @@ def scatter_slots(table: LayerTable, slot_mapping, row_offsets, staging: torch.T
             pages, offs, _, rest = whole_pages(sm, ro, lay.block_size, row)
             if pages.size:
                 scatter(table, pages, offs, staging, layer0=layer0, layers=layers,
-                        shared_records=False)
+                        shared_records=None)
                 sm, ro = sm[rest], ro[rest]
                 if not np.any(sm >= 0):
                     return
@@ -810,7 +811,8 @@ def scatter_slots_rerotate(table: LayerTable, slot_mapping, row_offsets,
     ``cos_sin[rope_idx[t]]`` (-1 = copy), as :func:`scatter_rerotate` rotates
     a page row (same tables, scales and layer groups). Host tables are
     processed in destination-slot order, whole pages with one table index
-    through :func:`scatter_rerotate`."""
+    through :func:`scatter_rerotate` (the fan-out load where they share
+    records)."""
     lay = table.layout
     rot_dim, n_tables, n_groups, lg_d, ks_ptr = _rope_args(
         lay, cos_sin, rope_idx, rot_dim, k_scale, layer0, layer_group)
@@ -823,7 +825,7 @@ def scatter_slots_rerotate(table: LayerTable, slot_mapping, row_offsets,
             if pages.size:
                 scatter_rerotate(table, pages, offs, staging, cos_sin, pri, rot_dim=rot_dim,
                                  style=style, k_scale=k_scale, layer0=layer0, layers=layers,
-                                 layer_group=layer_group, shared_records=False)
+                                 layer_group=layer_group, shared_records=None)
                 sm, ro, ri = sm[rest], ro[rest], ri[rest]
                 if not np.any(sm >= 0):
                     return

@@ -172,3 +172,42 @@ def test_fanout_through_ops_matches_per_page_path():
     for l in range(4):
         assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), f"layer {l}"
 
+
+
+def test_token_form_with_shared_chunks_takes_the_fanout():
+    """A slot_mapping load in which three requests place the same two cached
+    chunks (shared records): its whole pages go through the fan-out, its
+    ragged tail through the token kernel; the result equals the per-page
+    re-rotation of the same pages (no sharing hint) plus the token kernel."""
+    print("case: token form, shared chunks", flush=True)
+    shape = KVShape(4, 8, 128, 16, 2)
+    bs, row = 16, 8 * 128 * 2
+    rng = np.random.default_rng(21)
+    n_chunk_pages, n_req = 4, 3
+    recs = torch.from_numpy(rng.standard_normal(2 * n_chunk_pages * shape.slot_bytes // 2)
+                            .astype(np.float32)).to(torch.bfloat16).view(torch.uint8).cuda()
+    nb = 64
+    a = rand_caches(shape, nb, "bf16", "cuda", seed=22)
+    b = [c.clone() for c in a]
+    blocks = rng.permutation(nb)[:n_req * 2 * n_chunk_pages].reshape(n_req, -1)
+    tok_per_req = 2 * n_chunk_pages * bs - 5  # the last page ragged
+    sm, ro, ri = [], [], []
+    for r in range(n_req):
+        t = np.arange(tok_per_req)
+        sm.append(blocks[r][t // bs] * bs + t % bs)
+        ro.append((t // bs) * shape.slot_bytes + (t % bs) * row)  # both chunks' records
+        ri.append(np.full(tok_per_req, r % 3))
+    sm, ro, ri = (np.concatenate(x).astype(np.int64) for x in (sm, ro, ri))
+    tabs = position.delta_tables([11, 4000, 29000], 128, 500000.0, device="cuda")
+    ops.scatter_slots_rerotate(ops.LayerTable(a), sm, ro, recs, tabs, ri)
+    # reference: the whole pages through the per-page kernel (no fan-out) and
+    # the ragged tail through the token kernel
+    sm_o, ro_o, ri_o = ops.slot_order(sm, ro, ri)
+    pages, poffs, pri, rest = ops.whole_pages(sm_o, ro_o, bs, row, ri_o)
+    assert pages.size == n_req * (2 * n_chunk_pages - 1) and rest.sum() > 0
+    assert 2 * np.unique(poffs).size <= poffs.size  # shared records: the fan-out path
+    ops.scatter_rerotate(ops.LayerTable(b), pages, poffs, recs, tabs, pri, shared_records=False)
+    ops.scatter_slots_rerotate(ops.LayerTable(b), sm_o[rest], ro_o[rest], recs, tabs, ri_o[rest])
+    torch.cuda.synchronize()
+    for l in range(4):
+        assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), f"layer {l}"
