@@ -211,3 +211,33 @@ def test_token_form_with_shared_chunks_takes_the_fanout():
     torch.cuda.synchronize()
     for l in range(4):
         assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), f"layer {l}"
+
+
+def test_prepared_fanout_graph_capture_and_replay():
+    """A prepared fan-out load (device tables) launches nothing but the
+    kernel, so it can be captured into a HIP graph; each of three replays,
+    with new records written eagerly in between, equals the eager call."""
+    print("case: fanout graph capture", flush=True)
+    shape, nb, recs, a, b, page_ids, offs, ridx, tabs, lg, ks, n_tables = _case(
+        4, 128, "bf16", 0, 128, False, n_src=5, n=30, seed=31)
+    prep = ops.PreparedFanout(ops.LayerTable(a), page_ids, offs, recs,
+                              rope=(ridx, tabs, None, "neox", None, None))
+    eager = ops.PreparedFanout(ops.LayerTable(b), page_ids, offs, recs,
+                               rope=(ridx, tabs, None, "neox", None, None))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        prep()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        prep()
+    for rep in range(3):
+        recs.view(torch.bfloat16).normal_(generator=torch.Generator(device="cuda")
+                                          .manual_seed(40 + rep))
+        g.replay()
+        eager()
+        torch.cuda.synchronize()
+        for l in range(4):
+            assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), (rep, l)
