@@ -241,3 +241,62 @@ def test_prepared_fanout_graph_capture_and_replay():
         torch.cuda.synchronize()
         for l in range(4):
             assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), (rep, l)
+
+
+def _fanout_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        dt = ["bf16", "fp16", "e4m3", "e5m2"][rng.integers(4)]
+        D = int(rng.choice([64, 96, 128, 256]))
+        H = int(rng.choice([1, 2, 4, 8]))
+        bs = int(rng.choice([1, 4, 8, 16, 32]))
+        style = "gptj" if rng.random() < 0.3 else "neox"
+        R = D if rng.random() < 0.7 else D // 2
+        lay = ops.PagedKVLayout(num_layers=3, num_blocks=1, block_size=bs, num_heads=H,
+                                head_dim=D, dtype=TORCH_DT[dt],
+                                elem_bytes=1 if dt in ("e4m3", "e5m2") else 2,
+                                kv_stride=0, page_stride=0, layer_bytes=0,
+                                page_bytes=bs * H * D * (1 if dt in ("e4m3", "e5m2") else 2),
+                                device=torch.device("cuda"))
+        if lay.page_bytes % 16 or not ops.fanout_supported(lay, R, style):
+            continue
+        out.append((dt, D, H, bs, style, R, int(rng.integers(1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("case", _fanout_cases(16, 77))
+def test_fanout_random_geometries_match_per_page(case):
+    """Random geometries the fan-out takes (dtype, head_dim, heads, block
+    size, style, partial rotary), through ops with host tables: the fan-out
+    (shared-records hint) and the per-page kernels (no hint) give the same
+    bits."""
+    dt, D, H, bs, style, R, seed = case
+    print(f"case: fanout random {case}", flush=True)
+    e = 1 if dt in ("e4m3", "e5m2") else 2
+    shape = KVShape(3, H, D, bs, e)
+    rng = np.random.default_rng(seed)
+    n_src, n = int(rng.integers(1, 6)), int(rng.integers(6, 40))
+    nb = n + 3
+    recs = torch.from_numpy(rng.standard_normal(n_src * shape.slot_bytes // 2)
+                            .astype(np.float32)).to(torch.bfloat16).view(torch.uint8)
+    if e == 1:  # finite 8-bit codes
+        recs[(recs & 0x7F) == 0x7F] = 0x12
+        recs[(recs & 0x7C) == 0x7C] = 0x22
+    elif dt == "fp16":
+        w = recs.view(torch.int16)
+        w[((w >> 10) & 0x1F) == 0x1F] = 0x3C00
+    recs = recs.cuda()
+    page_ids = rng.permutation(nb)[:n].astype(np.int32)
+    offs = rng.integers(0, n_src, n).astype(np.int64) * shape.slot_bytes
+    ridx = rng.integers(-1, 3, n).astype(np.int32)
+    tabs = position.delta_tables([17, 2048, 31111], R, 500000.0, device="cuda")
+    ks = torch.tensor([0.02, 0.04, 0.01], device="cuda") if e == 1 else None
+    a = rand_caches(shape, nb, dt, "cuda", seed=seed % 1000)
+    b = [c.clone() for c in a]
+    for caches, hint in ((a, True), (b, False)):
+        ops.scatter_rerotate(ops.LayerTable(caches), page_ids, offs, recs, tabs, ridx,
+                             rot_dim=R, style=style, k_scale=ks, shared_records=hint)
+    torch.cuda.synchronize()
+    for l in range(3):
+        assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), f"layer {l}"
