@@ -222,7 +222,8 @@ def test_round_trip_full_size(gpu, cfg, dtype):
 def test_rerotate_full_size_oracle_sample(gpu, cfg):
     """The benchmark's re-rotating scatter at full size (config 5: 80 layers,
     171.8 GB of destination caches, 64 shared source chunks read by many
-    pages with the shared-records launch), sampled against the oracle."""
+    pages: host tables with shared records take the fan-out load, each
+    record read once), sampled against the oracle."""
     print(f"case: full-size rerotate oracle sample cfg{cfg}", flush=True)
     wl = workloads.config(cfg)
     sh = wl.shape
