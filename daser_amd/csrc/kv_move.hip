@@ -1282,19 +1282,6 @@ int dsr_scatter_fanout(const uint64_t* layer_base, int n_layers, int64_t kv_stri
   // the page (or its part) in registers: at most 8 vectors per lane
   const int64_t nvec = page_bytes >> 4;
   if (nvec > 8 * kThreads) return DSR_ERR_SHAPE;
-  int parts = 1;
-  if (const int64_t t = tune(DSR_TUNE_FANOUT_PARTS)) parts = (int)t;
-  const int64_t row_vecs_all = dst_rope_idx && head_dim > 0
-                                   ? (int64_t)head_dim * (dtype >= DSR_DTYPE_FP8_E4M3 ? 1 : 2) / 16
-                                   : 1;
-  // parts of whole rows of at least one vector per lane
-  while (parts > 1 && (nvec % parts || (nvec / parts) % (row_vecs_all > 0 ? row_vecs_all : 1) ||
-                       nvec / parts < kThreads))
-    parts /= 2;
-  if (parts < 1) parts = 1;
-  const int64_t pv = nvec / parts;
-  const int U = pv <= kThreads ? 1 : pv <= 2 * kThreads ? 2 : pv <= 4 * kThreads ? 4 : 8;
-  if ((int64_t)n_src * n_layers * parts > 0x7fffffffLL) return DSR_ERR_ARG;
   RotArgs ra{};
   ra.u = make_unit(layer_base, n_layers, kv_stride, page_stride, page_bytes, num_blocks,
                    nullptr, nullptr, 0, staging, staging_bytes, layer_bytes, layer0);
@@ -1348,6 +1335,17 @@ int dsr_scatter_fanout(const uint64_t* layer_base, int n_layers, int64_t kv_stri
     dt = dtype;
     style = rope_style;
   }
+  // parts of whole rows (the rotation columns stay those of the page), at
+  // least one vector per lane each
+  int parts = 1;
+  if (const int64_t t = tune(DSR_TUNE_FANOUT_PARTS)) parts = (int)t;
+  const int64_t row_vecs = dst_rope_idx ? ra.row_vecs : 1;
+  while (parts > 1 && (nvec % parts || (nvec / parts) % row_vecs || nvec / parts < kThreads))
+    parts /= 2;
+  if (parts < 1) parts = 1;
+  if ((int64_t)n_src * n_layers * parts > 0x7fffffffLL) return DSR_ERR_ARG;
+  const int64_t pv = nvec / parts;
+  const int U = pv <= kThreads ? 1 : pv <= 2 * kThreads ? 2 : pv <= 4 * kThreads ? 4 : 8;
   FanArgs fa{};
   fa.ra = ra;
   fa.src_offsets = src_offsets;
