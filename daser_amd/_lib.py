@@ -44,6 +44,7 @@ DSR_ROPE_NEOX = 0
 DSR_ROPE_GPTJ = 1
 
 DSR_SHARED_RECORDS = 1
+DSR_K_NHD, DSR_K_KX, DSR_K_HND = 0, 1, 2
 DSR_REROTATE_SHARED_RECORDS = DSR_SHARED_RECORDS
 
 # dsr_set_tuning knobs (measurements and tests only)
@@ -85,7 +86,7 @@ SIGNATURES = {
     ),
     "dsr_scatter_fanout": (
         [_P, _I, _I64, _I64, _I64, _I64, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I,
-         _P, _I, _P, _I, _I, _I, _I, _I, _P, _P], _I),
+         _P, _I, _P, _I, _I, _I, _I, _I, _P, _I, _I, _I, _P], _I),
     "dsr_scatter_rerotate_static": (
         _COPY_ARGS[:-1] + [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, ctypes.c_uint, _P],
         _I,

@@ -39,7 +39,14 @@ constexpr int kFanMaxBatch = 16;
 // lane of K and of V. K rotation as in the contig kernel (neox partner from
 // lane ^ half_vecs, fetched once per source since every destination rotates
 // the same stored vectors).
-template <int DT, int STYLE, int U>
+// Cache layouts (LAYOUT): kFanNhd token-major pages; kFanKx split-x K pages
+// of vLLM's 3-D PagedAttention caches (K vector i of the record is physical
+// vector kx_phys(i) on both sides, neox partners lane ^ 32); kFanHnd
+// head-major pages (records token-major: cache vector hnd_vec(i) for K and V,
+// rotation columns in record order). kx and hnd units are whole pages.
+constexpr int kFanNhd = 0, kFanKx = 1, kFanHnd = 2;
+
+template <int DT, int STYLE, int U, int LAYOUT = kFanNhd>
 __global__ __launch_bounds__(kThreads) void kv_fanout_kernel(FanArgs fa) {
   __shared__ float2 tabs[kFanLdsFloat2];
   __shared__ int32_t s_blk[kFanMaxBatch];
@@ -66,7 +73,10 @@ __global__ __launch_bounds__(kThreads) void kv_fanout_kernel(FanArgs fa) {
   const int nvec = (int)(sb >> 4);
   VRound<U> v, kk;
   v.load(make_rsrc(rec + pb, sb), threadIdx.x, nvec);
-  kk.load(make_rsrc(rec, sb), threadIdx.x, nvec);
+  if (LAYOUT == kFanKx)
+    kk.load_kx(ra, make_rsrc(rec, sb), threadIdx.x, nvec);
+  else
+    kk.load(make_rsrc(rec, sb), threadIdx.x, nvec);
   // this layer's table block, or no rotation at all
   const int grp = ra.layer_group ? ra.layer_group[a.layer0 + (int)l] : 0;
   const bool rot_layer = fa.dst_rope != nullptr && grp >= 0 && grp < ra.n_groups;
@@ -81,7 +91,8 @@ __global__ __launch_bounds__(kThreads) void kv_fanout_kernel(FanArgs fa) {
     q[k] = kk.r[k];
     if (STYLE == DSR_ROPE_NEOX && rot_layer) {  // uniform: the whole wave shuffles
 #pragma unroll
-      for (int c = 0; c < 4; ++c) q[k][c] = (unsigned)__shfl_xor((int)kk.r[k][c], ra.half_vecs);
+      for (int c = 0; c < 4; ++c)
+        q[k][c] = (unsigned)__shfl_xor((int)kk.r[k][c], LAYOUT == kFanKx ? 32 : ra.half_vecs);
     }
   }
   const int rh = ra.rot_half;
@@ -108,20 +119,23 @@ __global__ __launch_bounds__(kThreads) void kv_fanout_kernel(FanArgs fa) {
       if (blk < 0 || blk >= a.num_blocks) continue;  // skipped, as by the page scatter
       uint8_t* const cache = lbase + blk * a.page_stride;
       const rsrc_t kd = make_rsrc(cache, sb), vd = make_rsrc(cache + a.kv_stride, sb);
-      v.store(vd, threadIdx.x, nvec);
+      if (LAYOUT == kFanHnd)
+        v.store_hnd(a, vd, threadIdx.x, nvec);
+      else
+        v.store(vd, threadIdx.x, nvec);
       const int ti = s_ti[t];
-      if (ti < 0) {
-        kk.store(kd, threadIdx.x, nvec);
-        continue;
-      }
       const float2* tab = tabs + t * rh;
 #pragma unroll
       for (int k = 0; k < U; ++k) {
         const int i = (int)threadIdx.x + k * kThreads;
-        if (i < nvec)
-          bstore(kd, i << 4,
-                 rotate_vec<DT, STYLE>(ra, kk.r[k], q[k], k_column<false>(ra, i), tab, scale,
-                                       inv_scale));
+        if (i >= nvec) continue;
+        const int p = LAYOUT == kFanKx ? kx_phys(ra, i) : i;  // record-side vector
+        const int o = LAYOUT == kFanHnd ? hnd_vec(a, i) : p;  // cache-side vector
+        bstore(kd, o << 4,
+               ti < 0 ? kk.r[k]
+                      : rotate_vec<DT, STYLE>(ra, kk.r[k], q[k],
+                                              k_column<LAYOUT == kFanKx>(ra, p), tab, scale,
+                                              inv_scale));
       }
     }
   }

@@ -1221,7 +1221,7 @@ namespace {
 // 6's 4 KiB pages: 4.53 ms at 8, 4.55 at 4, 4.74 at 2, 6.54 at 1).
 int fanout_wg_per_cu(int U) { return U >= 4 ? 2 : 8; }
 
-template <int DT, int STYLE>
+template <int DT, int STYLE, int LAYOUT>
 int launch_fanout_u(FanArgs fa, int U, int64_t n_src, hipStream_t s) {
   int wpc = fanout_wg_per_cu(U);
   if (const int64_t t = tune(DSR_TUNE_FANOUT_WG_PER_CU)) wpc = (int)t;
@@ -1241,10 +1241,10 @@ int launch_fanout_u(FanArgs fa, int U, int64_t n_src, hipStream_t s) {
     f.ra.u.n_units = n * fa.ra.u.n_layers;
     const unsigned grid = (unsigned)((f.ra.u.n_units * fa.parts + kXcds - 1) / kXcds * kXcds);
     switch (U) {
-      case 1: kv_fanout_kernel<DT, STYLE, 1><<<grid, kThreads, dyn, s>>>(f); break;
-      case 2: kv_fanout_kernel<DT, STYLE, 2><<<grid, kThreads, dyn, s>>>(f); break;
-      case 4: kv_fanout_kernel<DT, STYLE, 4><<<grid, kThreads, dyn, s>>>(f); break;
-      default: kv_fanout_kernel<DT, STYLE, 8><<<grid, kThreads, dyn, s>>>(f); break;
+      case 1: kv_fanout_kernel<DT, STYLE, 1, LAYOUT><<<grid, kThreads, dyn, s>>>(f); break;
+      case 2: kv_fanout_kernel<DT, STYLE, 2, LAYOUT><<<grid, kThreads, dyn, s>>>(f); break;
+      case 4: kv_fanout_kernel<DT, STYLE, 4, LAYOUT><<<grid, kThreads, dyn, s>>>(f); break;
+      default: kv_fanout_kernel<DT, STYLE, 8, LAYOUT><<<grid, kThreads, dyn, s>>>(f); break;
     }
     const int rc = (int)hipGetLastError();
     if (rc != 0) return rc;
@@ -1252,10 +1252,20 @@ int launch_fanout_u(FanArgs fa, int U, int64_t n_src, hipStream_t s) {
   return DSR_OK;
 }
 
+template <int DT, int LAYOUT>
+int launch_fanout_l(const FanArgs& fa, int U, int64_t n_src, int style, hipStream_t s) {
+  return style == DSR_ROPE_GPTJ ? launch_fanout_u<DT, DSR_ROPE_GPTJ, LAYOUT>(fa, U, n_src, s)
+                                : launch_fanout_u<DT, DSR_ROPE_NEOX, LAYOUT>(fa, U, n_src, s);
+}
+
 template <int DT>
-int launch_fanout(const FanArgs& fa, int U, int64_t n_src, int style, hipStream_t s) {
-  return style == DSR_ROPE_GPTJ ? launch_fanout_u<DT, DSR_ROPE_GPTJ>(fa, U, n_src, s)
-                                : launch_fanout_u<DT, DSR_ROPE_NEOX>(fa, U, n_src, s);
+int launch_fanout(const FanArgs& fa, int U, int64_t n_src, int style, int layout,
+                  hipStream_t s) {
+  switch (layout) {
+    case kFanKx: return launch_fanout_l<DT, kFanKx>(fa, U, n_src, style, s);
+    case kFanHnd: return launch_fanout_l<DT, kFanHnd>(fa, U, n_src, style, s);
+    default: return launch_fanout_l<DT, kFanNhd>(fa, U, n_src, style, s);
+  }
 }
 
 }  // namespace
@@ -1269,16 +1279,19 @@ int dsr_scatter_fanout(const uint64_t* layer_base, int n_layers, int64_t kv_stri
                        const void* staging, int64_t staging_bytes, int64_t layer_bytes,
                        int layer0, const float* cos_sin, int n_tables,
                        const int32_t* layer_group, int n_groups, int head_dim, int rot_dim,
-                       int rope_style, int dtype, const float* k_scale, dsr_stream_t stream) {
+                       int rope_style, int dtype, const float* k_scale, int k_layout,
+                       int block_size, int num_heads, dsr_stream_t stream) {
   if (n_src < 0 || n_dst < 0) return DSR_ERR_ARG;
+  if (k_layout != DSR_K_NHD && k_layout != DSR_K_KX && k_layout != DSR_K_HND) return DSR_ERR_ARG;
+  if (k_layout != DSR_K_NHD && block_size <= 0) return DSR_ERR_ARG;
   // the page-table checks of the copies, with the destination ids and the
   // source offsets in the tables' places
   int rc = check_common(layer_base, n_layers, kv_stride, page_stride, page_bytes, num_blocks,
                         dst_page_ids, src_offsets, n_dst, staging, staging_bytes, layer_bytes,
                         layer0);
   if (rc != DSR_OK) return rc;
-  if (n_src == 0 || n_dst == 0 || n_layers == 0) return DSR_OK;
-  if (!dst_start) return DSR_ERR_ARG;
+  // the geometry is checked before the empty-work return below, so that a
+  // call with n_dst = 0 tells whether the fan-out takes a geometry
   // the page (or its part) in registers: at most 8 vectors per lane
   const int64_t nvec = page_bytes >> 4;
   if (nvec > 8 * kThreads) return DSR_ERR_SHAPE;
@@ -1334,11 +1347,41 @@ int dsr_scatter_fanout(const uint64_t* layer_base, int n_layers, int64_t kv_stri
     ra.k_scale = k_scale;
     dt = dtype;
     style = rope_style;
+    if (k_layout == DSR_K_KX) {
+      // the contig kernel's split-x conditions: head blocks of a power-of-two
+      // number (>= 64) of vectors, power-of-two block size, neox partners a
+      // multiple of 32 vectors apart
+      const int64_t hv = row_bytes / 16 * block_size;
+      const int dist = rope_style == DSR_ROPE_NEOX ? rot_dim / 2 / ve * block_size : 0;
+      if ((hv & (hv - 1)) || hv < kWave || (block_size & (block_size - 1)) || dist % 32 ||
+          page_bytes % (row_bytes * block_size) || page_bytes % 1024)
+        return DSR_ERR_SHAPE;
+      ra.kx_row_shift = __builtin_ctzll((unsigned long long)hv);
+      ra.kx_bs_shift = __builtin_ctz((unsigned)block_size);
+      ra.kx_dist = dist;
+      ra.row_vecs = (int)hv;
+    } else if (k_layout == DSR_K_HND) {
+      const int64_t rows = page_bytes / row_bytes;
+      if (rows % block_size) return DSR_ERR_SHAPE;
+      ra.u.hnd_heads = (int)(rows / block_size);
+      ra.u.hnd_block = block_size;
+      ra.u.hnd_row_vecs = row_vecs;
+    }
+  } else if (k_layout == DSR_K_HND) {
+    // plain copy of head-major pages: rows of page_bytes / (block_size *
+    // num_heads) bytes, whole vectors
+    if (num_heads <= 0 || page_bytes % ((int64_t)block_size * num_heads * 16)) return DSR_ERR_SHAPE;
+    ra.u.hnd_heads = num_heads;
+    ra.u.hnd_block = block_size;
+    ra.u.hnd_row_vecs = (int)(page_bytes / ((int64_t)block_size * num_heads) / 16);
   }
+  // a plain copy of split-x pages moves raw bytes: the token-major kernel
+  const int layout = k_layout == DSR_K_HND ? kFanHnd
+                     : k_layout == DSR_K_KX && dst_rope_idx ? kFanKx : kFanNhd;
   // parts of whole rows (the rotation columns stay those of the page), at
   // least one vector per lane each
   int parts = 1;
-  if (const int64_t t = tune(DSR_TUNE_FANOUT_PARTS)) parts = (int)t;
+  if (const int64_t t = tune(DSR_TUNE_FANOUT_PARTS)) parts = layout == kFanNhd ? (int)t : 1;
   const int64_t row_vecs = dst_rope_idx ? ra.row_vecs : 1;
   while (parts > 1 && (nvec % parts || (nvec / parts) % row_vecs || nvec / parts < kThreads))
     parts /= 2;
@@ -1346,6 +1389,8 @@ int dsr_scatter_fanout(const uint64_t* layer_base, int n_layers, int64_t kv_stri
   if ((int64_t)n_src * n_layers * parts > 0x7fffffffLL) return DSR_ERR_ARG;
   const int64_t pv = nvec / parts;
   const int U = pv <= kThreads ? 1 : pv <= 2 * kThreads ? 2 : pv <= 4 * kThreads ? 4 : 8;
+  if (n_src == 0 || n_dst == 0 || n_layers == 0) return DSR_OK;
+  if (!dst_start) return DSR_ERR_ARG;
   FanArgs fa{};
   fa.ra = ra;
   fa.src_offsets = src_offsets;
@@ -1358,10 +1403,10 @@ int dsr_scatter_fanout(const uint64_t* layer_base, int n_layers, int64_t kv_stri
   fa.batch = b < kFanMaxBatch ? b : kFanMaxBatch;
   hipStream_t s = (hipStream_t)stream;
   switch (dt) {
-    case DSR_DTYPE_BF16: return launch_fanout<DSR_DTYPE_BF16>(fa, U, n_src, style, s);
-    case DSR_DTYPE_FP16: return launch_fanout<DSR_DTYPE_FP16>(fa, U, n_src, style, s);
-    case DSR_DTYPE_FP8_E4M3: return launch_fanout<DSR_DTYPE_FP8_E4M3>(fa, U, n_src, style, s);
-    default: return launch_fanout<DSR_DTYPE_FP8_E5M2>(fa, U, n_src, style, s);
+    case DSR_DTYPE_BF16: return launch_fanout<DSR_DTYPE_BF16>(fa, U, n_src, style, layout, s);
+    case DSR_DTYPE_FP16: return launch_fanout<DSR_DTYPE_FP16>(fa, U, n_src, style, layout, s);
+    case DSR_DTYPE_FP8_E4M3: return launch_fanout<DSR_DTYPE_FP8_E4M3>(fa, U, n_src, style, layout, s);
+    default: return launch_fanout<DSR_DTYPE_FP8_E5M2>(fa, U, n_src, style, layout, s);
   }
 }
 

@@ -431,28 +431,28 @@ def fanout_tables(page_ids: np.ndarray, slot_offsets: np.ndarray,
     return so[starts], dst_start, ids[order], dst_rope
 
 
+_K_LAYOUTS = {"nhd": _lib.DSR_K_NHD, "kx": _lib.DSR_K_KX, "hnd": _lib.DSR_K_HND}
+
+
 def fanout_supported(lay: PagedKVLayout, rot_dim: Optional[int] = None,
                      style: str = "neox") -> bool:
     """Whether dsr_scatter_fanout takes these pages (``rot_dim`` None: a
-    plain copy): pages of at most 32 KiB in record order (not head-major);
-    with rotation, token-major K rows with whole-vector rotary widths and a
-    neox partner a power of two of at most 32 vectors away, or gptj."""
-    if lay.k_layout == "hnd" or lay.page_bytes > 32 << 10 or lay.page_bytes % 16:
+    plain copy), asked of the library itself: a call with no work checks
+    the geometry and launches nothing. It takes pages of at most 32 KiB in
+    every cache layout; the re-rotation wants whole-vector rotary widths
+    and neox partners a power of two of at most 32 vectors apart (split-x
+    pages: the split-x kernels' conditions)."""
+    rot = rot_dim is not None
+    if rot and (not lay.has_geometry or lay.dtype not in _DTYPE_CODES):
         return False
-    if rot_dim is None:
-        return True
-    if lay.k_layout != "nhd" or not lay.has_geometry or lay.dtype not in _DTYPE_CODES:
+    if lay.k_layout != "nhd" and lay.block_size <= 0:
         return False
-    e = lay.elem_bytes
-    ve = 16 // e
-    if (lay.head_dim - rot_dim) * e % 16 or lay.head_dim * e % 16:
-        return False
-    if style == "gptj":
-        return rot_dim % ve == 0
-    h = rot_dim // 2 * e // 16
-    row_vecs = lay.head_dim * e // 16
-    return (rot_dim // 2) % ve == 0 and 0 < h <= 32 and h & (h - 1) == 0 and \
-        row_vecs % (2 * h) == 0
+    rc = _lib.lib().dsr_scatter_fanout(
+        16, lay.num_layers, lay.kv_stride, lay.page_stride, lay.page_bytes, lay.num_blocks,
+        None, 0, None, None, 16 if rot else None, 0, 16, 0, lay.layer_bytes, 0, None, 0, None, 0,
+        lay.head_dim, rot_dim or 0, ROPE_STYLES[style], _DTYPE_CODES.get(lay.dtype, 0), 16,
+        _K_LAYOUTS[lay.k_layout], lay.block_size, lay.num_heads, None)
+    return rc == _lib.DSR_OK
 
 
 class PreparedFanout:
@@ -513,7 +513,8 @@ class PreparedFanout:
                       lay.num_blocks, src_d.data_ptr(), self.n_src, start_d.data_ptr(),
                       pages_d.data_ptr(), None if rope_d is None else rope_d.data_ptr(),
                       self.n_dst, staging.data_ptr(), staging.numel() * staging.element_size(),
-                      lay.layer_bytes, layer0 + first, *tail)
+                      lay.layer_bytes, layer0 + first, *tail, _K_LAYOUTS[lay.k_layout],
+                      lay.block_size, lay.num_heads)
         self._device = dev
 
     def __call__(self) -> None:

@@ -134,6 +134,11 @@ typedef struct ihipStream_t* dsr_stream_t; /* == hipStream_t */
 /* dsr_scatter_ex / dsr_scatter_rerotate* flags: several pages of the call
  * read the same records (a cached chunk placed in several requests). A
  * launch-shape hint; results do not depend on it. */
+/* dsr_scatter_fanout cache page layouts. */
+#define DSR_K_NHD 0 /* token-major [block_size][H][D]                         */
+#define DSR_K_KX 1  /* split-x K [H][D / X][block_size][X] (3-D caches)       */
+#define DSR_K_HND 2 /* head-major [H][block_size][D], records token-major     */
+
 #define DSR_SHARED_RECORDS 1u
 #define DSR_REROTATE_SHARED_RECORDS DSR_SHARED_RECORDS
 
@@ -279,10 +284,17 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
  * request's pages copied from its staged chunk), for requests that share
  * cached chunks; the reference reads a shared chunk once per request.
  *
- * Geometry: pages of at most 32 KiB (8 vectors per lane), token-major K
- * rows; with rotation, whole-vector rotary widths and neox partners a
- * power of two <= 32 vectors apart dividing the row, or gptj. Other shapes
- * return DSR_ERR_SHAPE (dsr_scatter_rerotate covers them).
+ * Geometry: pages of at most 32 KiB (8 vectors per lane); with rotation,
+ * whole-vector rotary widths and neox partners a power of two <= 32 vectors
+ * apart dividing the row, or gptj. k_layout names the cache pages:
+ * DSR_K_NHD token-major (block_size and num_heads unused), DSR_K_KX the
+ * split-x K pages of dsr_scatter_rerotate_kx (with its geometry conditions;
+ * a plain copy moves them as raw bytes), DSR_K_HND head-major pages as for
+ * the _hnd entry points (num_heads needed for a plain copy). Other shapes
+ * return DSR_ERR_SHAPE (the per-page entry points cover them). The
+ * geometry is checked before the tables: a call with n_src = n_dst = 0 and
+ * null tables launches nothing and returns DSR_OK or DSR_ERR_SHAPE, whether
+ * the fan-out takes these pages.
  *
  *   src_offsets   [device] n_src int64 record offsets
  *   dst_start     [device] n_src + 1 int32, non-decreasing, dst_start[0] = 0,
@@ -299,7 +311,8 @@ int dsr_scatter_fanout(const uint64_t* layer_base, int n_layers, int64_t kv_stri
                        const void* staging, int64_t staging_bytes, int64_t layer_bytes,
                        int layer0, const float* cos_sin, int n_tables,
                        const int32_t* layer_group, int n_groups, int head_dim, int rot_dim,
-                       int rope_style, int dtype, const float* k_scale, dsr_stream_t stream);
+                       int rope_style, int dtype, const float* k_scale, int k_layout,
+                       int block_size, int num_heads, dsr_stream_t stream);
 
 /*
  * Allocation-free form of dsr_scatter_rerotate. No counterpart in the

@@ -144,8 +144,17 @@ def test_fanout_refuses_shapes_it_does_not_take():
     base = [16, 1, 1 << 20, 1 << 20, 64 << 10, 8, 32, 1, 48, 64, 80, 1, 96, 1 << 24, 128 << 10,
             0, 112, 1, None, 0]
     # 64 KiB pages: more than 8 vectors per lane
-    assert lib.dsr_scatter_fanout(*base, 128, 128, 0, 0, None, None) == _lib.DSR_ERR_SHAPE
+    assert lib.dsr_scatter_fanout(*base, 128, 128, 0, 0, None, 0, 0, 0, None) == _lib.DSR_ERR_SHAPE
     # neox partner 6 vectors away (head_dim 96): not a power of two
     base[4] = 24 << 10
     base[14] = 48 << 10
-    assert lib.dsr_scatter_fanout(*base, 96, 96, 0, 0, None, None) == _lib.DSR_ERR_SHAPE
+    assert lib.dsr_scatter_fanout(*base, 96, 96, 0, 0, None, 0, 0, 0, None) == _lib.DSR_ERR_SHAPE
+    # an unknown page layout, and split-x pages without a block size
+    base[4] = 32 << 10
+    base[14] = 64 << 10
+    assert lib.dsr_scatter_fanout(*base, 128, 128, 0, 0, None, 7, 16, 8, None) == _lib.DSR_ERR_ARG
+    assert lib.dsr_scatter_fanout(*base, 128, 128, 0, 0, None, 1, 0, 8, None) == _lib.DSR_ERR_ARG
+    # the capability query: no work, null tables, the geometry's verdict
+    assert lib.dsr_scatter_fanout(16, 1, 1 << 20, 1 << 20, 32 << 10, 8, None, 0, None, None, 16, 0,
+                                  16, 0, 64 << 10, 0, None, 0, None, 0, 128, 128, 0, 0, None,
+                                  0, 16, 8, None) == _lib.DSR_OK

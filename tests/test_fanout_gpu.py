@@ -110,7 +110,7 @@ def test_fanout_matches_per_page_rerotate(tuning, parts, heads, head_dim, dt, st
         len(src), start_d.data_ptr(), dp_d.data_ptr(), dr_d.data_ptr(), len(dpages),
         recs.data_ptr(), recs.numel(), shape.layer_bytes, 0, tabs.data_ptr(), n_tables,
         None if lg_d is None else lg_d.data_ptr(), n_groups, head_dim, rot_dim, style,
-        DCODE[dt], ks_p, stream)
+        DCODE[dt], ks_p, _lib.DSR_K_NHD, 0, 0, stream)
     _lib.check("dsr_scatter_fanout", rc)
     torch.cuda.synchronize()
     for l in range(4):
@@ -148,7 +148,8 @@ def test_fanout_plain_copy_matches_scatter(tuning, max_wg, parts):
     _lib.check("dsr_scatter_fanout", lib.dsr_scatter_fanout(
         base_b.data_ptr(), 4, kv_stride, page_stride, shape.page_bytes, nb, src_d.data_ptr(),
         len(src), start_d.data_ptr(), dp_d.data_ptr(), None, len(dpages), recs.data_ptr(),
-        recs.numel(), shape.layer_bytes, 0, None, 0, None, 0, 0, 0, 0, 0, None, stream))
+        recs.numel(), shape.layer_bytes, 0, None, 0, None, 0, 0, 0, 0, 0, None, _lib.DSR_K_NHD,
+        0, 0, stream))
     torch.cuda.synchronize()
     for l in range(4):
         assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), f"layer {l}"
@@ -300,3 +301,73 @@ def test_fanout_random_geometries_match_per_page(case):
     torch.cuda.synchronize()
     for l in range(3):
         assert torch.equal(a[l].view(torch.uint8), b[l].view(torch.uint8)), f"layer {l}"
+
+
+def _hnd_like(caches):
+    """(2, NB, bs, H, D) views of head-major memory holding the same values."""
+    out = []
+    for c in caches:
+        two, nb, bs, h, d = c.shape
+        m = torch.empty((two, nb, h, bs, d), dtype=c.dtype, device=c.device)
+        v = m.permute(0, 1, 3, 2, 4)
+        v.copy_(c)
+        out.append(v)
+    return out
+
+
+@pytest.mark.parametrize("layout", ["kx", "hnd"])
+@pytest.mark.parametrize("dt,heads,head_dim,style,rot", [
+    ("bf16", 8, 128, "neox", 128), ("e4m3", 8, 128, "neox", 128), ("bf16", 2, 64, "gptj", 64),
+    ("fp16", 4, 128, "neox", 64), ("bf16", 1, 128, "neox", 128)])
+def test_fanout_other_cache_layouts_match_per_page(layout, dt, heads, head_dim, style, rot):
+    """Split-x (3-D PagedAttention caches) and head-major pages: the fan-out
+    (shared-records hint) gives the bits of the per-page _kx / _hnd entry
+    points (no hint), re-rotating and plain."""
+    print(f"case: fanout {layout} {dt} H{heads} D{head_dim} {style} R{rot}", flush=True)
+    e = 1 if dt in ("e4m3", "e5m2") else 2
+    shape = KVShape(3, heads, head_dim, 16, e)
+    rng = np.random.default_rng(heads * 31 + head_dim)
+    n_src, n = 3, 24
+    nb = n + 4
+    recs = torch.from_numpy(rng.standard_normal(n_src * shape.slot_bytes // 2)
+                            .astype(np.float32)).to(torch.bfloat16).view(torch.uint8)
+    if e == 1:
+        recs[(recs & 0x7F) == 0x7F] = 0x13
+    elif dt == "fp16":
+        w = recs.view(torch.int16)
+        w[((w >> 10) & 0x1F) == 0x1F] = 0x3C00
+    recs = recs.cuda()
+    page_ids = rng.permutation(nb)[:n].astype(np.int32)
+    offs = rng.integers(0, n_src, n).astype(np.int64) * shape.slot_bytes
+    ridx = rng.integers(-1, 2, n).astype(np.int32)
+    tabs = position.delta_tables([300, 17000], rot, 500000.0, device="cuda")
+    ks = torch.tensor([0.02, 0.04, 0.01], device="cuda") if e == 1 else None
+    base = rand_caches(shape, nb, dt, "cuda", seed=8)
+
+    def table(caches):
+        if layout == "kx":
+            return ops.LayerTable([c.reshape(2, nb, -1) for c in caches], block_size=16,
+                                  head_dim=head_dim)
+        return ops.LayerTable(caches)
+
+    outs = []
+    for hint in (True, False):
+        for rotate in (True, False):
+            caches = [c.clone() for c in base]
+            if layout == "hnd":
+                caches = _hnd_like(caches)
+            t = table(caches)
+            if layout == "hnd" and heads > 1:
+                assert t.layout.k_layout == "hnd"
+            if rotate:
+                ops.scatter_rerotate(t, page_ids, offs, recs, tabs, ridx, rot_dim=rot,
+                                     style=style, k_scale=ks, shared_records=hint)
+            else:
+                ops.scatter(t, page_ids, offs, recs, shared_records=hint)
+            outs.append([c.contiguous().view(torch.uint8) for c in caches])
+    torch.cuda.synchronize()
+    lay = table(base).layout
+    assert ops.fanout_supported(lay, rot, style)
+    for l in range(3):
+        assert torch.equal(outs[0][l], outs[2][l]), f"rotated, layer {l}"
+        assert torch.equal(outs[1][l], outs[3][l]), f"plain, layer {l}"
