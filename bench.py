@@ -853,7 +853,8 @@ def bench_ceilings(torch, dev, nbytes: int = 16 << 30, reps: int = 5) -> dict:
     """Plain streams over `nbytes` buffers (daser_amd/csrc/bw_probe.hip):
     read-only, write-only and copy, one workgroup per unit of 16, 32 or 64
     KiB at 1, 2, 4 or 8 workgroups per CU; best HIP-event time of `reps`
-    launches each. Bytes counted: read or written once (copy: both). The
+    launches each. write_random writes the same units at randomly permuted
+    places (the placement of a load's destination pages). Bytes counted: read or written once (copy: both). The
     harmonic mean of the best read and write rates is what a copy that
     alternates the two directions at those rates would sustain."""
     import ctypes
@@ -868,13 +869,20 @@ def bench_ceilings(torch, dev, nbytes: int = 16 << 30, reps: int = 5) -> dict:
     sink = torch.zeros(256, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     out = {}
-    for op, name in ((0, "read"), (1, "write"), (2, "copy")):
+    perms = {}
+    for op, name in ((0, "read"), (1, "write"), (2, "copy"), (3, "write_random"),
+                     (4, "write_random_16_per_wg")):
         moved = nbytes * (2 if op == 2 else 1)
         sweep = []
         for unit in (16 << 10, 32 << 10, 64 << 10):
+            if op == 3:  # the same units written at randomly permuted places
+                g = torch.Generator().manual_seed(unit)
+                perms[unit] = torch.randperm(nbytes // unit, generator=g,
+                                             dtype=torch.int32).to(dev)
             for wpc in (1, 2, 4, 8):
                 def launch():
-                    rc = fn(op, a.data_ptr(), b.data_ptr(), nbytes, unit, wpc, sink.data_ptr(),
+                    s_ptr = perms[unit].data_ptr() if op >= 3 else a.data_ptr()
+                    rc = fn(op, s_ptr, b.data_ptr(), nbytes, unit, wpc, sink.data_ptr(),
                             stream)
                     if rc:
                         raise RuntimeError(f"dsr_bw_probe failed with {rc}")
@@ -891,6 +899,7 @@ def bench_ceilings(torch, dev, nbytes: int = 16 << 30, reps: int = 5) -> dict:
         out[name] = {"best_GBps": best["GBps"], "frac": round(best["GBps"] / HBM_PEAK_GBS, 4),
                      "unit_kib": best["unit_kib"], "wg_per_cu": best["wg_per_cu"],
                      "sweep": sweep}
+    del perms
     r, w = out["read"]["best_GBps"], out["write"]["best_GBps"]
     out["read_write_harmonic_GBps"] = round(2 / (1 / r + 1 / w), 1)
     del a, b
@@ -1267,6 +1276,8 @@ def main() -> int:
         out["hbm_ceilings"] = {
             "read_GBps": ceil["read"]["best_GBps"], "write_GBps": ceil["write"]["best_GBps"],
             "copy_bound_GBps": bound, "plain_copy_GBps": ceil["copy"]["best_GBps"],
+            "write_random_GBps": ceil["write_random"]["best_GBps"],
+            "write_random_16_per_wg_GBps": ceil["write_random_16_per_wg"]["best_GBps"],
             "note": "measured on this GPU in this run (libdaser_bwprobe.so streams); a copy "
                     "moves as many bytes each way, so it is bounded near the harmonic mean "
                     "of the read and write rates"}

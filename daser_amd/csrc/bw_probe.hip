@@ -55,6 +55,22 @@ __global__ __launch_bounds__(kThreads) void probe_write(uint8_t* dst, int64_t un
   }
 }
 
+// write-only to units at permuted places: workgroup g writes units
+// g * per_wg ... + per_wg - 1 of the list, unit i at place perm[i]
+template <int U>
+__global__ __launch_bounds__(kThreads) void probe_write_perm(uint8_t* dst, int64_t unit,
+                                                             const int32_t* perm, int per_wg) {
+  const u32x4 v = {threadIdx.x, blockIdx.x, 0x5a5a5a5au, 0};
+  for (int j = 0; j < per_wg; ++j) {
+    const rsrc_t r = rsrc(dst + (int64_t)perm[(int64_t)blockIdx.x * per_wg + j] * unit, unit);
+    for (int base = threadIdx.x; base < (int)(unit >> 4); base += kThreads * U) {
+#pragma unroll
+      for (int k = 0; k < U; ++k)
+        __builtin_amdgcn_raw_buffer_store_b128(v, r, (base + k * kThreads) << 4, 0, 17);
+    }
+  }
+}
+
 template <int U>
 __global__ __launch_bounds__(kThreads) void probe_copy(const uint8_t* src, uint8_t* dst,
                                                        int64_t unit) {
@@ -83,17 +99,21 @@ size_t lds_for(int wg_per_cu) {
 
 extern "C" {
 
-// op: 0 read, 1 write, 2 copy. bytes a multiple of unit; unit a multiple of
-// 4 KiB and at most 1 GiB; 16-byte aligned buffers. Returns 0, -1 for bad
-// arguments, or a hipError_t.
+// op: 0 read, 1 write, 2 copy, 3 write with unit i at place src[i] (src: a
+// permutation of the bytes / unit places, int32), one unit per workgroup;
+// 4 the same with 16 units per workgroup. bytes a multiple of unit;
+// unit a multiple of 4 KiB and at most 1 GiB; 16-byte aligned buffers.
+// Returns 0, -1 for bad arguments, or a hipError_t.
 int dsr_bw_probe(int op, const void* src, void* dst, int64_t bytes, int64_t unit,
                  int wg_per_cu, void* sink, hipStream_t stream) {
-  if (op < 0 || op > 2 || unit < 4096 || unit % 4096 || unit > (1LL << 30) || bytes <= 0 ||
+  if (op < 0 || op > 4 || unit < 4096 || unit % 4096 || unit > (1LL << 30) || bytes <= 0 ||
       bytes % unit || bytes / unit > 0x7fffffffLL)
     return -1;
   if ((op != 1 && !src) || (op != 0 && !dst) || (op == 0 && !sink)) return -1;
   if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) return -1;
-  const unsigned grid = (unsigned)(bytes / unit);
+  const int per_wg = op == 4 ? 16 : 1;
+  if ((bytes / unit) % per_wg) return -1;
+  const unsigned grid = (unsigned)(bytes / unit / per_wg);
   const size_t lds = lds_for(wg_per_cu);
   // vectors per lane per round: the whole unit in one round up to 32 KiB
   const int64_t v = unit >> 12;
@@ -104,6 +124,9 @@ int dsr_bw_probe(int op, const void* src, void* dst, int64_t bytes, int64_t unit
 #define DSR_PROBE_LAUNCH(UU)                                                   \
   if (op == 0) probe_read<UU><<<grid, kThreads, lds, stream>>>(s, unit, k);    \
   else if (op == 1) probe_write<UU><<<grid, kThreads, lds, stream>>>(d, unit); \
+  else if (op >= 3)                                                            \
+    probe_write_perm<UU><<<grid, kThreads, lds, stream>>>(                     \
+        d, unit, reinterpret_cast<const int32_t*>(s), per_wg);                 \
   else probe_copy<UU><<<grid, kThreads, lds, stream>>>(s, d, unit);
   switch (U) {
     case 8: DSR_PROBE_LAUNCH(8) break;

@@ -25,7 +25,9 @@ def _probe():
 
 def test_probe_refuses_bad_arguments():
     fn = _probe()
-    assert fn(3, 16, 16, 1 << 20, 16384, 1, 16, None) == -1      # unknown stream
+    assert fn(5, 16, 16, 1 << 20, 16384, 1, 16, None) == -1      # unknown stream
+    assert fn(4, 16, 16, 8 * 16384, 16384, 1, 16, None) == -1    # 8 units: not 16 per group
+    assert fn(3, None, 16, 1 << 20, 16384, 1, 16, None) == -1    # no permutation
     assert fn(2, 16, 16, 1 << 20, 1000, 1, 16, None) == -1       # unit not 4 KiB-aligned
     assert fn(2, 16, 16, 1 << 20 | 4096, 16384, 1, 16, None) == -1  # bytes not whole units
     assert fn(2, None, 16, 1 << 20, 16384, 1, 16, None) == -1    # copy without a source
@@ -52,6 +54,12 @@ def test_probe_streams_move_their_bytes(unit):
     torch.cuda.synchronize(dev)
     words = dst.view(torch.int32).view(-1, 4)
     assert bool((words[:, 2] == 0x5a5a5a5a).all())  # every 16-byte vector written
+    for op in (3, 4):  # every unit written once, at its permuted place
+        dst.zero_()
+        perm = torch.randperm(n // unit, generator=g, dtype=torch.int32).to(dev)
+        assert fn(op, perm.data_ptr(), dst.data_ptr(), n, unit, 2, None, stream) == 0
+        torch.cuda.synchronize(dev)
+        assert bool((dst.view(torch.int32).view(-1, 4)[:, 2] == 0x5a5a5a5a).all())
     assert fn(0, src.data_ptr(), None, n, unit, 2, sink.data_ptr(), stream) == 0
     torch.cuda.synchronize(dev)
     assert int(sink.abs().sum()) == 0  # the read stream stores nothing
