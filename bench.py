@@ -851,8 +851,8 @@ def bench_patterns(torch, ops, dev, reps: int = 5) -> dict:
 
 def bench_ceilings(torch, dev, nbytes: int = 16 << 30, reps: int = 5) -> dict:
     """Plain streams over `nbytes` buffers (daser_amd/csrc/bw_probe.hip):
-    read-only, write-only and copy, one workgroup per unit of 16, 32 or 64
-    KiB at 1, 2, 4 or 8 workgroups per CU; best HIP-event time of `reps`
+    read-only, write-only and copy, one workgroup per unit of 4 to 64 KiB
+    at 1 to 16 workgroups per CU; best HIP-event time of `reps`
     launches each. write_random writes the same units at randomly permuted
     places (the placement of a load's destination pages). Bytes counted: read or written once (copy: both). The
     harmonic mean of the best read and write rates is what a copy that
@@ -874,12 +874,12 @@ def bench_ceilings(torch, dev, nbytes: int = 16 << 30, reps: int = 5) -> dict:
                      (4, "write_random_16_per_wg")):
         moved = nbytes * (2 if op == 2 else 1)
         sweep = []
-        for unit in (16 << 10, 32 << 10, 64 << 10):
+        for unit in (4 << 10, 8 << 10, 16 << 10, 32 << 10, 64 << 10):
             if op == 3:  # the same units written at randomly permuted places
                 g = torch.Generator().manual_seed(unit)
                 perms[unit] = torch.randperm(nbytes // unit, generator=g,
                                              dtype=torch.int32).to(dev)
-            for wpc in (1, 2, 4, 8):
+            for wpc in (1, 2, 4, 8, 16):
                 def launch():
                     s_ptr = perms[unit].data_ptr() if op >= 3 else a.data_ptr()
                     rc = fn(op, s_ptr, b.data_ptr(), nbytes, unit, wpc, sink.data_ptr(),
