@@ -174,6 +174,61 @@ int main() {
   hipMemcpy(got2.data(), stg2, got2.size(), hipMemcpyDeviceToHost);
   REQUIRE(got2 == want, "slot_mapping gather equals page gather");
 
+  // shared records, each read once (dsr_scatter_fanout): record p goes to
+  // block ids[p] and records 0 and 2 also to blocks 1 and 3
+  {
+    const int64_t src_off[] = {0, slot, 2 * slot, 3 * slot};
+    const int32_t start[] = {0, 2, 3, 5, 6};
+    const int32_t dpages[] = {1, 7, 2, 3, 5, 0};
+    int64_t* d_src;
+    int32_t *d_start, *d_dp;
+    REQUIRE(hipMalloc(&d_src, sizeof(src_off)) == hipSuccess, "hipMalloc");
+    REQUIRE(hipMalloc(&d_start, sizeof(start)) == hipSuccess, "hipMalloc");
+    REQUIRE(hipMalloc(&d_dp, sizeof(dpages)) == hipSuccess, "hipMalloc");
+    hipMemcpy(d_src, src_off, sizeof(src_off), hipMemcpyHostToDevice);
+    hipMemcpy(d_start, start, sizeof(start), hipMemcpyHostToDevice);
+    hipMemcpy(d_dp, dpages, sizeof(dpages), hipMemcpyHostToDevice);
+    hipMemset(cache2, 0, L * cache_bytes);
+    rc = dsr_scatter_fanout(bases + L, L, NB * page, page, page, NB, d_src, 4, d_start, d_dp,
+                            nullptr, 6, stg, n * slot, layer_bytes, 0, nullptr, 0, nullptr, 0,
+                            0, 0, 0, 0, nullptr, DSR_K_NHD, 0, 0, nullptr);
+    REQUIRE(rc == 0, dsr_error_string(rc));
+    hipMemcpy(c3.data(), cache2, c3.size(), hipMemcpyDeviceToHost);
+    std::vector<uint8_t> want3 = c2;  // the page scatter's result, plus blocks 1 and 3
+    for (int l = 0; l < L; ++l)
+      for (int kv = 0; kv < 2; ++kv) {
+        const int64_t base = l * cache_bytes + kv * NB * page;
+        memcpy(want3.data() + base + 1 * page, host.data() + base + ids[0] * page, page);
+        memcpy(want3.data() + base + 3 * page, host.data() + base + ids[2] * page, page);
+      }
+    REQUIRE(c3 == want3, "fan-out load of shared records");
+    // the geometry query: no work, null tables
+    REQUIRE(dsr_scatter_fanout(bases + L, L, NB * page, page, 64 << 10, NB, nullptr, 0, nullptr,
+                               nullptr, nullptr, 0, stg, 0, 128 << 10, 0, nullptr, 0, nullptr, 0,
+                               0, 0, 0, 0, nullptr, DSR_K_NHD, 0, 0,
+                               nullptr) == DSR_ERR_SHAPE,
+            "fan-out refuses 64 KiB pages");
+    hipFree(d_src);
+    hipFree(d_start);
+    hipFree(d_dp);
+  }
+
+  // the allocation-free load: host tables, staged in the library's own
+  // device array; every page unrotated, so the plain scatter's bytes
+  {
+    std::vector<int32_t> h_ridx(n, -1);
+    std::vector<float> h_tab(D, 0.0f);
+    hipMemset(cache2, 0, L * cache_bytes);
+    rc = dsr_scatter_rerotate_static(b.data() + L, L, NB * page, page, page, NB, ids,
+                                     offs.data(), n, stg, n * slot, layer_bytes, 0, h_tab.data(),
+                                     h_ridx.data(), 1, nullptr, 0, D, D, DSR_ROPE_NEOX,
+                                     DSR_DTYPE_BF16, nullptr, 0u, nullptr);
+    REQUIRE(rc == 0, dsr_error_string(rc));
+    REQUIRE(hipDeviceSynchronize() == hipSuccess, "device sync");
+    hipMemcpy(c3.data(), cache2, c3.size(), hipMemcpyDeviceToHost);
+    REQUIRE(c3 == c2, "allocation-free load equals the plain scatter");
+  }
+
   // staging ring: records -> store file at a slot offset -> back to the device
   char path[] = "/tmp/dsr_abi_XXXXXX";
   const int fd = mkstemp(path);
