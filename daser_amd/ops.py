@@ -386,10 +386,12 @@ def scatter(
 ) -> None:
     """Unpacks slot records into pages (reference load loop, :536-551).
 
-    ``shared_records``: several pages read the same records; shapes the
-    launch for cache-served reads. None: inferred from host ``slot_offsets``
-    (at most half of them distinct), False for device tables. Results do
-    not depend on it."""
+    ``shared_records``: several pages read the same records. Host tables
+    then take the fan-out load (:class:`PreparedFanout`: each record read
+    once and written to all of its pages) where the pages allow it, device
+    tables a launch shaped for cache-served reads. None: inferred from host
+    ``slot_offsets`` (at most half of them distinct), False for device
+    tables. Results do not depend on it."""
     if shared_records is None:
         shared_records = _shared_offsets(slot_offsets)
     page_ids, slot_offsets, _ = dest_order(page_ids, slot_offsets)
@@ -614,9 +616,11 @@ def scatter_rerotate(
     (-1: no RoPE, K copied).
 
     ``shared_records``: several pages read the same records (a cached chunk
-    placed in several requests); shapes the launch for cache-served reads.
-    None: inferred from host ``slot_offsets`` (at most half of them
-    distinct), False for device tables. Results do not depend on it.
+    placed in several requests). Host tables then take the fan-out load
+    (:class:`PreparedFanout`) where the pages allow it, device tables a
+    launch shaped for cache-served reads. None: inferred from host
+    ``slot_offsets`` (at most half of them distinct), False for device
+    tables. Results do not depend on it.
     """
     lay = table.layout
     rot_dim, n_tables, n_groups, lg_d, ks_ptr = _rope_args(
