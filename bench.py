@@ -32,7 +32,7 @@ sustain there.
 
 Usage: python bench.py [--steps K] [--warmup W] [--configs 2,3,4,5,6] [--no-cpu]
                        [--no-ref-loop] [--io] [--serving] [--patterns] [--shapes]
-                       [--calibrate] [--ceilings | --no-ceilings] [--tune k=v,...]
+                       [--calibrate] [--ceilings | --no-ceilings] [--reuse] [--tune k=v,...]
 """
 
 from __future__ import annotations
@@ -907,6 +907,52 @@ def bench_ceilings(torch, dev, nbytes: int = 16 << 30, reps: int = 5) -> dict:
     return out
 
 
+def bench_reuse(torch, ops, position, dev, steps: int = 6) -> list:
+    """RAG loads at the Llama-3-8B shape with more or fewer requests sharing
+    the cached chunks (10 chunks of 512 tokens per request, n_src distinct
+    ones): the fan-out load (ops' path for host tables with shared records)
+    against the per-page re-rotation of the same pages, medians of HIP-event
+    times."""
+    from daser_amd import workloads
+
+    shape = workloads.LLAMA3_8B
+
+    def timed(fn):
+        fn()
+        t = Timer(torch)
+        for _ in range(steps):
+            with t:
+                fn()
+        torch.cuda.synchronize()
+        return float(np.median([s_.elapsed_time(e_) for s_, e_ in t.pairs]))
+
+    out = []
+    for n_req, n_src in ((2, 16), (3, 16), (4, 20), (8, 16), (16, 16), (32, 160), (32, 64),
+                         (32, 40), (32, 20)):
+        wl = workloads.rag_reuse(shape, n_req, 10, 512, n_src, 32768, seed=1, pool_slack=1.05)
+        full, caches, _ = fill_caches(torch, shape, wl.num_blocks, "bf16", dev, seed=2)
+        table = ops.LayerTable(caches)
+        src = torch.empty(wl.meta["src_staging_bytes"], dtype=torch.uint8, device=dev)
+        src.view(torch.bfloat16).normal_()
+        ridx, uniq = position.page_rope_index(wl.chunk_pages, wl.chunk_delta)
+        tabs = position.delta_tables(uniq, shape.head_dim, THETA, device=dev)
+        ids, offs, rd = ops.dest_order(wl.page_ids, wl.src_offsets, ridx)
+        prep = ops.PreparedFanout(table, ids, offs, src, rope=(rd, tabs, None, "neox", None, None))
+        ids_d = torch.from_numpy(ids.astype(np.int32)).to(dev)
+        offs_d = torch.from_numpy(offs).to(dev)
+        rd_d = torch.from_numpy(rd.astype(np.int32)).to(dev)
+        per_page = timed(lambda: ops.scatter_rerotate(table, ids_d, offs_d, src, tabs, rd_d,
+                                                      shared_records=False))
+        fan = timed(prep)
+        out.append({"requests": n_req, "cached_chunks": n_src, "pages": wl.n_pages,
+                    "placements_per_record": round(wl.n_pages / prep.n_src, 2),
+                    "fanout_ms": round(fan, 4), "per_page_ms": round(per_page, 4),
+                    "speedup": round(per_page / fan, 3)})
+        del full, caches, table, src, prep
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_model() -> str:
     """The host CPU as /proc/cpuinfo names it: model name verbatim, with its
     family / model / stepping numbers and the logical CPUs listed there."""
@@ -1105,6 +1151,9 @@ def main() -> int:
                     help="also time plain read-only, write-only and copy streams of 16 GiB "
                          "(libdaser_bwprobe.so) over unit sizes and workgroups per CU: what "
                          "the memory system sustains per direction of traffic")
+    ap.add_argument("--reuse", action="store_true",
+                    help="also time RAG loads with more or fewer requests sharing the cached "
+                         "chunks: the fan-out load against the per-page re-rotation")
     ap.add_argument("--no-ceilings", action="store_true",
                     help="skip the short read/write/copy stream measurement that the default "
                          "run adds beside the roofline (hbm_ceilings)")
@@ -1283,6 +1332,10 @@ def main() -> int:
                     "of the read and write rates"}
         if "roofline" in out:
             out["roofline"]["frac_of_copy_bound"] = round(out["roofline"]["achieved"] / bound, 4)
+    if args.reuse:
+        log("[bench] reuse: fan-out against per-page loads by chunk sharing")
+        out["reuse"] = bench_reuse(torch, ops, position, dev)
+        log(f"[bench] reuse: {json.dumps(out['reuse'])}")
     if args.patterns:
         log("[bench] patterns: config 2's bytes in other access patterns")
         out["patterns"] = bench_patterns(torch, ops, dev)
