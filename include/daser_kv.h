@@ -298,7 +298,8 @@ int dsr_scatter_rerotate(const uint64_t* layer_base, int n_layers,
  *
  *   src_offsets   [device] n_src int64 record offsets
  *   dst_start     [device] n_src + 1 int32, non-decreasing, dst_start[0] = 0,
- *                 dst_start[n_src] = n_dst
+ *                 dst_start[n_src] = n_dst (trusted, as the tables' lengths
+ *                 are: daser_amd.ops.fanout_tables builds it)
  *   dst_page_ids  [device] n_dst int32 block ids
  *   dst_rope_idx  [device] n_dst int32 table indices, or null (plain copy:
  *                 cos_sin, n_tables, layer_group, head_dim, rot_dim,
